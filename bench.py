@@ -1,0 +1,236 @@
+#!/usr/bin/env python3
+"""FP4 MoE grouped-matmul throughput on one MI355X.
+
+A step is one FP4 grouped matmul (gmm_v2 with prepacked e2m1 + e8m0 weights)
+over one batch of routed rows of the decode gate+up workload: 32 local
+experts, 256 tokens x top-8 (M = 2048 routed rows, 4 guaranteed-empty
+experts), K = 7168, N = 2 x 2048, bf16 activations, bf16 output.  Inputs are
+resident in HBM before the timed region; the weight set is rotated over
+copies larger than the 256 MB Infinity Cache so the stream comes from HBM.
+
+`value` is algorithmic HBM GB/s (non-empty experts' packed weights + scales,
+lhs once, output once) divided by the average step time measured with HIP
+events on the stream the kernels run on.  `extra` reports the other workloads
+(decode down-projection with dispatch / combine, prefill) the same way, and
+`cpu_baseline` times the numpy oracle of the same math on a bounded sample of
+experts on this host.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--extra all|none]
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "dw-tpu_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "FP4 MoE gmm TFLOP/s + HBM GB/s (% of peak) at decode & prefill sizes"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+MALL_BYTES = 256 * 2 ** 20
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def _to_dev_bf16(bits, dev):
+    import numpy as np
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(torch.bfloat16).to(dev)
+
+
+class GmmBench:
+    """Device-resident inputs of one gmm workload plus a raw C-ABI launcher."""
+
+    def __init__(self, wl, dev, copies):
+        import torch
+        from dw_tpu_amd import _lib, fp4_weight_to_codes
+        self.wl = wl
+        self.lib = _lib.load()
+        rhs = torch.from_numpy(wl.rhs_e2m1).to(dev)
+        sc = torch.from_numpy(wl.scale_codes).to(dev)
+        self.weights = [fp4_weight_to_codes(rhs, sc) for _ in range(copies)]
+        del rhs, sc
+        self.lhs = [_to_dev_bf16(wl.lhs_bits, dev) for _ in range(copies)]
+        self.gs = torch.from_numpy(wl.group_sizes).to(dev)
+        self.out = [torch.empty((wl.M, wl.N), dtype=torch.bfloat16, device=dev) for _ in range(copies)]
+        self.stream = _lib.stream_handle(dev)
+        self.args = []
+        for i in range(copies):
+            w = self.weights[i]
+            self.args.append((ctypes.c_void_p(self.lhs[i].data_ptr()), wl.M, wl.K, ctypes.c_void_p(w.weight.data_ptr()),
+                              ctypes.c_void_p(w.scale.data_ptr()), ctypes.c_void_p(self.gs.data_ptr()), wl.E, None,
+                              wl.E, wl.N, ctypes.c_void_p(self.out[i].data_ptr()), _lib.BF16, 0, self.stream))
+        self.fn = self.lib.dwm_gmm_fp4
+
+    def step(self, i):
+        rc = self.fn(*self.args[i % len(self.args)])
+        if rc:
+            raise RuntimeError(self.lib.dwm_last_error().decode())
+
+
+def time_steps(step, steps, warmup):
+    """Average ms per step over `steps` back-to-back launches (HIP events on
+    torch's current stream, which is the stream the kernels are launched on)."""
+    import torch
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        step(warmup + i)
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def gmm_result(wl, ms):
+    bts = wl.algorithmic_bytes()
+    fl = wl.flops()
+    gbs = bts / (ms * 1e-3) / 1e9
+    tfl = fl / (ms * 1e-3) / 1e12
+    return {"ms": round(ms, 5), "GB_s": round(gbs, 1), "TFLOP_s": round(tfl, 1),
+            "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "mfma_bf16_frac": round(tfl / BF16_PEAK_TFLOPS, 4),
+            "bytes": bts, "flops": fl, "M": wl.M, "K": wl.K, "N": wl.N, "E": wl.E,
+            "nonempty_groups": int((wl.group_sizes > 0).sum())}
+
+
+def copies_for(wl):
+    return max(1, min(4, -(-2 * MALL_BYTES // max(1, wl.weight_bytes()))))
+
+
+def bench_gmm(name, dev, steps, warmup):
+    from dw_tpu_amd.workloads import make_gmm_workload
+    wl = make_gmm_workload(name)
+    b = GmmBench(wl, dev, copies_for(wl))
+    ms = time_steps(b.step, steps, warmup)
+    return wl, b, ms
+
+
+def bench_dispatch_combine(dev, steps, warmup):
+    """decode_down routing: dispatch indices, row gather of hidden [512, 2048]
+    and the combine of the down-projection output [4096, 7168] -> [512, 7168]."""
+    import numpy as np
+    import torch
+    from dw_tpu_amd import fast_combine, moe_dispatch, row_gather
+    from dw_tpu_amd.workloads import make_gmm_workload
+    wl = make_gmm_workload("decode_down")
+    ids = torch.from_numpy(wl.topk_ids).to(dev)
+    rng = np.random.Generator(np.random.PCG64(11))
+    hidden = torch.from_numpy(rng.standard_normal((wl.T, wl.K), dtype=np.float32)).to(torch.bfloat16).to(dev)
+    y = torch.from_numpy(rng.standard_normal((wl.M, wl.N), dtype=np.float32)).to(torch.bfloat16).to(dev)
+    w = torch.from_numpy(wl.topk_weights).to(dev)
+    d = moe_dispatch(ids, wl.E)
+    res = {}
+    ms = time_steps(lambda i: moe_dispatch(ids, wl.E), steps, warmup)
+    res["dispatch"] = {"ms": round(ms, 5), "ids": wl.M, "experts": wl.E}
+    ms = time_steps(lambda i: row_gather(hidden, d.token_indices_sorted), steps, warmup)
+    gb = 2 * wl.M * wl.K * 2
+    res["row_gather"] = {"ms": round(ms, 5), "GB_s": round(gb / (ms * 1e-3) / 1e9, 1), "rows": wl.M, "H": wl.K}
+    ms = time_steps(lambda i: fast_combine(y, d.topk_argsort_revert_indices, w, wl.topk), steps, warmup)
+    gb = wl.M * wl.N * 2 + wl.T * wl.N * 2 + wl.M * 8
+    res["combine"] = {"ms": round(ms, 5), "GB_s": round(gb / (ms * 1e-3) / 1e9, 1), "T": wl.T, "topk": wl.topk,
+                      "H": wl.N}
+    return res
+
+
+def cpu_baseline(wl, budget_s):
+    """numpy oracle of the same math (exact dequant to f32, per-expert f32
+    matmul, bf16 round) over as many non-empty experts as fit the budget."""
+    import numpy as np
+    from oracle import fp4, gmm
+    from oracle.numerics import bf16_to_f32, round_bf16
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
+    except Exception:
+        threads = 1
+    starts = np.concatenate([[0], np.cumsum(wl.group_sizes)])
+    lhs = bf16_to_f32(wl.lhs_bits)
+    done, bts, t0 = 0, 0, time.perf_counter()
+    for e in range(wl.E):
+        sz = int(wl.group_sizes[e])
+        if sz == 0:
+            continue
+        codes = fp4.e2m1_to_codes(fp4.unpack_nibbles(wl.rhs_e2m1[e]))
+        w = fp4.dequant_fp4_block(codes, fp4.e8m0_decode(wl.scale_codes[e]))
+        round_bf16(lhs[starts[e]:starts[e + 1]] @ w)
+        done += 1
+        bts += wl.K * wl.N // 2 + (wl.K // 32) * wl.N + sz * wl.K * 2 + sz * wl.N * 2
+        if time.perf_counter() - t0 > budget_s:
+            break
+    dt = time.perf_counter() - t0
+    return {"value": round(bts / dt / 1e9, 4), "unit": "GB/s", "cores": int(threads), "kind": "port",
+            "sample": f"{done} of {int((wl.group_sizes > 0).sum())} non-empty experts of {wl.name} "
+                      f"(numpy oracle: dequant single-threaded, f32 matmul on {threads} BLAS threads), {dt:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--extra", choices=["all", "none"], default="all")
+    ap.add_argument("--cpu-budget", type=float, default=15.0)
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU only: the MoE hot path is built and measured on one MI355X's share of "
+              "the experts; runs on more than one GPU are not part of this build.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    dev = torch.device("cuda:0")
+    log("bench: decode_gate_up gmm")
+    wl, b, ms = bench_gmm("decode_gate_up", dev, args.steps, args.warmup)
+    main_res = gmm_result(wl, ms)
+    extra = {}
+    if args.extra == "all":
+        for name in ("decode_down", "prefill"):
+            log(f"bench: {name} gmm")
+            del b
+            torch.cuda.empty_cache()
+            wl2, b, ms2 = bench_gmm(name, dev, args.steps, args.warmup)
+            extra[name] = gmm_result(wl2, ms2)
+        del b
+        torch.cuda.empty_cache()
+        log("bench: dispatch / gather / combine")
+        extra.update(bench_dispatch_combine(dev, args.steps, args.warmup))
+    log("bench: cpu baseline")
+    cpu = cpu_baseline(wl, args.cpu_budget)
+    line = {
+        "metric": METRIC,
+        "value": main_res["GB_s"],
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": main_res["ms"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded numpy PCG64: N(0,1) bf16 activations, uniform e2m1 nibbles, e8m0 exponents "
+                "in [-4,2], softmax top-k routing)",
+        "config": {"workload": "decode_gate_up: 32 local experts, 256 tokens x top-8 (M=2048 routed rows, 4 empty "
+                               "experts), K=7168, N=4096, fp4 e2m1 weights with e8m0 block-32 scales, bf16 out",
+                   "TFLOP_s": main_res["TFLOP_s"], "mfma_bf16_frac": main_res["mfma_bf16_frac"],
+                   "bytes_per_step": main_res["bytes"], "flops_per_step": main_res["flops"]},
+        "roofline": {"bound": "hbm", "achieved": main_res["GB_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": main_res["hbm_frac"], "traffic": None},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,92 @@
+// Shared helpers of the gfx950 kernels and the C ABI: error reporting,
+// argument checks, bf16 rounding, fp4 decode and wavefront scans.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "../../include/dwtpu_moe.h"
+
+namespace dwm {
+
+// ---- host-side error reporting -------------------------------------------
+
+void set_error(const char *fmt, ...);
+void clear_error();
+
+#define DWM_CHECK_ARG(cond, ...)        \
+  do {                                  \
+    if (!(cond)) {                      \
+      ::dwm::set_error(__VA_ARGS__);    \
+      return DWM_ERR_INVALID;           \
+    }                                   \
+  } while (0)
+
+#define DWM_UNSUPPORTED_IF(cond, ...)   \
+  do {                                  \
+    if (cond) {                         \
+      ::dwm::set_error(__VA_ARGS__);    \
+      return DWM_ERR_UNSUPPORTED;       \
+    }                                   \
+  } while (0)
+
+// Reports the launch status of the kernels just enqueued.
+int launch_status(const char *what);
+
+inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
+
+// ---- device helpers --------------------------------------------------------
+
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+typedef __attribute__((ext_vector_type(16))) float f32x16_t;
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;
+
+// float -> bf16 bits, round to nearest even; NaN stays a quiet NaN.
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __builtin_bit_cast(uint32_t, f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) {
+  return __builtin_bit_cast(float, b << 16);
+}
+
+// Two e2m1 nibbles of byte `SEL` of `src` -> packed bf16x2 (low nibble in the
+// low half), each multiplied by 2^(e-127) where e is the exponent field of
+// `scale`.  The result is bit-cast to u32 at once: extracting bf16 vector
+// elements of the builtin's result directly miscompiles (both halves come
+// out equal to the low one).
+template <int SEL>
+__device__ __forceinline__ uint32_t cvt_fp4x2_bf16(uint32_t src, float scale) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(src, scale, SEL));
+}
+
+// e8m0 code -> the f32 with that exponent field (2^(c-127) for 1 <= c <= 254).
+__device__ __forceinline__ float e8m0_to_f32(uint32_t code) {
+  return __builtin_bit_cast(float, (code & 0xFFu) << 23);
+}
+
+// Inclusive prefix sum across a 64-lane wavefront.
+__device__ __forceinline__ int wave_inclusive_scan(int v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    int t = __shfl_up(v, d, 64);
+    if (lane >= d) v += t;
+  }
+  return v;
+}
+
+__device__ __forceinline__ int wave_sum(int v) {
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
+  return v;
+}
+
+}  // namespace dwm

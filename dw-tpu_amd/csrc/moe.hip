@@ -1,0 +1,307 @@
+// MoE dispatch (expert-stable counting sort), row gather and combine.
+//
+// Dispatch replaces jnp.argsort(topk_ids.flatten()) + argsort // topk +
+// one_hot(...).sum(0) (patches/tpu-inference-ext/0405-moe-fast-dispatch.patch:70-98,
+// kernels/tpu_inference/layers/common/moe_fast_dispatch.py:41-44) with a
+// three-launch counting sort that is bit-exact to a stable argsort:
+//   1. per 1024-id chunk, an LDS histogram -> counts[chunk][expert]
+//   2. one block: group sizes, exclusive offsets, per-(chunk, expert) bases
+//   3. per chunk, in id order (256 ids per step, wave by wave): each lane's
+//      rank among equal ids of its wave comes from ballots over the id bits;
+//      earlier waves' counts come from LDS.  Position = base + rank.
+// Ids outside [0, E) get the key E, i.e. they sort after every valid id.
+//
+// This file is compiled with -ffp-contract=off: the combine's f32 products
+// and sums must stay separately rounded (moe_fast_combine.py:44-54).
+#include "common.h"
+
+namespace dwm {
+
+constexpr int kChunk = 1024;
+constexpr int kDispThreads = 256;
+constexpr int kMaxExperts = 1024;
+
+__device__ __forceinline__ int dispatch_key(int32_t id, int E, bool *bad) {
+  if (id < 0 || id >= E) {
+    *bad = true;
+    return E;
+  }
+  return id;
+}
+
+__global__ __launch_bounds__(kDispThreads) void dispatch_count_kernel(const int32_t *ids, int64_t n,
+                                                                      int E, int32_t *counts,
+                                                                      int32_t *flags) {
+  __shared__ int s_hist[kMaxExperts + 1];
+  for (int e = threadIdx.x; e <= E; e += kDispThreads) s_hist[e] = 0;
+  __syncthreads();
+  bool bad = false;
+  const int64_t base = (int64_t)blockIdx.x * kChunk;
+  for (int i = 0; i < kChunk / kDispThreads; ++i) {
+    const int64_t j = base + i * kDispThreads + threadIdx.x;
+    if (j < n) atomicAdd(&s_hist[dispatch_key(ids[j], E, &bad)], 1);
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e <= E; e += kDispThreads)
+    counts[(int64_t)blockIdx.x * (E + 1) + e] = s_hist[e];
+  if (bad && flags) atomicOr(flags, 1);
+}
+
+// One block.  counts[c][e] -> base position of chunk c's first id of key e.
+__global__ __launch_bounds__(1024) void dispatch_scan_kernel(int32_t *counts, int nchunks, int E,
+                                                             int32_t *group_sizes,
+                                                             int32_t *group_offsets) {
+  __shared__ int s_tot[kMaxExperts + 1];
+  __shared__ int s_off[kMaxExperts + 1];
+  for (int e = threadIdx.x; e <= E; e += blockDim.x) {
+    int t = 0;
+    for (int c = 0; c < nchunks; ++c) t += counts[(int64_t)c * (E + 1) + e];
+    s_tot[e] = t;
+  }
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    int carry = 0;
+    for (int b = 0; b <= E; b += 64) {
+      const int e = b + lane;
+      const int v = e <= E ? s_tot[e] : 0;
+      const int inc = wave_inclusive_scan(v);
+      if (e <= E) s_off[e] = carry + inc - v;
+      carry += __shfl(inc, 63, 64);
+    }
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e <= E; e += blockDim.x) {
+    if (e < E) group_sizes[e] = s_tot[e];
+    if (group_offsets) group_offsets[e] = s_off[e];  // entry E = number of valid ids
+    int run = s_off[e];
+    for (int c = 0; c < nchunks; ++c) {
+      const int64_t idx = (int64_t)c * (E + 1) + e;
+      const int v = counts[idx];
+      counts[idx] = run;
+      run += v;
+    }
+  }
+}
+
+__global__ __launch_bounds__(kDispThreads) void dispatch_scatter_kernel(
+    const int32_t *ids, int64_t n, int topk, int E, const int32_t *bases, int32_t *perm,
+    int32_t *tok_sorted, int32_t *revert) {
+  __shared__ int s_run[kMaxExperts + 1];
+  __shared__ int s_wcnt[kDispThreads / 64][kMaxExperts + 1];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int e = tid; e <= E; e += kDispThreads) {
+    s_run[e] = bases[(int64_t)blockIdx.x * (E + 1) + e];
+#pragma unroll
+    for (int w = 0; w < kDispThreads / 64; ++w) s_wcnt[w][e] = 0;
+  }
+  int nbits = 0;
+  while ((1 << nbits) <= E) ++nbits;  // keys 0..E
+  __syncthreads();
+  const int64_t base = (int64_t)blockIdx.x * kChunk;
+  for (int i = 0; i < kChunk / kDispThreads; ++i) {
+    const int64_t j = base + i * kDispThreads + tid;
+    const bool active = j < n;
+    bool bad = false;
+    const int key = active ? dispatch_key(ids[j], E, &bad) : 0;
+    uint64_t peers = __ballot(active);
+    for (int b = 0; b < nbits; ++b) {
+      const bool bit = (key >> b) & 1;
+      const uint64_t m = __ballot(bit);
+      peers &= bit ? m : ~m;
+    }
+    const int rank = __popcll(peers & ((1ull << lane) - 1ull));
+    const int cnt = __popcll(peers);
+    const bool leader = active && rank == 0;
+    if (leader) s_wcnt[wave][key] = cnt;
+    __syncthreads();
+    if (active) {
+      int pos = s_run[key] + rank;
+      for (int w = 0; w < wave; ++w) pos += s_wcnt[w][key];
+      perm[pos] = (int32_t)j;
+      tok_sorted[pos] = (int32_t)(j / topk);
+      revert[j] = pos;
+    }
+    __syncthreads();
+    if (leader) {
+      atomicAdd(&s_run[key], cnt);
+      s_wcnt[wave][key] = 0;
+    }
+    __syncthreads();
+  }
+}
+
+// JAX gather index semantics: wrap a negative index once, then clamp.
+__device__ __forceinline__ int64_t gather_index(int64_t i, int64_t n) {
+  if (i < 0) i += n;
+  if (i < 0) i = 0;
+  if (i >= n) i = n - 1;
+  return i;
+}
+
+template <typename V>
+__global__ __launch_bounds__(256) void row_gather_kernel(const char *src, int64_t src_rows,
+                                                         int64_t row_bytes, const int32_t *idx,
+                                                         int64_t rows, char *out) {
+  const int64_t nv = row_bytes / (int64_t)sizeof(V);
+  for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+    const int64_t s = gather_index(idx[r], src_rows);
+    const V *sp = (const V *)(src + s * row_bytes);
+    V *dp = (V *)(out + r * row_bytes);
+    for (int64_t i = threadIdx.x; i < nv; i += blockDim.x) dp[i] = sp[i];
+  }
+}
+
+__device__ __forceinline__ float load_f32(const void *p, int dtype, int64_t i) {
+  return dtype == DWM_F32 ? ((const float *)p)[i]
+                          : bf16_bits_to_f32(((const uint16_t *)p)[i]);
+}
+
+// One block per token; each thread owns 8 consecutive columns per step.
+template <int XF32, int OF32>
+__global__ __launch_bounds__(256) void combine_kernel(const void *x, int64_t x_rows, int64_t H,
+                                                      const int32_t *idx, const void *w, int w_dtype,
+                                                      int64_t T, int topk, void *out, int vec) {
+  for (int64_t t = blockIdx.x; t < T; t += gridDim.x) {
+    for (int64_t c = (int64_t)threadIdx.x * 8; c < H; c += (int64_t)blockDim.x * 8) {
+      float acc[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+      const bool full = vec && c + 8 <= H;
+      for (int k = 0; k < topk; ++k) {
+        const int64_t r = gather_index(idx[t * topk + k], x_rows);
+        const float wk = load_f32(w, w_dtype, t * topk + k);
+        float v[8];
+        if (full && !XF32) {
+          const u32x4_t q = *(const u32x4_t *)((const uint16_t *)x + r * H + c);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            v[2 * i] = __builtin_bit_cast(float, q[i] << 16);
+            v[2 * i + 1] = __builtin_bit_cast(float, q[i] & 0xFFFF0000u);
+          }
+        } else if (full) {
+          const f32x4_t q0 = *(const f32x4_t *)((const float *)x + r * H + c);
+          const f32x4_t q1 = *(const f32x4_t *)((const float *)x + r * H + c + 4);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            v[i] = q0[i];
+            v[4 + i] = q1[i];
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+            v[i] = c + i < H ? load_f32(x, XF32 ? DWM_F32 : DWM_BF16, r * H + c + i) : 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float p = v[i] * wk;  // separately rounded product
+          acc[i] = acc[i] + p;        // then sum, k ascending from +0.0
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if (c + i >= H) break;
+        if (OF32) ((float *)out)[t * H + c + i] = acc[i];
+        else ((uint16_t *)out)[t * H + c + i] = f32_to_bf16_bits(acc[i]);
+      }
+    }
+  }
+}
+
+}  // namespace dwm
+
+using namespace dwm;
+
+extern "C" int dwm_moe_dispatch_workspace_size(int64_t n, int num_experts, int64_t *bytes) {
+  clear_error();
+  DWM_CHECK_ARG(n >= 0 && num_experts > 0 && bytes, "moe_dispatch_workspace_size: bad arguments");
+  DWM_UNSUPPORTED_IF(num_experts > kMaxExperts, "moe_dispatch: at most %d experts", kMaxExperts);
+  const int64_t nchunks = (n + kChunk - 1) / kChunk;
+  *bytes = nchunks * (num_experts + 1) * 4;
+  if (*bytes == 0) *bytes = 4;
+  return DWM_OK;
+}
+
+extern "C" int dwm_moe_dispatch(const int32_t *topk_ids, int64_t T, int topk, int num_experts,
+                                int32_t *perm, int32_t *tok_sorted, int32_t *revert,
+                                int32_t *group_sizes, int32_t *group_offsets, int32_t *flags,
+                                void *workspace, void *stream) {
+  clear_error();
+  DWM_CHECK_ARG(T >= 0 && topk > 0 && num_experts > 0, "moe_dispatch: bad sizes T=%lld topk=%d E=%d",
+                (long long)T, topk, num_experts);
+  DWM_UNSUPPORTED_IF(num_experts > kMaxExperts, "moe_dispatch: at most %d experts (got %d)", kMaxExperts,
+                     num_experts);
+  const int64_t n = T * topk;
+  DWM_CHECK_ARG(n < (1ll << 31), "moe_dispatch: T*topk must be < 2^31");
+  DWM_CHECK_ARG(group_sizes && workspace, "moe_dispatch: null pointer");
+  hipStream_t st = as_stream(stream);
+  const int64_t nchunks = (n + kChunk - 1) / kChunk;
+  int32_t *counts = (int32_t *)workspace;
+  if (n == 0) {
+    hipLaunchKernelGGL(dispatch_scan_kernel, dim3(1), dim3(1024), 0, st, counts, 0, num_experts,
+                       group_sizes, group_offsets);
+    return launch_status("moe_dispatch");
+  }
+  DWM_CHECK_ARG(topk_ids && perm && tok_sorted && revert, "moe_dispatch: null pointer");
+  hipLaunchKernelGGL(dispatch_count_kernel, dim3((unsigned)nchunks), dim3(kDispThreads), 0, st,
+                     topk_ids, n, num_experts, counts, flags);
+  hipLaunchKernelGGL(dispatch_scan_kernel, dim3(1), dim3(1024), 0, st, counts, (int)nchunks,
+                     num_experts, group_sizes, group_offsets);
+  hipLaunchKernelGGL(dispatch_scatter_kernel, dim3((unsigned)nchunks), dim3(kDispThreads), 0, st,
+                     topk_ids, n, topk, num_experts, counts, perm, tok_sorted, revert);
+  return launch_status("moe_dispatch");
+}
+
+extern "C" int dwm_row_gather(const void *src, int64_t src_rows, int64_t row_bytes,
+                              const int32_t *idx, int64_t rows, void *out, void *stream) {
+  clear_error();
+  DWM_CHECK_ARG(src_rows >= 0 && row_bytes >= 0 && rows >= 0, "row_gather: bad sizes");
+  if (rows == 0 || row_bytes == 0) return DWM_OK;
+  DWM_CHECK_ARG(src_rows > 0, "row_gather: empty source with rows to gather");
+  DWM_CHECK_ARG(src && idx && out, "row_gather: null pointer");
+  const unsigned grid = (unsigned)(rows < 65536 ? rows : 65536);
+  hipStream_t st = as_stream(stream);
+  const uintptr_t al = (uintptr_t)src | (uintptr_t)out | (uintptr_t)row_bytes;
+  if (al % 16 == 0)
+    hipLaunchKernelGGL(row_gather_kernel<u32x4_t>, dim3(grid), dim3(256), 0, st, (const char *)src,
+                       src_rows, row_bytes, idx, rows, (char *)out);
+  else if (al % 4 == 0)
+    hipLaunchKernelGGL(row_gather_kernel<uint32_t>, dim3(grid), dim3(256), 0, st, (const char *)src,
+                       src_rows, row_bytes, idx, rows, (char *)out);
+  else
+    hipLaunchKernelGGL(row_gather_kernel<uint8_t>, dim3(grid), dim3(256), 0, st, (const char *)src,
+                       src_rows, row_bytes, idx, rows, (char *)out);
+  return launch_status("row_gather");
+}
+
+extern "C" int dwm_moe_combine(const void *x, int x_dtype, int64_t x_rows, int64_t H,
+                               const int32_t *idx, const void *w, int w_dtype, int64_t T, int topk,
+                               void *out, int out_dtype, void *stream) {
+  clear_error();
+  DWM_CHECK_ARG(x_rows >= 0 && H >= 0 && T >= 0 && topk > 0, "moe_combine: bad sizes");
+  DWM_CHECK_ARG((x_dtype == DWM_BF16 || x_dtype == DWM_F32) && (w_dtype == DWM_BF16 || w_dtype == DWM_F32) &&
+                    (out_dtype == DWM_BF16 || out_dtype == DWM_F32),
+                "moe_combine: bad dtype");
+  if (T == 0 || H == 0) return DWM_OK;
+  DWM_CHECK_ARG(x_rows > 0, "moe_combine: empty x with tokens to combine");
+  DWM_CHECK_ARG(x && idx && w && out, "moe_combine: null pointer");
+  const int xf32 = x_dtype == DWM_F32;
+  // 16-byte row loads need 8-column multiples and an aligned base.
+  const int vec = (H % 8 == 0) && ((uintptr_t)x % 16 == 0);
+  const unsigned grid = (unsigned)(T < 65536 ? T : 65536);
+  hipStream_t st = as_stream(stream);
+  const int of32 = out_dtype == DWM_F32;
+  if (!xf32 && !of32)
+    hipLaunchKernelGGL((combine_kernel<0, 0>), dim3(grid), dim3(256), 0, st, x, x_rows, H, idx, w,
+                       w_dtype, T, topk, out, vec);
+  else if (!xf32 && of32)
+    hipLaunchKernelGGL((combine_kernel<0, 1>), dim3(grid), dim3(256), 0, st, x, x_rows, H, idx, w,
+                       w_dtype, T, topk, out, vec);
+  else if (xf32 && !of32)
+    hipLaunchKernelGGL((combine_kernel<1, 0>), dim3(grid), dim3(256), 0, st, x, x_rows, H, idx, w,
+                       w_dtype, T, topk, out, vec);
+  else
+    hipLaunchKernelGGL((combine_kernel<1, 1>), dim3(grid), dim3(256), 0, st, x, x_rows, H, idx, w,
+                       w_dtype, T, topk, out, vec);
+  return launch_status("moe_combine");
+}

@@ -1,0 +1,120 @@
+"""ctypes binding of libdwtpu_moe.so (the C ABI declared in include/dwtpu_moe.h).
+
+The library is built in-tree (``__graft_entry__.build()`` or
+``make -C dw-tpu_amd/csrc``).  There is no other implementation: when the
+library is missing, every entry point raises ``LibraryMissing``.
+"""
+import ctypes
+import os
+import threading
+
+import torch
+
+LIB_NAME = "libdwtpu_moe.so"
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+
+# enum dwm_status / dwm_dtype / dwm_fp4_format
+OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_HIP = 0, 1, 2, 3
+BF16, F32, U8 = 0, 1, 2
+FP4_E2M1, FP4_CODES = 0, 1
+
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int
+_p = ctypes.c_void_p
+
+# name -> argument types (restype is int unless listed in _RESTYPES)
+SIGNATURES = {
+    "dwm_version": [],
+    "dwm_last_error": [],
+    "dwm_e2m1_to_codes": [_p, _p, _i64, _p],
+    "dwm_fp4_decode": [_p, _i32, _i64, _p, _p, _p, _p],
+    "dwm_gmm_fp4_prepack_size": [_i64, _i64, _i64, _p, _p],
+    "dwm_gmm_fp4_prepack": [_p, _i32, _p, _i32, _i64, _i64, _i64, _p, _p, _p, _p],
+    "dwm_gmm_fp4": [_p, _i64, _i64, _p, _p, _p, _i32, _p, _i64, _i64, _p, _i32, _i32, _p],
+    "dwm_moe_dispatch_workspace_size": [_i64, _i32, _p],
+    "dwm_moe_dispatch": [_p, _i64, _i32, _i32, _p, _p, _p, _p, _p, _p, _p, _p],
+    "dwm_row_gather": [_p, _i64, _i64, _p, _i64, _p, _p],
+    "dwm_moe_combine": [_p, _i32, _i64, _i64, _p, _p, _i32, _i64, _i32, _p, _i32, _p],
+}
+_RESTYPES = {"dwm_last_error": ctypes.c_char_p}
+
+
+class LibraryMissing(RuntimeError):
+    """libdwtpu_moe.so is not built; there is no fallback implementation."""
+
+
+class Unsupported(NotImplementedError):
+    """DWM_ERR_UNSUPPORTED: a valid request the kernels do not handle."""
+
+
+_lock = threading.Lock()
+_lib = None
+
+
+def load():
+    """Loads the library once (thread-safe) and declares every signature."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise LibraryMissing(
+                    f"{LIB_PATH} is not built; run __graft_entry__.build() or "
+                    "make -C dw-tpu_amd/csrc")
+            lib = ctypes.CDLL(LIB_PATH)
+            for name, args in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.argtypes = args
+                fn.restype = _RESTYPES.get(name, ctypes.c_int)
+            _lib = lib
+    return _lib
+
+
+def call(name, *args):
+    """Calls an entry point and maps its status to an exception."""
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if rc == OK:
+        return
+    msg = lib.dwm_last_error().decode(errors="replace")
+    if rc == ERR_INVALID:
+        raise ValueError(msg)
+    if rc == ERR_UNSUPPORTED:
+        raise Unsupported(msg)
+    raise RuntimeError(msg)
+
+
+def ptr(t):
+    """Device (or host) address of a tensor, or None for None."""
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def stream_handle(device=None):
+    """The current torch stream of ``device`` as a hipStream_t."""
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def dtype_code(dt):
+    if dt == torch.bfloat16:
+        return BF16
+    if dt == torch.float32:
+        return F32
+    if dt == torch.uint8:
+        return U8
+    raise ValueError(f"unsupported dtype {dt}")
+
+
+def require_cuda(*tensors):
+    """The kernels run on one HIP device: every tensor must live there."""
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise ValueError(f"expected a device tensor, got one on {t.device}")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"tensors on different devices: {dev} and {t.device}")
+    return dev

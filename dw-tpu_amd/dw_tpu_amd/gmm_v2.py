@@ -1,0 +1,220 @@
+"""FP4 grouped matmul with the tokamax ``gmm_v2`` call signature.
+
+Mirrors patches/tokamax/0001-gmm_v2-fp4-emulation-v6e.patch:
+``needs_fp4_emulation`` (:9-14), ``e2m1_to_codes`` (:17-30), ``decode_codes``
+(:33-41) and ``gmm_v2(..., rhs_fp4_codes)`` (:100-151), on MI355X.
+
+Weights.  The reference stores fp4 expert weights as uint4 codes once at load
+time so that gmm_v2 does not re-encode them per call.  Here the load-time step
+is ``prepack_fp4`` (and ``fused_moe_gmm.fp4_weight_to_codes``), which also
+takes the block scales and returns an ``Fp4Weight`` in the K-major layout the
+gfx950 kernel streams with 16-byte loads.  ``gmm_v2`` accepts an ``Fp4Weight``
+directly; a raw packed weight tensor is prepacked on every call (a full pass
+over all experts, as the reference's per-call re-encoding is).
+
+Tensor conventions (torch has no uint4): a 4-bit array of shape [..., N] is a
+uint8 tensor [..., N/2] with element 2j in the low nibble, or a
+``torch.float4_e2m1fn_x2`` tensor of the same bytes.
+"""
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+
+FP4_DTYPES = tuple(t for t in (getattr(torch, "float4_e2m1fn_x2", None),) if t is not None)
+
+
+def needs_fp4_emulation(dtype) -> bool:
+    """Whether an fp4 rhs must be converted before the kernel can stream it.
+
+    The reference returns True for float4_e2m1fn on TPUs older than v7
+    (:9-14).  On MI355X the converter is native, but the kernel streams the
+    prepacked layout, so a float4 weight always goes through ``prepack_fp4``
+    (once, at load time).
+    """
+    return dtype in FP4_DTYPES
+
+
+def _as_bytes(t: torch.Tensor) -> torch.Tensor:
+    if t.dtype in FP4_DTYPES:
+        return t.view(torch.uint8)
+    if t.dtype != torch.uint8:
+        raise ValueError(f"expected packed 4-bit bytes (uint8 or float4_e2m1fn_x2), got {t.dtype}")
+    return t
+
+
+def e2m1_to_codes(rhs: torch.Tensor) -> torch.Tensor:
+    """Re-encodes packed e2m1 nibbles as gmm_v2 uint4 codes (same shape, uint8).
+
+    A code holds the int4 q = sign * (2 * exponent + mantissa); -0 becomes +0
+    (:17-30).  One elementwise device pass.
+    """
+    src = _as_bytes(rhs).contiguous()
+    _lib.require_cuda(src)
+    out = torch.empty_like(src, dtype=torch.uint8)
+    _lib.call("dwm_e2m1_to_codes", _lib.ptr(src), _lib.ptr(out), src.numel(), _lib.stream_handle(src.device))
+    return out
+
+
+def decode_fp4(packed: torch.Tensor, fmt: int, scales: torch.Tensor = None, check: bool = True) -> torch.Tensor:
+    """Packed 4-bit values (``_lib.FP4_E2M1`` or ``_lib.FP4_CODES``) -> bf16
+    [..., 2 * last], times the e8m0 scale of each 32-value block of the flat
+    index when ``scales`` (uint8 codes) is given.  Decodes through the same
+    converter as the gmm kernel."""
+    src = _as_bytes(packed).contiguous()
+    _lib.require_cuda(src, scales)
+    n = src.numel() * 2
+    if scales is not None:
+        scales = scales.contiguous()
+        if scales.dtype != torch.uint8 or scales.numel() * 32 < n:
+            raise ValueError("scales must be uint8 e8m0 codes, one per 32 values")
+    out = torch.empty(src.shape[:-1] + (src.shape[-1] * 2,), dtype=torch.bfloat16, device=src.device)
+    flags = torch.zeros(1, dtype=torch.int32, device=src.device)
+    _lib.call("dwm_fp4_decode", _lib.ptr(src), fmt, n, _lib.ptr(scales), _lib.ptr(out), _lib.ptr(flags),
+              _lib.stream_handle(src.device))
+    if check and int(flags.item()) & 1:
+        raise ValueError("e8m0 scale code 255 (not a finite power of two)")
+    return out
+
+
+def decode_codes(codes: torch.Tensor, dtype=torch.bfloat16) -> torch.Tensor:
+    """Exactly decodes gmm_v2 uint4 codes (packed, uint8) to ``dtype`` (:33-41)."""
+    return decode_fp4(codes, _lib.FP4_CODES).to(dtype)
+
+
+@dataclass(frozen=True)
+class Fp4Weight:
+    """Prepacked fp4 expert weights [E, K, N] with e8m0 block-32 scales along K.
+
+    ``weight`` and ``scale`` are uint8 device tensors in the kernel layout
+    (documented in dw-tpu_amd/csrc/fp4.hip).
+    """
+    weight: torch.Tensor
+    scale: torch.Tensor
+    num_experts: int
+    k: int
+    n: int
+
+    @property
+    def shape(self):
+        return (self.num_experts, self.k, self.n)
+
+    @property
+    def device(self):
+        return self.weight.device
+
+
+def prepack_fp4(rhs: torch.Tensor, rhs_scale: torch.Tensor, rhs_fp4_codes: bool = False) -> Fp4Weight:
+    """One-time relayout of packed fp4 expert weights and their scales.
+
+    rhs: [E, K, N/2] packed bytes -- e2m1 nibbles (uint8 or
+    float4_e2m1fn_x2), or gmm_v2 codes when ``rhs_fp4_codes``.
+    rhs_scale: [E, K/32, 1, N] or [E, K/32, N]: uint8 e8m0 codes, or f32 /
+    bf16 powers of two (the lossless e8m0 set, e8m0_scale.py:25-34).
+    Synchronises the stream once to check the scales (load time).
+    """
+    if rhs_fp4_codes and rhs.dtype != torch.uint8:
+        raise ValueError(f"rhs_fp4_codes expects uint4 rhs, got {rhs.dtype}.")
+    src = _as_bytes(rhs).contiguous()
+    _lib.require_cuda(src, rhs_scale)
+    if src.dim() != 3:
+        raise ValueError(f"rhs must be [E, K, N/2] packed bytes, got shape {tuple(src.shape)}")
+    e, k, half_n = src.shape
+    n = 2 * half_n
+    if rhs_scale is None:
+        raise ValueError("fp4 weights need block scales")
+    sc = rhs_scale
+    if sc.dim() == 4:
+        if sc.shape[2] != 1:
+            raise ValueError(f"rhs_scale must be [E, K/32, 1, N], got {tuple(sc.shape)}")
+        sc = sc.reshape(sc.shape[0], sc.shape[1], sc.shape[3])
+    if tuple(sc.shape) != (e, k // 32, n) or k % 32:
+        raise ValueError(f"rhs_scale shape {tuple(rhs_scale.shape)} does not match rhs [E={e}, K={k}, N={n}]"
+                         " with 32-element blocks along K")
+    sc = sc.contiguous()
+    wb = ctypes.c_int64(0)
+    sb = ctypes.c_int64(0)
+    _lib.call("dwm_gmm_fp4_prepack_size", e, k, n, ctypes.byref(wb), ctypes.byref(sb))
+    wout = torch.empty(wb.value, dtype=torch.uint8, device=src.device)
+    sout = torch.zeros(sb.value, dtype=torch.uint8, device=src.device)
+    flags = torch.zeros(1, dtype=torch.int32, device=src.device)
+    fmt = _lib.FP4_CODES if rhs_fp4_codes else _lib.FP4_E2M1
+    _lib.call("dwm_gmm_fp4_prepack", _lib.ptr(src), fmt, _lib.ptr(sc), _lib.dtype_code(sc.dtype), e, k, n,
+              _lib.ptr(wout), _lib.ptr(sout), _lib.ptr(flags), _lib.stream_handle(src.device))
+    f = int(flags.item())
+    if f & 1:
+        raise ValueError("rhs_scale holds a value that is not +0.0 or a power of two in the e8m0 range "
+                         "(code 255, a negative, subnormal or non-power-of-two scale)")
+    if f & 2:
+        raise ValueError("rhs holds uint4 code 8 (q = -8), which e2m1_to_codes never produces")
+    return Fp4Weight(wout, sout, e, k, n)
+
+
+def gmm_v2(lhs: torch.Tensor,
+           rhs,
+           group_sizes: torch.Tensor,
+           rhs_scale: torch.Tensor = None,
+           rhs_bias: torch.Tensor = None,
+           group_offset=None,
+           *,
+           tile_info=None,
+           vmem_limit_bytes=None,
+           preferred_element_type=None,
+           lhs_quant_dtype=None,
+           rhs_quant_dtype=None,
+           zero_initialize: bool = True,
+           fuse_act=None,
+           transpose_rhs: bool = False,
+           rhs_fp4_codes: bool = False) -> torch.Tensor:
+    """Ragged grouped matmul: out[rows of g] = lhs[rows of g] @ dequant(rhs[g - group_offset]).
+
+    lhs: [M, K] bf16, rows sorted by group.  rhs: ``Fp4Weight`` (prepacked)
+    or packed fp4 bytes [E, K, N/2] (prepacked per call).  group_sizes:
+    int32 [G] device tensor.  group_offset: None, an int, or an int32 [1]
+    device tensor (first local group).  Returns [M, N] in
+    ``preferred_element_type`` (bf16 default, or float32).  Rows outside the
+    local groups are zero when ``zero_initialize`` and unspecified otherwise.
+    Tiling / VMEM arguments of the TPU kernel are accepted and ignored.
+    """
+    if rhs_bias is not None:
+        raise NotImplementedError("gmm_v2: rhs_bias is not supported by the fp4 kernel")
+    if fuse_act is not None:
+        raise NotImplementedError(f"gmm_v2: fused activation {fuse_act!r} is not supported")
+    if transpose_rhs:
+        raise NotImplementedError("gmm_v2: transpose_rhs is not supported")
+    if lhs_quant_dtype is not None:
+        raise NotImplementedError("gmm_v2: lhs quantization is not supported with fp4 codes")
+    if isinstance(rhs, Fp4Weight):
+        if rhs_scale is not None:
+            raise ValueError("gmm_v2: a prepacked Fp4Weight carries its own scales; pass rhs_scale=None")
+        w = rhs
+    else:
+        w = prepack_fp4(rhs, rhs_scale, rhs_fp4_codes=rhs_fp4_codes)
+    out_dtype = lhs.dtype if preferred_element_type is None else preferred_element_type
+    if lhs.dtype != torch.bfloat16:
+        raise ValueError(f"gmm_v2: lhs must be bfloat16, got {lhs.dtype}")
+    if out_dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError(f"gmm_v2: preferred_element_type must be bfloat16 or float32, got {out_dtype}")
+    if lhs.dim() != 2 or lhs.shape[1] != w.k:
+        raise ValueError(f"gmm_v2: lhs shape {tuple(lhs.shape)} does not match rhs K={w.k}")
+    if group_sizes.dtype != torch.int32 or group_sizes.dim() != 1:
+        raise ValueError("gmm_v2: group_sizes must be a 1-D int32 tensor")
+    dev = _lib.require_cuda(lhs, w.weight, group_sizes)
+    lhs = lhs.contiguous()
+    if lhs.data_ptr() % 16:
+        lhs = lhs.clone()  # the kernel streams 16-byte rows
+    gs = group_sizes.contiguous()
+    if group_offset is None:
+        go = None
+    elif isinstance(group_offset, int):
+        go = torch.tensor([group_offset], dtype=torch.int32, device=dev)
+    else:
+        go = group_offset.reshape(-1)[:1].to(device=dev, dtype=torch.int32).contiguous()
+    m = lhs.shape[0]
+    out = torch.empty((m, w.n), dtype=out_dtype, device=dev)
+    _lib.call("dwm_gmm_fp4", _lib.ptr(lhs), m, w.k, _lib.ptr(w.weight), _lib.ptr(w.scale), _lib.ptr(gs),
+              gs.numel(), _lib.ptr(go), w.num_experts, w.n, _lib.ptr(out), _lib.dtype_code(out_dtype),
+              1 if zero_initialize else 0, _lib.stream_handle(dev))
+    return out

@@ -1,0 +1,166 @@
+/*
+ * dwtpu_moe.h -- C ABI of the MI355X (gfx950) MoE expert hot path.
+ *
+ * One shared library, libdwtpu_moe.so, built with hipcc for gfx950.  Every
+ * entry point takes caller-owned device pointers, plain sizes and a HIP
+ * stream handle passed as `void *` (a hipStream_t; NULL = the null stream).
+ * Calls are asynchronous on that stream unless stated otherwise, allocate no
+ * device memory (scratch comes in through a `workspace` argument sized by a
+ * *_workspace_size query) and are reentrant.
+ *
+ * Return value: DWM_OK, or an error status; dwm_last_error() then returns a
+ * thread-local message.  DWM_ERR_UNSUPPORTED means "valid request this
+ * library has no kernel for" -- the Python layer maps it to the reference's
+ * fail-closed fallback (None), like try_dense_fp8 / pallas_supported.
+ * Argument checks run on the host before any launch.
+ *
+ * References below are to files of the reference (jamesdborin/dw-tpu).
+ */
+#ifndef DWTPU_MOE_H_
+#define DWTPU_MOE_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum dwm_status {
+  DWM_OK = 0,
+  DWM_ERR_INVALID = 1,     /* bad argument (shape, pointer, dtype, value) */
+  DWM_ERR_UNSUPPORTED = 2, /* valid but not handled here: caller falls back */
+  DWM_ERR_HIP = 3          /* a HIP runtime call failed */
+};
+
+enum dwm_dtype {
+  DWM_BF16 = 0,
+  DWM_F32 = 1,
+  DWM_U8 = 2 /* e8m0 exponent codes for scales */
+};
+
+/* Packed 4-bit weight formats (two per byte, element 2j in the low nibble). */
+enum dwm_fp4_format {
+  DWM_FP4_E2M1 = 0, /* OCP e2m1 nibbles (torch float4_e2m1fn_x2 bytes) */
+  DWM_FP4_CODES = 1 /* gmm_v2 uint4 codes: int4 q = sign*(2*exp+mant) */
+};
+
+/* Library version (major*100 + minor). */
+int dwm_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char *dwm_last_error(void);
+
+/* ---------------------------------------------------------------------- */
+/* FP4 weight codes.                                                       */
+/* ---------------------------------------------------------------------- */
+
+/* e2m1 nibbles -> gmm_v2 uint4 codes, elementwise over `nbytes` packed bytes.
+ * Replaces e2m1_to_codes (patches/tokamax/0001-gmm_v2-fp4-emulation-v6e.patch:17-30)
+ * as used by fp4_weight_to_codes (patches/tpu-inference/0001-dsv4-v6e-enablement.patch:276-300). */
+int dwm_e2m1_to_codes(const uint8_t *e2m1, uint8_t *codes, int64_t nbytes, void *stream);
+
+/* Decode `n` packed 4-bit values (format DWM_FP4_*) to bf16 bit patterns,
+ * each multiplied by the e8m0 scale of its 32-element block along the flat
+ * index when `scales` is not NULL (one uint8 code per 32 values).  Bit-exact
+ * test hook for decode_codes (patches/tokamax/0001-...:33-41) and the block
+ * dequant order of patches/tpu-inference-experimental/fused-moe-fp4/0901-...:84-96.
+ * It converts through the same canonical e2m1 nibbles and hardware
+ * converter as the gmm kernel.  n must be even.  `flags` (device int32[1])
+ * gets bit 0 ORed in for scale code 255 (output NaN) and bit 1 for code 8
+ * (q = -8, decoded to -8 * scale although no e2m1 value equals it). */
+int dwm_fp4_decode(const uint8_t *packed, int format, int64_t n, const uint8_t *scales,
+                   uint16_t *out_bf16, int32_t *flags, void *stream);
+
+/* ---------------------------------------------------------------------- */
+/* FP4 grouped matmul (tokamax gmm_v2 with rhs_fp4_codes).                 */
+/* ---------------------------------------------------------------------- */
+
+/* Bytes of the load-time weight layout produced by dwm_gmm_fp4_prepack for
+ * E experts of a [K, N] fp4 matrix with 32-element e8m0 block scales along K.
+ * Requires K % 64 == 0 and N % 32 == 0. */
+int dwm_gmm_fp4_prepack_size(int64_t E, int64_t K, int64_t N, int64_t *weight_bytes,
+                             int64_t *scale_bytes);
+
+/* One-time relayout of expert weights into the kernel's K-major tiles; the
+ * load-time step the reference performs with fp4_weight_to_codes
+ * (patches/tpu-inference/0001-...:276-300, shard_moe_weights :302-313).
+ *   rhs:   [E, K, N/2] bytes, format DWM_FP4_E2M1 or DWM_FP4_CODES.
+ *   scale: [E, K/32, N] (the reference's [E, K/32, 1, N]) of dtype
+ *          DWM_U8 (e8m0 codes, e8m0_scale.py:14-40), DWM_F32 or DWM_BF16.
+ *          f32/bf16 scales must be powers of two or +0.0 (the lossless
+ *          e8m0 subset, e8m0_scale.py:25-34).
+ *   flags: device int32[1]; the kernel ORs 1 into it for a scale that is not
+ *          an e8m0-representable power of two or +0.0 (including code 255).
+ *          The caller zeroes it beforehand and checks it after the stream
+ *          synchronises (weight load time).
+ * Scale code 0 (+0.0) is kept exact: the block's values become +-0 with
+ * the sign of the decoded code, as decode(q) * bf16(0.0) gives. */
+int dwm_gmm_fp4_prepack(const uint8_t *rhs, int format, const void *scale, int scale_dtype,
+                        int64_t E, int64_t K, int64_t N, uint8_t *weight_out,
+                        uint8_t *scale_out, int32_t *flags, void *stream);
+
+/* Ragged grouped matmul on prepacked weights:
+ *   for g in [group_offset, group_offset + E_local):
+ *     out[off_g : off_g + size_g] = lhs[off_g : off_g + size_g] @ dequant(rhs[g - group_offset])
+ * with off_g the exclusive prefix sum of group_sizes[0..num_groups).  bf16 x
+ * bf16 products of the exact dequantised weights, f32 accumulation, output
+ * bf16 (round to nearest even) or f32.  Rows outside the local groups are
+ * zeroed when zero_init != 0 and left untouched otherwise.
+ * Replaces gmm_v2(lhs, rhs, group_sizes, rhs_scale, group_offset,
+ * preferred_element_type, zero_initialize, rhs_fp4_codes=True)
+ * (patches/tokamax/0001-...:100-151) behind gmm_wrapper
+ * (patches/tpu-inference/0001-...:214-233).
+ *   lhs:          [M, K] bf16, expert-sorted rows.
+ *   group_sizes:  device int32[num_groups].
+ *   group_offset: device int32[1] or NULL (= 0).
+ *   out_dtype:    DWM_BF16 or DWM_F32 (the MOE_F32_REDUCE variant,
+ *                 patches/tpu-inference-ext/0106-...:243-250).
+ * Requires K % 64 == 0, N % 32 == 0, num_groups <= 1024. */
+int dwm_gmm_fp4(const uint16_t *lhs, int64_t M, int64_t K, const uint8_t *weight,
+                const uint8_t *scale, const int32_t *group_sizes, int num_groups,
+                const int32_t *group_offset, int64_t E_local, int64_t N, void *out,
+                int out_dtype, int zero_init, void *stream);
+
+/* ---------------------------------------------------------------------- */
+/* MoE dispatch and combine.                                               */
+/* ---------------------------------------------------------------------- */
+
+/* Scratch bytes for dwm_moe_dispatch over n = T*topk ids and E experts. */
+int dwm_moe_dispatch_workspace_size(int64_t n, int num_experts, int64_t *bytes);
+
+/* Expert-sorted dispatch indices from topk_ids [T, topk] (int32):
+ *   perm        = stable argsort(topk_ids.flatten())     (0405-moe-fast-dispatch.patch:73)
+ *   tok_sorted  = perm / topk                           (moe_fast_dispatch.py:41-44)
+ *   revert      = inverse permutation of perm           (combine indices, moe_fast_combine.py:14-22)
+ *   group_sizes = bincount(topk_ids, num_experts)       (0405-...:85-87)
+ *   group_offsets (nullable) = [0, cumsum(group_sizes)]  (num_experts + 1 entries)
+ * Bit-exact.  Ids outside [0, num_experts) are rejected on the device:
+ * `flags` (device int32[1], nullable) gets bit 0 ORed in and such ids are
+ * ordered after every valid id. */
+int dwm_moe_dispatch(const int32_t *topk_ids, int64_t T, int topk, int num_experts,
+                     int32_t *perm, int32_t *tok_sorted, int32_t *revert, int32_t *group_sizes,
+                     int32_t *group_offsets, int32_t *flags, void *workspace, void *stream);
+
+/* out[j, :] = src[idx[j], :] for j < rows, bitwise, with JAX gather index
+ * semantics (a negative index wraps once, then indices clamp into
+ * [0, src_rows)).  Replaces dispatch_gather_pallas / hidden[tok_sorted]
+ * (moe_fast_dispatch.py:134-194). */
+int dwm_row_gather(const void *src, int64_t src_rows, int64_t row_bytes, const int32_t *idx,
+                   int64_t rows, void *out, void *stream);
+
+/* out[t] = round(sum_{k=0..topk-1} f32(x[idx[t*topk+k]]) * f32(w[t, k])),
+ * summed left to right from +0.0 with separately rounded f32 multiply and
+ * add (no FMA), one rounding to out_dtype.  Bit-exact to combine_xla /
+ * combine_pallas (moe_fast_combine.py:44-54, 57-122, 201-207).
+ *   x: [x_rows, H] of x_dtype (DWM_BF16 / DWM_F32); idx: [T*topk] int32
+ *   (JAX gather semantics as dwm_row_gather); w: [T, topk] of w_dtype;
+ *   out: [T, H] of out_dtype. */
+int dwm_moe_combine(const void *x, int x_dtype, int64_t x_rows, int64_t H, const int32_t *idx,
+                    const void *w, int w_dtype, int64_t T, int topk, void *out, int out_dtype,
+                    void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DWTPU_MOE_H_ */

@@ -1,0 +1,59 @@
+"""Dense FP8 block-quantized GEMM -- numpy restatement.
+
+Test infrastructure only (see oracle/__init__.py).
+
+* W8A16: kernels/tpu_inference/kernels/experimental/dense_fp8.py:23-59.
+  For each 128-row K block kb: acc += dot(x_bf16[:, kb], w_e4m3[kb, :]) (f32)
+  * s[kb, :] (f32), acc initialised to zero; stored as bf16.
+* W8A8 (activations e4m3 with per-(token, 128-K) f32 scales, weights e4m3 with
+  128x128 f32 block scales): no reference kernel; the closed form is
+  out[m, n] = sum_kb sx[m, kb] * sw[kb, n // 128] * dot(xq[m, kb], wq[kb, n]).
+"""
+import numpy as np
+
+from .numerics import E4M3_VALUES, round_bf16
+
+
+def matmul_w8a16(x, w_codes, s, accumulate: str = "f64", out_dtype: str = "bfloat16"):
+    """x [M, K] f32 (bf16-exact); w_codes [K, N] e4m3 codes; s [K/128, 1, N] f32."""
+    x = np.asarray(x, np.float32)
+    m, k = x.shape
+    n = w_codes.shape[1]
+    w = E4M3_VALUES[np.asarray(w_codes)].astype(np.float32)
+    s = np.asarray(s, np.float32).reshape(k // 128, n)
+    dt = np.float64 if accumulate == "f64" else np.float32
+    acc = np.zeros((m, n), dt)
+    for kb in range(k // 128):
+        part = x[:, kb * 128:(kb + 1) * 128].astype(dt) @ w[kb * 128:(kb + 1) * 128].astype(dt)
+        acc = acc + part * s[kb].astype(dt)[None, :]
+    if out_dtype == "bfloat16":
+        return round_bf16(acc.astype(np.float32))
+    return acc
+
+
+def matmul_w8a8(xq, sx, wq, sw, accumulate: str = "f64", out_dtype: str = "bfloat16"):
+    """xq [M, K] e4m3 codes, sx [M, K/128] f32; wq [K, N] e4m3, sw [K/128, N/128] f32."""
+    xv = E4M3_VALUES[np.asarray(xq)].astype(np.float32)
+    wv = E4M3_VALUES[np.asarray(wq)].astype(np.float32)
+    m, k = xv.shape
+    n = wv.shape[1]
+    dt = np.float64 if accumulate == "f64" else np.float32
+    sx = np.asarray(sx, np.float32)
+    sw_full = np.repeat(np.asarray(sw, np.float32), 128, axis=1)[:, :n]  # [K/128, N]
+    acc = np.zeros((m, n), dt)
+    for kb in range(k // 128):
+        part = xv[:, kb * 128:(kb + 1) * 128].astype(dt) @ wv[kb * 128:(kb + 1) * 128].astype(dt)
+        acc = acc + part * (sx[:, kb:kb + 1].astype(dt) * sw_full[kb][None, :].astype(dt))
+    if out_dtype == "bfloat16":
+        return round_bf16(acc.astype(np.float32))
+    return acc
+
+
+def abs_product_w8a16(x, w_codes, s):
+    """sum_k |x_mk| |w_kn s_kn| (float64), for the error bound."""
+    k = x.shape[1]
+    n = w_codes.shape[1]
+    w = np.abs(E4M3_VALUES[np.asarray(w_codes)].astype(np.float64))
+    s = np.abs(np.asarray(s, np.float64).reshape(k // 128, 1, n))
+    w = (w.reshape(k // 128, 128, n) * s).reshape(k, n)
+    return np.abs(np.asarray(x, np.float64)) @ w

@@ -1,0 +1,116 @@
+"""Ragged grouped matmul (tokamax gmm_v2 with FP4 codes) -- numpy restatement.
+
+Test infrastructure only (see oracle/__init__.py).
+
+Semantics restated from:
+* patches/tokamax/0001-gmm_v2-fp4-emulation-v6e.patch:58-66 (decode each rhs
+  tile to the lhs dtype inside the kernel), :93-96 (lhs is not quantized when
+  rhs is emulated fp4), :128-141 (rhs_fp4_codes requires uint4 rhs).
+* patches/tpu-inference/0001-dsv4-v6e-enablement.patch:214-233 (gmm_wrapper
+  calls gmm_v2 with zero_initialize=False).
+* patches/tpu-inference-ext/0103-...:94-97 (rows outside the local groups are
+  left unwritten when zero_initialize is False).
+* patches/tpu-inference-ext/0106-...:243-250 (f32 output variant).
+
+Rows [off_g, off_g + size_g) of the expert-sorted lhs, for each local group
+g in [group_offset, group_offset + E_local), are multiplied by
+dequant(rhs[g - group_offset]); off_g is the exclusive prefix sum of ALL
+group sizes.  Accumulation is f32 in the reference; its order inside the
+un-vendored kernel is unknown, so this oracle offers the float64 product of
+the exact bf16 inputs (the closed form) and an f32 BLAS product.
+"""
+import numpy as np
+
+from .fp4 import dequant_fp4_block
+from .numerics import round_bf16
+
+
+def group_starts(group_sizes: np.ndarray) -> np.ndarray:
+    gs = np.asarray(group_sizes, np.int64)
+    return np.concatenate([[0], np.cumsum(gs)])[:-1]
+
+
+def dequant_rhs(codes: np.ndarray, scale: np.ndarray, block: int = 32) -> np.ndarray:
+    """codes [E, K, N] uint4 values; scale [E, K/block, 1, N] f32 -> f32 [E, K, N]."""
+    e, k, n = codes.shape
+    scale = np.asarray(scale, np.float32).reshape(e, k // block, 1, n)
+    return np.stack([dequant_fp4_block(codes[i], scale[i], block) for i in range(e)])
+
+
+def gmm(lhs, codes, scale, group_sizes, group_offset: int = 0, out_dtype: str = "bfloat16",
+        accumulate: str = "f64", zero_initialize: bool = True, w=None):
+    """Returns (out [M, N] float32 or float64 values, written-row mask [M]).
+
+    lhs: [M, K] float32 holding bf16-exact values.  codes: [E_local, K, N]
+    uint4 code values (0..15).  scale: [E_local, K/32, 1, N] f32.
+    ``w`` may pass a precomputed ``dequant_rhs`` result.
+    With out_dtype 'bfloat16' the result is rounded to bf16 (RNE); with
+    'float32' to f32; with 'float64' it is returned unrounded.
+    """
+    lhs = np.asarray(lhs, np.float32)
+    m, k = lhs.shape
+    e_local = codes.shape[0] if w is None else w.shape[0]
+    n = codes.shape[2] if w is None else w.shape[2]
+    if w is None:
+        w = dequant_rhs(codes, scale)
+    starts = group_starts(group_sizes)
+    gs = np.asarray(group_sizes, np.int64)
+    out = np.zeros((m, n), np.float64)
+    written = np.zeros(m, bool)
+    for g in range(group_offset, min(group_offset + e_local, len(gs))):
+        r0, r1 = int(starts[g]), int(starts[g] + gs[g])
+        r1 = min(r1, m)
+        if r1 <= r0:
+            continue
+        a = lhs[r0:r1]
+        if accumulate == "f64":
+            y = a.astype(np.float64) @ w[g - group_offset].astype(np.float64)
+        else:
+            y = (a @ w[g - group_offset].astype(np.float32)).astype(np.float64)
+        out[r0:r1] = y
+        written[r0:r1] = True
+    if out_dtype == "bfloat16":
+        out = round_bf16(out.astype(np.float32))
+    elif out_dtype == "float32":
+        out = out.astype(np.float32)
+    if not zero_initialize:
+        out = np.where(written[:, None], out, np.nan)
+    return out, written
+
+
+def abs_product(lhs, w, group_sizes, group_offset: int = 0):
+    """sum_k |a_mk| |w_kn| per output element (float64): the scale of the
+    f32 accumulation error term of the tolerance."""
+    m = lhs.shape[0]
+    starts = group_starts(group_sizes)
+    gs = np.asarray(group_sizes, np.int64)
+    out = np.zeros((m, w.shape[2]), np.float64)
+    for g in range(group_offset, min(group_offset + w.shape[0], len(gs))):
+        r0, r1 = int(starts[g]), min(int(starts[g] + gs[g]), m)
+        if r1 > r0:
+            out[r0:r1] = np.abs(lhs[r0:r1]).astype(np.float64) @ np.abs(w[g - group_offset]).astype(np.float64)
+    return out
+
+
+def error_bound(y64, absprod, k: int, out_dtype: str = "bfloat16"):
+    """Stated tolerance for a gmm output element against the float64 value:
+
+        |y - y64| <= u_out * |y64| + K * 2^-24 * sum_k |a_k w_k|
+
+    u_out = 2^-8 (bf16 round to nearest) or 2^-24 (f32); the second term
+    bounds any order of f32 accumulation of K exact bf16 x bf16 products.
+    """
+    u_out = 2.0 ** -8 if out_dtype == "bfloat16" else 2.0 ** -24
+    return u_out * np.abs(y64) + k * 2.0 ** -24 * absprod
+
+
+def error_stats(y, y64, mask=None):
+    """max abs error and relative Frobenius error against float64."""
+    y = np.asarray(y, np.float64)
+    y64 = np.asarray(y64, np.float64)
+    if mask is not None:
+        y, y64 = y[mask], y64[mask]
+    d = y - y64
+    den = np.linalg.norm(y64)
+    return {"max_abs": float(np.abs(d).max()) if d.size else 0.0,
+            "rel_fro": float(np.linalg.norm(d) / den) if den > 0 else float(np.linalg.norm(d))}

@@ -1,0 +1,109 @@
+"""Weight/activation (re)quantization formats feeding the hot path -- numpy.
+
+Test infrastructure only (see oracle/__init__.py).
+
+Reference files restated here:
+* patches/tpu-inference/0001-dsv4-v6e-enablement.patch:315-350
+  (quantize_tensor with power_of_two_scale: 2^ceil(log2(absmax/dtype_max)))
+* patches/tpu-inference/0001-dsv4-v6e-enablement.patch:47-56
+  (DeepSeek act_quant reference: amax floor 1e-4, pow2 scale, clip +-448)
+"""
+import numpy as np
+
+from .fp4 import E2M1_VALUES
+from .numerics import E4M3_VALUES, to_e4m3
+
+E2M1_MAX = 6.0
+E4M3_MAX = 448.0
+
+
+def pow2_ceil(scale: np.ndarray) -> np.ndarray:
+    """2^ceil(log2(s)) for s > 0 computed exactly via frexp (mant in
+    [0.5, 1)); s <= 0 passes through (0001-...:339-347)."""
+    s = np.asarray(scale, np.float32)
+    mant, exp = np.frexp(s)
+    e = np.where(mant == 0.5, exp - 1, exp)
+    return np.where(s > 0, np.ldexp(np.float32(1.0), e).astype(np.float32), s).astype(np.float32)
+
+
+def to_e2m1(x: np.ndarray) -> np.ndarray:
+    """float32 -> e2m1 nibble (0..15), round to nearest even, saturating at 6."""
+    x = np.asarray(x, np.float32)
+    mags = E2M1_VALUES[:8].astype(np.float64)  # 0, .5, 1, 1.5, 2, 3, 4, 6
+    a = np.minimum(np.abs(x).astype(np.float64), 6.0)
+    idx = np.clip(np.searchsorted(mags, a, side="left"), 1, 7)
+    lo, hi = mags[idx - 1], mags[idx]
+    pick_hi = (hi - a < a - lo) | ((hi - a == a - lo) & (idx % 2 == 0))
+    code = np.where(pick_hi, idx, idx - 1)
+    code = np.where(a == 0, 0, code)
+    return (code | (np.signbit(x).astype(np.int64) << 3)).astype(np.uint8)
+
+
+def quantize_tensor_pow2(x: np.ndarray, dtype: str, axis: int, block: int):
+    """Blockwise quantization along ``axis`` with power-of-two scales.
+
+    0001-...:315-350: scale = absmax / dtype_max rounded up to a power of two;
+    q = round(x / scale) in the target format.  Returns (codes, scale) where
+    scale has the blocked axis reduced to size len/block (keepdims layout
+    [..., nblocks, ...]).
+    """
+    x = np.asarray(x, np.float32)
+    x = np.moveaxis(x, axis, -1)
+    shp = x.shape
+    xb = x.reshape(shp[:-1] + (shp[-1] // block, block))
+    dmax = E2M1_MAX if dtype == "e2m1" else E4M3_MAX
+    amax = np.abs(xb).max(axis=-1, keepdims=True)
+    scale = pow2_ceil((amax / np.float32(dmax)).astype(np.float32))
+    inv = np.where(scale == 0, np.float32(np.inf), np.float32(1.0) / np.where(scale == 0, 1, scale))
+    q = xb * np.where(np.isinf(inv), 0, inv).astype(np.float32)
+    codes = to_e2m1(q) if dtype == "e2m1" else to_e4m3(q)
+    codes = np.moveaxis(codes.reshape(shp), -1, axis)
+    scale = np.moveaxis(scale[..., 0], -1, axis)
+    return codes, scale
+
+
+def dequantize(codes: np.ndarray, scale: np.ndarray, dtype: str, axis: int, block: int) -> np.ndarray:
+    tab = E2M1_VALUES if dtype == "e2m1" else E4M3_VALUES
+    v = np.moveaxis(tab[np.asarray(codes)], axis, -1)
+    s = np.moveaxis(np.asarray(scale, np.float32), axis, -1)
+    shp = v.shape
+    out = v.reshape(shp[:-1] + (shp[-1] // block, block)) * s[..., None]
+    return np.moveaxis(out.reshape(shp), -1, axis)
+
+
+def act_quant_ue8m0(x: np.ndarray, block: int, nope: int) -> np.ndarray:
+    """DeepSeek-V4 act_quant(x, block, 'ue8m0', inplace) on x[..., :nope]:
+    amax floored at 1e-4, scale 2^ceil(log2(amax/448)), clip to +-448, e4m3
+    round, dequantize in place (0001-...:47-56)."""
+    out = np.asarray(x, np.float32).copy()
+    xb = out[..., :nope].reshape(*x.shape[:-1], nope // block, block)
+    amax = np.maximum(np.abs(xb).max(-1, keepdims=True), np.float32(1e-4))
+    scale = np.exp2(np.ceil(np.log2(amax / np.float32(448.0)))).astype(np.float32)
+    q = np.clip(xb / scale, -448, 448).astype(np.float32)
+    q = E4M3_VALUES[to_e4m3(q)]
+    out[..., :nope] = (q * scale).reshape(*x.shape[:-1], nope)
+    return out
+
+
+def quantize_fp8_blocks(w: np.ndarray, block=(128, 128)):
+    """[K, N] float32 -> (e4m3 codes [K, N], f32 scales [K/bk, N/bn]) with
+    scale = block absmax / 448 (not rounded to a power of two)."""
+    k, n = w.shape
+    bk, bn = block
+    wb = np.asarray(w, np.float32).reshape(k // bk, bk, n // bn, bn)
+    amax = np.abs(wb).max(axis=(1, 3)).astype(np.float32)
+    scale = (amax / np.float32(448.0)).astype(np.float32)
+    safe = np.where(scale == 0, np.float32(1), scale)
+    q = (wb / safe[:, None, :, None]).astype(np.float32)
+    return to_e4m3(q.reshape(k, n)), scale
+
+
+def quantize_fp8_rows(x: np.ndarray, block: int = 128):
+    """[M, K] float32 -> (e4m3 codes [M, K], f32 scales [M, K/block]),
+    scale = absmax of each (row, K-block) / 448."""
+    m, k = x.shape
+    xb = np.asarray(x, np.float32).reshape(m, k // block, block)
+    amax = np.abs(xb).max(axis=2).astype(np.float32)
+    scale = (amax / np.float32(448.0)).astype(np.float32)
+    safe = np.where(scale == 0, np.float32(1), scale)
+    return to_e4m3((xb / safe[:, :, None]).reshape(m, k)), scale

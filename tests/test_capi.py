@@ -1,0 +1,95 @@
+"""The C ABI library loads without a GPU, exports every symbol the header
+declares, and rejects bad arguments on the host before any launch."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from dw_tpu_amd import _lib
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "dwtpu_moe.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(dwm_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_bound_entry_points():
+    names = declared_functions()
+    assert names, "no declarations parsed"
+    assert sorted(_lib.SIGNATURES) == names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(_lib.LIB_PATH)
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_version_and_empty_error():
+    lib = _lib.load()
+    assert lib.dwm_version() >= 100
+    assert lib.dwm_last_error() == b""
+
+
+def _rc(name, *args):
+    lib = _lib.load()
+    return getattr(lib, name)(*args), lib.dwm_last_error().decode()
+
+
+def test_gmm_argument_checks_need_no_gpu():
+    null = None
+    # K not a multiple of 64 -> unsupported (fail-closed fallback)
+    rc, msg = _rc("dwm_gmm_fp4", null, 8, 100, null, null, null, 4, null, 4, 64, null, _lib.BF16, 0, null)
+    assert rc == _lib.ERR_UNSUPPORTED and "K" in msg
+    rc, msg = _rc("dwm_gmm_fp4", null, 8, 128, null, null, null, 4, null, 4, 64, null, 7, 0, null)
+    assert rc == _lib.ERR_INVALID and "dtype" in msg
+    rc, msg = _rc("dwm_gmm_fp4", null, 8, 128, null, null, null, 4, null, 4, 64, null, _lib.BF16, 0, null)
+    assert rc == _lib.ERR_INVALID and "null" in msg
+    rc, _ = _rc("dwm_gmm_fp4", null, 0, 128, null, null, null, 4, null, 4, 64, null, _lib.BF16, 0, null)
+    assert rc == _lib.OK  # M == 0: nothing to do
+    rc, msg = _rc("dwm_gmm_fp4", null, 8, 128, null, null, null, 2000, null, 4, 64, null, _lib.BF16, 0, null)
+    assert rc == _lib.ERR_UNSUPPORTED and "groups" in msg
+
+
+def test_prepack_size_query():
+    wb, sb = ctypes.c_int64(), ctypes.c_int64()
+    rc, _ = _rc("dwm_gmm_fp4_prepack_size", 32, 7168, 4096, ctypes.byref(wb), ctypes.byref(sb))
+    assert rc == _lib.OK
+    assert wb.value == 32 * 7168 * 4096 // 2
+    assert sb.value == 32 * (4096 // 32) * ((7168 // 64 + 3) // 4) * 256
+    rc, _ = _rc("dwm_gmm_fp4_prepack_size", 1, 96, 64, ctypes.byref(wb), ctypes.byref(sb))
+    assert rc == _lib.ERR_UNSUPPORTED
+
+
+def test_dispatch_and_combine_argument_checks():
+    ws = ctypes.c_int64()
+    rc, _ = _rc("dwm_moe_dispatch_workspace_size", 65536, 32, ctypes.byref(ws))
+    assert rc == _lib.OK and ws.value == 64 * 33 * 4
+    rc, _ = _rc("dwm_moe_dispatch_workspace_size", 10, 4096, ctypes.byref(ws))
+    assert rc == _lib.ERR_UNSUPPORTED
+    rc, _ = _rc("dwm_moe_dispatch", None, 4, 0, 8, None, None, None, None, None, None, None, None)
+    assert rc == _lib.ERR_INVALID
+    rc, _ = _rc("dwm_moe_combine", None, 5, 4, 8, None, None, _lib.F32, 2, 2, None, _lib.BF16, None)
+    assert rc == _lib.ERR_INVALID
+    rc, _ = _rc("dwm_row_gather", None, 4, 16, None, 0, None, None)
+    assert rc == _lib.OK  # zero rows
+    rc, _ = _rc("dwm_fp4_decode", None, 0, 3, None, None, None, None)
+    assert rc == _lib.ERR_INVALID  # odd count
+
+
+def test_python_layer_rejects_host_tensors():
+    import torch
+    from dw_tpu_amd import e2m1_to_codes
+    with pytest.raises(ValueError):
+        e2m1_to_codes(torch.zeros(4, dtype=torch.uint8))
+
+
+def test_missing_library_is_loud(monkeypatch, tmp_path):
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "nope.so"))
+    with pytest.raises(_lib.LibraryMissing):
+        _lib.load()

@@ -1,0 +1,197 @@
+"""FP4 grouped matmul on the GPU against the float64 oracle.
+
+Tolerance (stated, per element): |y - y64| <= u_out * |y64| + K * 2^-24 *
+sum_k |a_k w_k|, u_out = 2^-8 for bf16 output and 2^-24 for f32 output
+(oracle.gmm.error_bound).  Max abs error and relative Frobenius error are
+reported alongside.  Full-size workloads are checked on sampled rows (the
+first, last and a random row of every non-empty group) and sampled columns.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import bf16_bits, bf16_tensor
+from oracle import fp4, gmm
+from oracle.numerics import bf16_to_f32
+
+pytestmark = pytest.mark.gpu
+
+
+def _nibbles_at(rhs_packed, cols):
+    """e2m1 nibbles [E, K, len(cols)] of a packed [E, K, N/2] weight."""
+    cols = np.asarray(cols)
+    b = rhs_packed[:, :, cols // 2]
+    return np.where(cols % 2 == 1, b >> 4, b & 0xF).astype(np.uint8)
+
+
+def _oracle_cols(lhs_f32, rhs_packed, scale_codes, gs, cols, rows=None, group_offset=0):
+    """float64 oracle and bound for the given columns (and rows)."""
+    codes = fp4.e2m1_to_codes(_nibbles_at(rhs_packed, cols))
+    scale = fp4.e8m0_decode(scale_codes[..., np.asarray(cols)])
+    w = gmm.dequant_rhs(codes, scale)
+    y64, written = gmm.gmm(lhs_f32, None, None, gs, group_offset=group_offset, out_dtype="float64", w=w)
+    ap = gmm.abs_product(lhs_f32, w, gs, group_offset=group_offset)
+    if rows is not None:
+        return y64[rows], ap[rows], written[rows]
+    return y64, ap, written
+
+
+def _run(dev, lhs_bits, rhs, sc, gs, out_dtype=torch.bfloat16, group_offset=None, zero_init=True,
+         prepacked=True):
+    from dw_tpu_amd import fp4_weight_to_codes, gmm_v2
+    lhs = bf16_tensor(lhs_bits, dev)
+    w = torch.from_numpy(rhs).to(dev)
+    s = torch.from_numpy(sc).to(dev)
+    g = torch.from_numpy(np.asarray(gs, np.int32)).to(dev)
+    if prepacked:
+        pw = fp4_weight_to_codes(w, s)
+        out = gmm_v2(lhs, pw, g, group_offset=group_offset, preferred_element_type=out_dtype,
+                     zero_initialize=zero_init)
+    else:
+        out = gmm_v2(lhs, w, g, s, group_offset=group_offset, preferred_element_type=out_dtype,
+                     zero_initialize=zero_init)
+    torch.cuda.synchronize()
+    return out
+
+
+def _check(out, y64, ap, K, out_dtype, mask=None):
+    if out_dtype == torch.bfloat16:
+        y = bf16_to_f32(bf16_bits(out)).astype(np.float64)
+        kind = "bfloat16"
+    else:
+        y = out.cpu().numpy().astype(np.float64)
+        kind = "float32"
+    if mask is not None:
+        y, y64, ap = y[mask], y64[mask], ap[mask]
+    bound = gmm.error_bound(y64, ap, K, kind)
+    err = np.abs(y - y64)
+    stats = gmm.error_stats(y, y64)
+    assert np.all(np.isfinite(y))
+    assert np.all(err <= bound), (stats, float((err / np.maximum(bound, 1e-300)).max()))
+    return stats
+
+
+def _random_case(rng, sizes, K, N, extra_rows=0):
+    E = len(sizes)
+    M = int(sum(sizes)) + extra_rows
+    lhs_bits = bf16_bits_np(rng.standard_normal((M, K)).astype(np.float32))
+    rhs = rng.integers(0, 256, (E, K, N // 2), dtype=np.uint8)
+    sc = rng.integers(123, 130, (E, K // 32, 1, N), dtype=np.uint8)
+    return lhs_bits, rhs, sc, np.array(sizes, np.int32)
+
+
+def bf16_bits_np(x):
+    from oracle.numerics import bf16_bits as f
+    return f(x)
+
+
+CASES = [
+    ([5], 64, 32),
+    ([1, 0, 31, 32, 33], 128, 96),
+    ([127, 128, 129, 0, 3], 192, 256),
+    ([300, 0, 0, 64, 257], 1024, 512),
+    ([0, 0, 0], 64, 64),
+]
+
+
+@pytest.mark.parametrize("sizes,K,N", CASES)
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+def test_gmm_random_shapes(dev, rng, sizes, K, N, out_dtype):
+    lhs_bits, rhs, sc, gs = _random_case(rng, sizes, K, N)
+    out = _run(dev, lhs_bits, rhs, sc, gs, out_dtype=out_dtype)
+    y64, ap, written = _oracle_cols(bf16_to_f32(lhs_bits), rhs, sc, gs, np.arange(N))
+    if out.shape[0]:
+        _check(out, y64, ap, K, out_dtype)
+
+
+def test_gmm_per_call_prepack_equals_prepacked(dev, rng):
+    lhs_bits, rhs, sc, gs = _random_case(rng, [40, 0, 90], 256, 128)
+    a = _run(dev, lhs_bits, rhs, sc, gs, prepacked=True)
+    b = _run(dev, lhs_bits, rhs, sc, gs, prepacked=False)
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+def test_gmm_codes_storage_equals_e2m1_storage(dev, rng):
+    """uint4 codes (the reference's stored format) and raw e2m1 give the same bits."""
+    from dw_tpu_amd import e2m1_to_codes, gmm_wrapper, fp4_weight_to_codes
+    lhs_bits, rhs, sc, gs = _random_case(rng, [17, 50], 128, 64)
+    lhs = bf16_tensor(lhs_bits, dev)
+    w = torch.from_numpy(rhs).to(dev)
+    s = torch.from_numpy(sc).to(dev)
+    g = torch.from_numpy(gs).to(dev)
+    codes = e2m1_to_codes(w)
+    a = gmm_wrapper(lhs, fp4_weight_to_codes(codes, s, rhs_fp4_codes=True), None, None, g, None)
+    b = gmm_wrapper(lhs, codes, s, None, g, None)       # per-call prepack of uint4 codes
+    c = gmm_wrapper(lhs, w.view(torch.float4_e2m1fn_x2), s, None, g, None)  # raw fp4 per call
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    assert torch.equal(a.view(torch.int16), c.view(torch.int16))
+
+
+def test_gmm_group_offset_and_zero_init(dev, rng):
+    sizes = [20, 35, 0, 50, 9]
+    lhs_bits, rhs, sc, gs = _random_case(rng, sizes, 128, 64, extra_rows=7)
+    # local experts: groups 1..3 (rows 20..104); rows outside stay zero
+    out = _run(dev, lhs_bits, rhs[1:4], sc[1:4], gs, group_offset=1, zero_init=True)
+    y64, ap, written = _oracle_cols(bf16_to_f32(lhs_bits), rhs[1:4], sc[1:4], gs, np.arange(64), group_offset=1)
+    assert list(np.nonzero(written)[0]) == list(range(20, 105))
+    y = bf16_to_f32(bf16_bits(out))
+    assert np.all(y[~written] == 0)
+    _check(out, y64, ap, 128, torch.bfloat16, mask=written)
+    # device tensor group_offset, zero_initialize=False leaves other rows untouched
+    from dw_tpu_amd import fp4_weight_to_codes, gmm_v2
+    pw = fp4_weight_to_codes(torch.from_numpy(rhs[1:4]).to(dev), torch.from_numpy(sc[1:4]).to(dev))
+    go = torch.tensor([1], dtype=torch.int32, device=dev)
+    out2 = gmm_v2(bf16_tensor(lhs_bits, dev), pw, torch.from_numpy(gs).to(dev), group_offset=go,
+                  zero_initialize=False)
+    assert torch.equal(out2[20:105].view(torch.int16), out[20:105].view(torch.int16))
+
+
+def test_gmm_repeat_runs_bitwise_identical(dev, rng):
+    lhs_bits, rhs, sc, gs = _random_case(rng, [100, 3, 0, 200], 512, 256)
+    a = _run(dev, lhs_bits, rhs, sc, gs)
+    b = _run(dev, lhs_bits, rhs, sc, gs)
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+def test_gmm_cpu_plumbing_workload_full(dev):
+    from dw_tpu_amd.workloads import make_gmm_workload
+    wl = make_gmm_workload("cpu_plumbing")
+    out = _run(dev, wl.lhs_bits, wl.rhs_e2m1, wl.scale_codes, wl.group_sizes)
+    y64, ap, _ = _oracle_cols(bf16_to_f32(wl.lhs_bits), wl.rhs_e2m1, wl.scale_codes, wl.group_sizes,
+                              np.arange(wl.N))
+    stats = _check(out, y64, ap, wl.K, torch.bfloat16)
+    print("cpu_plumbing", stats)
+    assert stats["rel_fro"] < 4e-3
+
+
+def _sample_rows(gs, rng):
+    starts = np.concatenate([[0], np.cumsum(gs)])
+    rows = []
+    for g in range(len(gs)):
+        if gs[g] == 0:
+            continue
+        a, b = starts[g], starts[g + 1] - 1
+        rows += [a, b, int(rng.integers(a, b + 1))]
+    return np.unique(np.array(rows))
+
+
+@pytest.mark.parametrize("name", ["decode_gate_up", "decode_down", "prefill"])
+def test_gmm_full_size_workloads_sampled(dev, rng, name):
+    from dw_tpu_amd.workloads import make_gmm_workload
+    wl = make_gmm_workload(name)
+    print(name, "groups", wl.group_sizes.tolist(), flush=True)
+    assert (wl.group_sizes == 0).any() or name == "decode_down"
+    out = _run(dev, wl.lhs_bits, wl.rhs_e2m1, wl.scale_codes, wl.group_sizes)
+    rows = _sample_rows(wl.group_sizes, rng)
+    cols = np.unique(np.r_[0, wl.N - 1, rng.integers(0, wl.N, 62)])
+    lhs_f32 = bf16_to_f32(wl.lhs_bits)
+    # oracle on the sampled rows only: build a compact lhs with those rows
+    starts = np.concatenate([[0], np.cumsum(wl.group_sizes)])
+    grp = np.searchsorted(starts, rows, side="right") - 1
+    sub_gs = np.bincount(grp, minlength=wl.E).astype(np.int32)
+    y64, ap, _ = _oracle_cols(lhs_f32[rows], wl.rhs_e2m1, wl.scale_codes, sub_gs, cols)
+    got = out[torch.from_numpy(rows).to(dev)][:, torch.from_numpy(cols).to(dev)]
+    stats = _check(got, y64, ap, wl.K, torch.bfloat16)
+    print(name, stats, flush=True)
+    # size-independent checks on the full output: finite, every row written
+    assert torch.isfinite(out.float()).all()
