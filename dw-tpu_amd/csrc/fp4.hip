@@ -1,17 +1,17 @@
 // FP4 weight formats: e2m1 -> gmm_v2 codes, the decode test hook, and the
 // load-time prepack into the layout the grouped-matmul kernel streams.
 //
-// Prepacked weight layout (per expert e, 32-column block nb, 64-deep K block kb):
-//   weight[((e * N/32 + nb) * K/64 + kb) * 1024 + lane * 16 + j]
-//   lane = 32*h + c (c: column nb*32 + c; h: K half), byte j holds the e2m1
-//   nibbles of k = kb*64 + 32*h + 2*j (low) and k + 1 (high).
+// Prepacked weight layout (per expert e, 16-column block nb, 128-deep K block kb):
+//   weight[((e * N/16 + nb) * K/128 + kb) * 1024 + lane * 16 + j]
+//   lane = 16*q + c (c: column nb*16 + c; q: K quarter), byte j holds the e2m1
+//   nibbles of k = kb*128 + 32*q + 2*j (low) and k + 1 (high).
 // A wave reads one contiguous 1 KiB chunk per (nb, kb): lane l gets the 32
-// consecutive K values of its column, which is both the bf16 MFMA B-operand
-// order used by the gmm kernel (8 K per step, 4 steps) and the gfx950 scaled
-// MFMA fp4 operand order (32 K per lane).
-// Prepacked scales: scale[((e * N/32 + nb) * KB4 + kb / 4) * 256 + lane * 4 + kb % 4]
-//   with KB4 = ceil(K / 256): the e8m0 code of the 32-block (k = kb*64 + 32h)
-//   of column nb*32 + c; bytes past K/64 are zero.
+// consecutive K values of its column in one 32-element scale block.  That is
+// the bf16 MFMA 16x16x32 B-operand order the gmm kernel decodes into (8 K per
+// step, 4 steps) and the gfx950 scaled MFMA 16x16x128 fp4 operand order.
+// Prepacked scales: scale[((e * N/16 + nb) * KB4 + kb / 4) * 256 + lane * 4 + kb % 4]
+//   with KB4 = ceil(K / 512): the e8m0 code of the 32-block (k = kb*128 + 32q)
+//   of column nb*16 + c; bytes past K/128 are zero.
 #include "common.h"
 
 namespace dwm {
@@ -96,30 +96,30 @@ __global__ void fp4_decode_kernel(const uint8_t *packed, int format, int64_t nby
   out[i] = r;
 }
 
-// One thread per (e, nb, kb4, lane): up to 4 K-blocks of 64 (16 B each) and
+// One thread per (e, nb, kb4, lane): up to 4 K-blocks of 128 (16 B each) and
 // one 4-byte scale word.
 __global__ void gmm_fp4_prepack_kernel(const uint8_t *rhs, int format, const void *scale,
                                        int scale_dtype, int64_t E, int64_t K, int64_t N,
                                        uint8_t *wout, uint8_t *sout, int32_t *flags) {
-  const int64_t N32 = N / 32, KB = K / 64, KB4 = (KB + 3) / 4;
+  const int64_t N16 = N / 16, KB = K / 128, KB4 = (KB + 3) / 4;
   int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t total = E * N32 * KB4 * 64;
+  const int64_t total = E * N16 * KB4 * 64;
   if (t >= total) return;
   const int lane = (int)(t & 63);
   int64_t r = t >> 6;
   const int64_t kb4 = r % KB4;
   r /= KB4;
-  const int64_t nb = r % N32;
-  const int64_t e = r / N32;
-  const int h = lane >> 5, c = lane & 31;
-  const int64_t n = nb * 32 + c;
+  const int64_t nb = r % N16;
+  const int64_t e = r / N16;
+  const int q = lane >> 4, c = lane & 15;
+  const int64_t n = nb * 16 + c;
   const int64_t half_n = N / 2;
   bool bad_scale = false, bad_code = false;
   uint32_t sword = 0;
-  for (int q = 0; q < 4; ++q) {
-    const int64_t kb = kb4 * 4 + q;
+  for (int p = 0; p < 4; ++p) {
+    const int64_t kb = kb4 * 4 + p;
     if (kb >= KB) break;
-    const int64_t k0 = kb * 64 + 32 * h;
+    const int64_t k0 = kb * 128 + 32 * q;
     uint32_t code = scale_to_code(scale, scale_dtype, (e * (K / 32) + (k0 >> 5)) * N + n, &bad_scale);
     uint32_t words[4];
 #pragma unroll
@@ -137,11 +137,11 @@ __global__ void gmm_fp4_prepack_kernel(const uint8_t *rhs, int format, const voi
       words[w] = word;
     }
     if (code == 0u) code = 127u;
-    sword |= (code & 0xFFu) << (8 * q);
+    sword |= (code & 0xFFu) << (8 * p);
     u32x4_t v = {words[0], words[1], words[2], words[3]};
-    *(u32x4_t *)(wout + ((e * N32 + nb) * KB + kb) * 1024 + lane * 16) = v;
+    *(u32x4_t *)(wout + ((e * N16 + nb) * KB + kb) * 1024 + lane * 16) = v;
   }
-  *(uint32_t *)(sout + ((e * N32 + nb) * KB4 + kb4) * 256 + lane * 4) = sword;
+  *(uint32_t *)(sout + ((e * N16 + nb) * KB4 + kb4) * 256 + lane * 4) = sword;
   if (bad_scale) atomicOr(flags, 1);
   if (bad_code) atomicOr(flags, 2);
 }
@@ -183,13 +183,13 @@ extern "C" int dwm_gmm_fp4_prepack_size(int64_t E, int64_t K, int64_t N, int64_t
   clear_error();
   DWM_CHECK_ARG(E >= 0 && K > 0 && N > 0, "gmm_fp4_prepack_size: bad sizes E=%lld K=%lld N=%lld",
                 (long long)E, (long long)K, (long long)N);
-  DWM_UNSUPPORTED_IF(K % 64 != 0 || N % 32 != 0,
-                     "gmm_fp4: K %% 64 == 0 and N %% 32 == 0 required (K=%lld N=%lld)",
+  DWM_UNSUPPORTED_IF(K % 128 != 0 || N % 16 != 0,
+                     "gmm_fp4: K %% 128 == 0 and N %% 16 == 0 required (K=%lld N=%lld)",
                      (long long)K, (long long)N);
   DWM_CHECK_ARG(weight_bytes && scale_bytes, "gmm_fp4_prepack_size: null output pointer");
-  const int64_t KB4 = (K / 64 + 3) / 4;
+  const int64_t KB4 = (K / 128 + 3) / 4;
   *weight_bytes = E * K * N / 2;
-  *scale_bytes = E * (N / 32) * KB4 * 256;
+  *scale_bytes = E * (N / 16) * KB4 * 256;
   return DWM_OK;
 }
 
@@ -205,7 +205,7 @@ extern "C" int dwm_gmm_fp4_prepack(const uint8_t *rhs, int format, const void *s
                 "gmm_fp4_prepack: bad scale dtype %d", scale_dtype);
   if (E == 0) return DWM_OK;
   DWM_CHECK_ARG(rhs && scale && weight_out && scale_out && flags, "gmm_fp4_prepack: null pointer");
-  const int64_t total = E * (N / 32) * ((K / 64 + 3) / 4) * 64;
+  const int64_t total = E * (N / 16) * ((K / 128 + 3) / 4) * 64;
   const int64_t blocks = (total + 255) / 256;
   DWM_CHECK_ARG(blocks < (1ll << 31), "gmm_fp4_prepack: too large");
   hipLaunchKernelGGL(gmm_fp4_prepack_kernel, dim3((unsigned)blocks), dim3(256), 0,

@@ -77,7 +77,7 @@ int dwm_fp4_decode(const uint8_t *packed, int format, int64_t n, const uint8_t *
 
 /* Bytes of the load-time weight layout produced by dwm_gmm_fp4_prepack for
  * E experts of a [K, N] fp4 matrix with 32-element e8m0 block scales along K.
- * Requires K % 64 == 0 and N % 32 == 0. */
+ * Requires K % 128 == 0 and N % 16 == 0. */
 int dwm_gmm_fp4_prepack_size(int64_t E, int64_t K, int64_t N, int64_t *weight_bytes,
                              int64_t *scale_bytes);
 
@@ -115,7 +115,7 @@ int dwm_gmm_fp4_prepack(const uint8_t *rhs, int format, const void *scale, int s
  *   group_offset: device int32[1] or NULL (= 0).
  *   out_dtype:    DWM_BF16 or DWM_F32 (the MOE_F32_REDUCE variant,
  *                 patches/tpu-inference-ext/0106-...:243-250).
- * Requires K % 64 == 0, N % 32 == 0, num_groups <= 1024. */
+ * Requires K % 128 == 0, N % 16 == 0, num_groups <= 1024. */
 int dwm_gmm_fp4(const uint16_t *lhs, int64_t M, int64_t K, const uint8_t *weight,
                 const uint8_t *scale, const int32_t *group_sizes, int num_groups,
                 const int32_t *group_offset, int64_t E_local, int64_t N, void *out,

@@ -43,7 +43,7 @@ def _rc(name, *args):
 def test_gmm_argument_checks_need_no_gpu():
     null = None
     # K not a multiple of 64 -> unsupported (fail-closed fallback)
-    rc, msg = _rc("dwm_gmm_fp4", null, 8, 100, null, null, null, 4, null, 4, 64, null, _lib.BF16, 0, null)
+    rc, msg = _rc("dwm_gmm_fp4", null, 8, 192, null, null, null, 4, null, 4, 64, null, _lib.BF16, 0, null)
     assert rc == _lib.ERR_UNSUPPORTED and "K" in msg
     rc, msg = _rc("dwm_gmm_fp4", null, 8, 128, null, null, null, 4, null, 4, 64, null, 7, 0, null)
     assert rc == _lib.ERR_INVALID and "dtype" in msg
@@ -60,8 +60,8 @@ def test_prepack_size_query():
     rc, _ = _rc("dwm_gmm_fp4_prepack_size", 32, 7168, 4096, ctypes.byref(wb), ctypes.byref(sb))
     assert rc == _lib.OK
     assert wb.value == 32 * 7168 * 4096 // 2
-    assert sb.value == 32 * (4096 // 32) * ((7168 // 64 + 3) // 4) * 256
-    rc, _ = _rc("dwm_gmm_fp4_prepack_size", 1, 96, 64, ctypes.byref(wb), ctypes.byref(sb))
+    assert sb.value == 32 * (4096 // 16) * ((7168 // 128 + 3) // 4) * 256
+    rc, _ = _rc("dwm_gmm_fp4_prepack_size", 1, 192, 64, ctypes.byref(wb), ctypes.byref(sb))
     assert rc == _lib.ERR_UNSUPPORTED
 
 

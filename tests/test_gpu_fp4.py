@@ -64,35 +64,35 @@ def test_prepack_layout_matches_definition(dev, rng):
     """Every prepacked byte equals the documented layout of the reference
     [E, K, N/2] weight, and every scale byte its [E, K/32, N] code."""
     from dw_tpu_amd import prepack_fp4
-    E, K, N = 2, 320, 96  # K/64 = 5 (partial last scale word), N/32 = 3
+    E, K, N = 2, 640, 48  # K/128 = 5 (partial last scale word), N/16 = 3
     rhs = rng.integers(0, 256, (E, K, N // 2), dtype=np.uint8)
     sc = rng.integers(1, 255, (E, K // 32, 1, N), dtype=np.uint8)
     w = prepack_fp4(torch.from_numpy(rhs).to(dev), torch.from_numpy(sc).to(dev))
-    wp = w.weight.cpu().numpy().reshape(E, N // 32, K // 64, 64, 16)
-    sp = w.scale.cpu().numpy().reshape(E, N // 32, 2, 64, 4)
+    wp = w.weight.cpu().numpy().reshape(E, N // 16, K // 128, 64, 16)
+    sp = w.scale.cpu().numpy().reshape(E, N // 16, 2, 64, 4)
     nib = fp4.unpack_nibbles(rhs)  # [E, K, N]
     nib = np.where(nib == 8, 0, nib)  # -0 -> +0
     for e in range(E):
-        for nb in range(N // 32):
-            for kb in range(K // 64):
+        for nb in range(N // 16):
+            for kb in range(K // 128):
                 for lane in range(64):
-                    h, c = divmod(lane, 32)
-                    n = nb * 32 + c
-                    ks = kb * 64 + 32 * h + np.arange(32)
+                    q, c = divmod(lane, 16)
+                    n = nb * 16 + c
+                    ks = kb * 128 + 32 * q + np.arange(32)
                     want = fp4.pack_nibbles(nib[e, ks, n][None])[0]
                     assert np.array_equal(wp[e, nb, kb, lane], want)
-                    assert sp[e, nb, kb // 4, lane, kb % 4] == sc[e, (kb * 64 + 32 * h) // 32, 0, n]
-    assert np.all(sp[:, :, 1, :, 1:] == 0)  # padding past K/64
+                    assert sp[e, nb, kb // 4, lane, kb % 4] == sc[e, (kb * 128 + 32 * q) // 32, 0, n]
+    assert np.all(sp[:, :, 1, :, 1:] == 0)  # padding past K/128
 
 
 def test_prepack_rejects_bad_scales(dev):
     from dw_tpu_amd import prepack_fp4
-    rhs = torch.zeros((1, 64, 16), dtype=torch.uint8, device=dev)
-    bad = torch.full((1, 2, 1, 32), 3.0, dtype=torch.float32, device=dev)
+    rhs = torch.zeros((1, 128, 16), dtype=torch.uint8, device=dev)
+    bad = torch.full((1, 4, 1, 32), 3.0, dtype=torch.float32, device=dev)
     with pytest.raises(ValueError, match="power of two"):
         prepack_fp4(rhs, bad)
-    ok = torch.full((1, 2, 1, 32), 0.25, dtype=torch.bfloat16, device=dev)
+    ok = torch.full((1, 4, 1, 32), 0.25, dtype=torch.bfloat16, device=dev)
     prepack_fp4(rhs, ok)
-    codes = torch.full((1, 64, 16), 0x88, dtype=torch.uint8, device=dev)
+    codes = torch.full((1, 128, 16), 0x88, dtype=torch.uint8, device=dev)
     with pytest.raises(ValueError, match="code 8"):
-        prepack_fp4(codes, torch.full((1, 2, 1, 32), 127, dtype=torch.uint8, device=dev), rhs_fp4_codes=True)
+        prepack_fp4(codes, torch.full((1, 4, 1, 32), 127, dtype=torch.uint8, device=dev), rhs_fp4_codes=True)
