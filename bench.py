@@ -116,30 +116,65 @@ def bench_gmm(name, dev, steps, warmup):
 
 
 def bench_dispatch_combine(dev, steps, warmup):
-    """decode_down routing: dispatch indices, row gather of hidden [512, 2048]
-    and the combine of the down-projection output [4096, 7168] -> [512, 7168]."""
+    """decode_down routing through the C ABI with preallocated outputs:
+    dispatch indices for 512 tokens x top-8 over 32 experts, the row gather
+    of hidden [512, 2048] into [4096, 2048], and the combine of the
+    down-projection output [4096, 7168] back to [512, 7168]."""
     import numpy as np
     import torch
-    from dw_tpu_amd import fast_combine, moe_dispatch, row_gather
+    from dw_tpu_amd import _lib
     from dw_tpu_amd.workloads import make_gmm_workload
-    wl = make_gmm_workload("decode_down")
+    lib = _lib.load()
+    wl = make_gmm_workload("decode_down", with_data=False)
+    n = wl.M
+    i32 = dict(dtype=torch.int32, device=dev)
     ids = torch.from_numpy(wl.topk_ids).to(dev)
+    perm, tok, rev = (torch.empty(n, **i32) for _ in range(3))
+    gs, goff, flags = torch.empty(wl.E, **i32), torch.empty(wl.E + 1, **i32), torch.zeros(1, **i32)
+    wsb = ctypes.c_int64()
+    _lib.call("dwm_moe_dispatch_workspace_size", n, wl.E, ctypes.byref(wsb))
+    ws = torch.empty(wsb.value, dtype=torch.uint8, device=dev)
+    st = _lib.stream_handle(dev)
+    P = _lib.ptr
+    disp_args = (P(ids), wl.T, wl.topk, wl.E, P(perm), P(tok), P(rev), P(gs), P(goff), P(flags), P(ws), st)
     rng = np.random.Generator(np.random.PCG64(11))
     hidden = torch.from_numpy(rng.standard_normal((wl.T, wl.K), dtype=np.float32)).to(torch.bfloat16).to(dev)
-    y = torch.from_numpy(rng.standard_normal((wl.M, wl.N), dtype=np.float32)).to(torch.bfloat16).to(dev)
+    x = torch.empty((n, wl.K), dtype=torch.bfloat16, device=dev)
+    y = torch.from_numpy(rng.standard_normal((n, wl.N), dtype=np.float32)).to(torch.bfloat16).to(dev)
     w = torch.from_numpy(wl.topk_weights).to(dev)
-    d = moe_dispatch(ids, wl.E)
+    out = torch.empty((wl.T, wl.N), dtype=torch.bfloat16, device=dev)
+    gather_args = (P(hidden), wl.T, wl.K * 2, P(tok), n, P(x), st)
+    comb_args = (P(y), _lib.BF16, n, wl.N, P(rev), P(w), _lib.F32, wl.T, wl.topk, P(out), _lib.BF16, st)
+
+    def run(fn, args):
+        rc = fn(*args)
+        if rc:
+            raise RuntimeError(lib.dwm_last_error().decode())
+
     res = {}
-    ms = time_steps(lambda i: moe_dispatch(ids, wl.E), steps, warmup)
-    res["dispatch"] = {"ms": round(ms, 5), "ids": wl.M, "experts": wl.E}
-    ms = time_steps(lambda i: row_gather(hidden, d.token_indices_sorted), steps, warmup)
-    gb = 2 * wl.M * wl.K * 2
-    res["row_gather"] = {"ms": round(ms, 5), "GB_s": round(gb / (ms * 1e-3) / 1e9, 1), "rows": wl.M, "H": wl.K}
-    ms = time_steps(lambda i: fast_combine(y, d.topk_argsort_revert_indices, w, wl.topk), steps, warmup)
-    gb = wl.M * wl.N * 2 + wl.T * wl.N * 2 + wl.M * 8
+    ms = time_steps(lambda i: run(lib.dwm_moe_dispatch, disp_args), steps, warmup)
+    res["dispatch"] = {"ms": round(ms, 5), "ids": n, "experts": wl.E, "kernels": 3}
+    ms = time_steps(lambda i: run(lib.dwm_row_gather, gather_args), steps, warmup)
+    gb = 2 * n * wl.K * 2 + n * 4
+    res["row_gather"] = {"ms": round(ms, 5), "GB_s": round(gb / (ms * 1e-3) / 1e9, 1), "rows": n, "H": wl.K,
+                         "hbm_frac": round(gb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    ms = time_steps(lambda i: run(lib.dwm_moe_combine, comb_args), steps, warmup)
+    gb = n * wl.N * 2 + wl.T * wl.N * 2 + n * 8
     res["combine"] = {"ms": round(ms, 5), "GB_s": round(gb / (ms * 1e-3) / 1e9, 1), "T": wl.T, "topk": wl.topk,
-                      "H": wl.N}
+                      "H": wl.N, "hbm_frac": round(gb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
     return res
+
+
+def profiled_traffic(name="gmm_fp4_decode_gate_up.md"):
+    """HBM bytes per launch of the main kernel from the committed rocprofv3
+    counter summary (FETCH_SIZE + WRITE_SIZE, copy-calibrated), or None."""
+    import re
+    try:
+        text = open(os.path.join(ROOT, "profiles", name)).read()
+    except OSError:
+        return None
+    m = re.search(r"^traffic_bytes:\s*(\d+)", text, re.M)
+    return int(m.group(1)) if m else None
 
 
 def cpu_baseline(wl, budget_s):
@@ -179,7 +214,10 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--extra", choices=["all", "none"], default="all")
-    ap.add_argument("--cpu-budget", type=float, default=15.0)
+    ap.add_argument("--cpu-budget", type=float, default=15.0,
+                    help="seconds of CPU-baseline work (0 skips it)")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="only run a plain 1 GiB device-to-device copy (byte-counter calibration)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -189,6 +227,15 @@ def main():
 
     import torch
     dev = torch.device("cuda:0")
+    if args.calib_copy:
+        src = torch.empty(2 ** 30, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log("calib copy: 3 x 1 GiB device-to-device copies done")
+        return
     log("bench: decode_gate_up gmm")
     wl, b, ms = bench_gmm("decode_gate_up", dev, args.steps, args.warmup)
     main_res = gmm_result(wl, ms)
@@ -204,8 +251,10 @@ def main():
         torch.cuda.empty_cache()
         log("bench: dispatch / gather / combine")
         extra.update(bench_dispatch_combine(dev, args.steps, args.warmup))
-    log("bench: cpu baseline")
-    cpu = cpu_baseline(wl, args.cpu_budget)
+    cpu = None
+    if args.cpu_budget > 0:
+        log("bench: cpu baseline")
+        cpu = cpu_baseline(wl, args.cpu_budget)
     line = {
         "metric": METRIC,
         "value": main_res["GB_s"],
@@ -225,7 +274,7 @@ def main():
                    "TFLOP_s": main_res["TFLOP_s"], "mfma_bf16_frac": main_res["mfma_bf16_frac"],
                    "bytes_per_step": main_res["bytes"], "flops_per_step": main_res["flops"]},
         "roofline": {"bound": "hbm", "achieved": main_res["GB_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": main_res["hbm_frac"], "traffic": None},
+                     "frac": main_res["hbm_frac"], "traffic": profiled_traffic()},
         "cpu_baseline": cpu,
         "extra": extra,
     }
