@@ -165,6 +165,61 @@ def bench_dispatch_combine(dev, steps, warmup):
     return res
 
 
+def bench_dense(dev, steps, warmup, ms_list=(1, 16, 128, 1024, 4096)):
+    """Dense FP8 GEMM (K=7168, N=4096) at each M, W8A16 and W8A8, through
+    the C ABI with prepacked weights; 10 rotated weight copies (~290 MB) keep
+    the small-M weight stream out of the Infinity Cache."""
+    import torch
+    from dw_tpu_amd import _lib
+    from dw_tpu_amd.dense_fp8 import prepack_fp8
+    from dw_tpu_amd.workloads import make_dense_workload
+    lib = _lib.load()
+    st = _lib.stream_handle(dev)
+    P = _lib.ptr
+    res = {}
+    for m in ms_list:
+        wl = make_dense_workload(m)
+        k, n = wl.K, wl.N
+        copies = 10 if m <= 128 else 1
+        w = torch.from_numpy(wl.wq).to(dev)
+        pws = [prepack_fp8(w) for _ in range(copies)]
+        x = _to_dev_bf16(wl.x_bits, dev)
+        xq = torch.from_numpy(wl.xq).to(dev)
+        sx = torch.from_numpy(wl.sx).to(dev)
+        s16 = torch.from_numpy(wl.s_w8a16.reshape(k // 128, n)).to(dev)
+        sw = torch.from_numpy(wl.sw).to(dev)
+        out = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+        wsb = ctypes.c_int64()
+        _lib.call("dwm_dense_fp8_workspace_size", m, k, n, ctypes.byref(wsb))
+        ws = torch.empty(max(1, wsb.value), dtype=torch.uint8, device=dev)
+
+        def run16(i):
+            rc = lib.dwm_dense_fp8_w8a16(P(x), m, k, n, P(pws[i % copies].weight), P(s16), P(out), P(ws),
+                                         wsb.value, st)
+            if rc:
+                raise RuntimeError(lib.dwm_last_error().decode())
+
+        def run8(i):
+            rc = lib.dwm_dense_fp8_w8a8(P(xq), P(sx), m, k, n, P(pws[i % copies].weight), P(sw), P(out), P(ws),
+                                        wsb.value, st)
+            if rc:
+                raise RuntimeError(lib.dwm_last_error().decode())
+
+        fl = 2 * m * k * n
+        for tag, fn, xbytes in (("w8a16", run16, m * k * 2 + (k // 128) * n * 4),
+                                ("w8a8", run8, m * k + m * (k // 128) * 4 + (k // 128) * (n // 128) * 4)):
+            ms = time_steps(fn, steps, warmup)
+            bts = k * n + xbytes + m * n * 2
+            gbs = bts / (ms * 1e-3) / 1e9
+            tf = fl / (ms * 1e-3) / 1e12
+            res[f"dense_{tag}_M{m}"] = {"ms": round(ms, 5), "GB_s": round(gbs, 1), "TFLOP_s": round(tf, 2),
+                                        "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+                                        "mfma_bf16_frac": round(tf / BF16_PEAK_TFLOPS, 4), "bytes": bts, "flops": fl}
+        del pws, w
+        torch.cuda.empty_cache()
+    return res
+
+
 def profiled_traffic(name="gmm_fp4_decode_gate_up.md"):
     """HBM bytes per launch of the main kernel from the committed rocprofv3
     counter summary (FETCH_SIZE + WRITE_SIZE, copy-calibrated), or None."""
@@ -251,6 +306,8 @@ def main():
         torch.cuda.empty_cache()
         log("bench: dispatch / gather / combine")
         extra.update(bench_dispatch_combine(dev, args.steps, args.warmup))
+        log("bench: dense fp8")
+        extra.update(bench_dense(dev, args.steps, args.warmup))
     cpu = None
     if args.cpu_budget > 0:
         log("bench: cpu baseline")

@@ -1,2 +1,358 @@
-// Dense FP8 block-quantized GEMM (placeholder translation unit; kernels follow).
+// Dense FP8 block-quantised GEMM on gfx950.
+//
+// W8A16 -- the reference dense_fp8.matmul "native" semantics
+// (kernels/tpu_inference/kernels/experimental/dense_fp8.py:23-59): for each
+// 128-row K block kb, part = dot(x_bf16[:, kb], w_e4m3[kb, :]) in f32, then
+// acc += part * s[kb, n] (f32), stored as bf16.
+// W8A8 -- e4m3 activations with per-(token, 128-K) f32 scales sx and e4m3
+// weights with 128x128 block f32 scales sw:
+// acc += part * (sx[m, kb] * sw[kb, n / 128]).
+//
+// Both run on bf16 MFMA 16x16x32: e4m3 -> bf16 is exact (3 mantissa bits,
+// exponents inside bf16's range), so every product equals the fp8 product and
+// the 128-K partial is an f32 sum of exact products.
+//
+// Prepacked weight layout (load time, dwm_dense_fp8_prepack):
+//   w[(nb * K/128 + kb) * 2048 + lane * 32 + j], lane = 16*q + c,
+//   byte j = e4m3 code of k = 128*kb + 32*q + j, column n = 16*nb + c.
+// A wave streams one contiguous 2 KiB chunk per (16 columns, 128 K) with two
+// 16 B loads per lane; lane (c, q) holds 32 consecutive K of one column, the
+// MFMA 16x16x32 B-operand order (8 K per step, 4 steps).
+//
+// Small M: the K loop is split over `ksplit` blocks per tile; each writes an
+// f32 partial [ks][M][N] to the workspace and dense_fp8_reduce_kernel sums
+// the splits in order and rounds once (deterministic).
 #include "common.h"
+
+namespace dwm {
+
+constexpr int kDenseThreads = 256;
+constexpr int kDLdsRow = 136;  // bf16 per LDS row: 128 + 8 pad
+
+// Two e4m3 codes (bytes 0,1 or 2,3 of src) -> packed bf16x2, exact.
+template <bool HI>
+__device__ __forceinline__ uint32_t cvt_fp8x2_bf16(uint32_t src) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(src, 1.0f, HI));
+}
+
+__global__ void dense_fp8_prepack_kernel(const uint8_t *w, int64_t K, int64_t N, uint8_t *out) {
+  // one thread per (nb, kb, lane): 32 bytes
+  const int64_t KB = K / 128, N16 = N / 16;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= N16 * KB * 64) return;
+  const int lane = (int)(t & 63);
+  const int64_t r = t >> 6;
+  const int64_t kb = r % KB, nb = r / KB;
+  const int q = lane >> 4, c = lane & 15;
+  const int64_t n = nb * 16 + c;
+  uint32_t words[8];
+#pragma unroll
+  for (int wd = 0; wd < 8; ++wd) {
+    uint32_t v = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t k = kb * 128 + 32 * q + 4 * wd + i;
+      v |= (uint32_t)w[k * N + n] << (8 * i);
+    }
+    words[wd] = v;
+  }
+  u32x4_t *dst = (u32x4_t *)(out + (nb * KB + kb) * 2048 + lane * 32);
+  dst[0] = u32x4_t{words[0], words[1], words[2], words[3]};
+  dst[1] = u32x4_t{words[4], words[5], words[6], words[7]};
+}
+
+// A8: activations are e4m3 codes with scales sx [M, K/128]; else bf16.
+template <int MB, int NBW, bool A8>
+__global__ __launch_bounds__(kDenseThreads) void dense_fp8_kernel(
+    const void *__restrict__ xin, const float *__restrict__ sx, int64_t M, int K, int N,
+    const uint8_t *__restrict__ wpk, const float *__restrict__ sw, int sw_ld, int ksplit,
+    uint16_t *__restrict__ out, float *__restrict__ partial) {
+  constexpr int MT = 16 * MB;
+  __shared__ __attribute__((aligned(16))) uint16_t s_a[2][MT * kDLdsRow];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int KB = K >> 7, N16 = N >> 4;
+  const int64_t row0 = (int64_t)blockIdx.y * MT;
+  const int rows = (int)min((int64_t)MT, M - row0);
+  const int act_mb = (rows + 15) >> 4;
+  const int ks = blockIdx.z;
+  const int kb_per = (KB + ksplit - 1) / ksplit;
+  const int kb_begin = ks * kb_per;
+  const int kb_end = min(KB, kb_begin + kb_per);
+  const int nb0 = blockIdx.x * (NBW * 4) + wave * NBW;
+
+  const uint8_t *wp[NBW];
+  bool nvalid[NBW];
+#pragma unroll
+  for (int j = 0; j < NBW; ++j) {
+    nvalid[j] = nb0 + j < N16;
+    wp[j] = wpk + (int64_t)(nvalid[j] ? nb0 + j : 0) * KB * 2048 + lane * 32;
+  }
+  f32x4_t acc[MB][NBW];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int j = 0; j < NBW; ++j) acc[mb][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  // lhs staging: 16 rows per i, 16 chunks of 8 bf16 per row (A8: 16 chunks
+  // of 8 e4m3 bytes, widened to bf16 on the way into LDS).
+  const int srow = tid >> 4, scol = (tid & 15) * 8;
+  u32x4_t areg[MB];
+  uint32_t areg8[MB][2];
+  auto load_a = [&](int kb) {
+#pragma unroll
+    for (int i = 0; i < MB; ++i) {
+      if (i < act_mb) {
+        int64_t grow = row0 + 16 * i + srow;
+        if (grow >= M) grow = M - 1;
+        if (A8) {
+          const uint32_t *p = (const uint32_t *)((const uint8_t *)xin + grow * K + (int64_t)kb * 128 + scol);
+          areg8[i][0] = p[0];
+          areg8[i][1] = p[1];
+        } else {
+          areg[i] = *(const u32x4_t *)((const uint16_t *)xin + grow * K + (int64_t)kb * 128 + scol);
+        }
+      }
+    }
+  };
+  auto store_a = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < MB; ++i) {
+      if (i < act_mb) {
+        u32x4_t v;
+        if (A8) {
+          v[0] = cvt_fp8x2_bf16<false>(areg8[i][0]);
+          v[1] = cvt_fp8x2_bf16<true>(areg8[i][0]);
+          v[2] = cvt_fp8x2_bf16<false>(areg8[i][1]);
+          v[3] = cvt_fp8x2_bf16<true>(areg8[i][1]);
+        } else {
+          v = areg[i];
+        }
+        *(u32x4_t *)(&s_a[buf][(16 * i + srow) * kDLdsRow + scol]) = v;
+      }
+    }
+  };
+
+  u32x4_t wlo[NBW], whi[NBW], nlo[NBW], nhi[NBW];
+  if (kb_begin < kb_end) {
+    load_a(kb_begin);
+#pragma unroll
+    for (int j = 0; j < NBW; ++j) {
+      const u32x4_t *p = (const u32x4_t *)(wp[j] + (int64_t)kb_begin * 2048);
+      wlo[j] = p[0];
+      whi[j] = p[1];
+    }
+    store_a(0);
+  }
+  __syncthreads();
+
+  const int arow = lane & 15, acol = 32 * (lane >> 4), qrow = 4 * (lane >> 4);
+  for (int kb = kb_begin; kb < kb_end; ++kb) {
+    const int buf = (kb - kb_begin) & 1;
+    const bool more = kb + 1 < kb_end;
+    if (more) {
+      load_a(kb + 1);
+#pragma unroll
+      for (int j = 0; j < NBW; ++j) {
+        const u32x4_t *p = (const u32x4_t *)(wp[j] + (int64_t)(kb + 1) * 2048);
+        nlo[j] = p[0];
+        nhi[j] = p[1];
+      }
+    }
+    f32x4_t part[MB][NBW];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int j = 0; j < NBW; ++j) part[mb][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    const uint16_t *abase = &s_a[buf][arow * kDLdsRow + acol];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      u32x4_t bfrag[NBW];
+#pragma unroll
+      for (int j = 0; j < NBW; ++j) {
+        // 8 e4m3 codes of this step: words 2s, 2s+1 of the lane's 32 bytes
+        const uint32_t w0 = s < 2 ? wlo[j][2 * s] : whi[j][2 * s - 4];
+        const uint32_t w1 = s < 2 ? wlo[j][2 * s + 1] : whi[j][2 * s - 3];
+        bfrag[j][0] = cvt_fp8x2_bf16<false>(w0);
+        bfrag[j][1] = cvt_fp8x2_bf16<true>(w0);
+        bfrag[j][2] = cvt_fp8x2_bf16<false>(w1);
+        bfrag[j][3] = cvt_fp8x2_bf16<true>(w1);
+      }
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        if (mb < act_mb) {
+          const u32x4_t a = *(const u32x4_t *)(abase + mb * 16 * kDLdsRow + 8 * s);
+#pragma unroll
+          for (int j = 0; j < NBW; ++j)
+            part[mb][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                __builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, bfrag[j]), part[mb][j], 0, 0, 0);
+        }
+      }
+    }
+    // acc += part * scale (f32 multiply, then f32 add)
+#pragma unroll
+    for (int j = 0; j < NBW; ++j) {
+      const int64_t col = (int64_t)(nvalid[j] ? nb0 + j : 0) * 16 + (lane & 15);
+      const float wscale = A8 ? sw[(int64_t)kb * sw_ld + (col >> 7)] : sw[(int64_t)kb * sw_ld + col];
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        if (mb < act_mb) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            float f = wscale;
+            if (A8) {
+              int64_t m = row0 + mb * 16 + qrow + r;
+              if (m >= M) m = M - 1;
+              f = sx[m * KB + kb] * wscale;
+            }
+            acc[mb][j][r] = acc[mb][j][r] + part[mb][j][r] * f;
+          }
+        }
+      }
+    }
+    if (more) {
+      store_a(buf ^ 1);
+#pragma unroll
+      for (int j = 0; j < NBW; ++j) {
+        wlo[j] = nlo[j];
+        whi[j] = nhi[j];
+      }
+    }
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    if (mb >= act_mb) continue;
+#pragma unroll
+    for (int j = 0; j < NBW; ++j) {
+      if (!nvalid[j]) continue;
+      const int64_t col = (int64_t)(nb0 + j) * 16 + (lane & 15);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int lrow = mb * 16 + qrow + r;
+        if (lrow < rows) {
+          const int64_t o = (row0 + lrow) * N + col;
+          if (partial) partial[(int64_t)ks * M * N + o] = acc[mb][j][r];
+          else out[o] = f32_to_bf16_bits(acc[mb][j][r]);
+        }
+      }
+    }
+  }
+}
+
+// out = bf16(sum_{ks} partial[ks]) in split order.
+__global__ void dense_fp8_reduce_kernel(const float *partial, int ksplit, int64_t MN, uint16_t *out) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < MN; i += (int64_t)gridDim.x * blockDim.x) {
+    float s = partial[i];
+    for (int k = 1; k < ksplit; ++k) s = s + partial[(int64_t)k * MN + i];
+    out[i] = f32_to_bf16_bits(s);
+  }
+}
+
+struct DensePlan {
+  int mb, nbw, ksplit;
+};
+
+static DensePlan dense_plan(int64_t M, int64_t K, int64_t N) {
+  DensePlan p;
+  if (M <= 16) p = {1, 1, 0};
+  else if (M <= 64) p = {4, 2, 0};
+  else p = {8, 2, 0};
+  const int64_t tiles = ((N / 16 + p.nbw * 4 - 1) / (p.nbw * 4)) * ((M + 16 * p.mb - 1) / (16 * p.mb));
+  const int64_t KB = K / 128;
+  int ks = 1;
+  while (tiles * ks < 512 && ks * 2 <= KB && ks < 16) ks *= 2;  // fill the 256 CUs twice over
+  p.ksplit = ks;
+  return p;
+}
+
+template <int MB, int NBW, bool A8>
+static void launch_dense(const void *x, const float *sx, int64_t M, int64_t K, int64_t N, const uint8_t *w,
+                         const float *sw, int sw_ld, int ksplit, uint16_t *out, float *partial, hipStream_t st) {
+  const int64_t NT = 64 * NBW, MT = 16 * MB;
+  dim3 grid((unsigned)((N + NT - 1) / NT), (unsigned)((M + MT - 1) / MT), (unsigned)ksplit);
+  hipLaunchKernelGGL((dense_fp8_kernel<MB, NBW, A8>), grid, dim3(kDenseThreads), 0, st, x, sx, M, (int)K, (int)N,
+                     w, sw, sw_ld, ksplit, out, partial);
+}
+
+template <bool A8>
+static int run_dense(const void *x, const float *sx, int64_t M, int64_t K, int64_t N, const uint8_t *w,
+                     const float *sw, int sw_ld, uint16_t *out, void *workspace, int64_t workspace_bytes,
+                     hipStream_t st) {
+  const DensePlan p = dense_plan(M, K, N);
+  float *partial = nullptr;
+  if (p.ksplit > 1) {
+    const int64_t need = (int64_t)p.ksplit * M * N * 4;
+    DWM_CHECK_ARG(workspace && workspace_bytes >= need, "dense_fp8: workspace of %lld bytes needed", (long long)need);
+    partial = (float *)workspace;
+  }
+  DWM_UNSUPPORTED_IF((M + 16 * p.mb - 1) / (16 * p.mb) > 65535, "dense_fp8: M too large");
+  if (p.mb == 1) launch_dense<1, 1, A8>(x, sx, M, K, N, w, sw, sw_ld, p.ksplit, out, partial, st);
+  else if (p.mb == 4) launch_dense<4, 2, A8>(x, sx, M, K, N, w, sw, sw_ld, p.ksplit, out, partial, st);
+  else launch_dense<8, 2, A8>(x, sx, M, K, N, w, sw, sw_ld, p.ksplit, out, partial, st);
+  int rc = launch_status("dense_fp8");
+  if (rc != DWM_OK || p.ksplit == 1) return rc;
+  const int64_t MN = M * N;
+  const int64_t blocks = (MN + 255) / 256 < 4096 ? (MN + 255) / 256 : 4096;
+  hipLaunchKernelGGL(dense_fp8_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, st, partial, p.ksplit, MN, out);
+  return launch_status("dense_fp8 reduce");
+}
+
+static int check_dense(int64_t M, int64_t K, int64_t N) {
+  DWM_CHECK_ARG(M >= 0 && K > 0 && N > 0, "dense_fp8: bad sizes M=%lld K=%lld N=%lld", (long long)M, (long long)K,
+                (long long)N);
+  DWM_UNSUPPORTED_IF(K % 128 != 0 || N % 16 != 0, "dense_fp8: K %% 128 == 0 and N %% 16 == 0 required");
+  DWM_UNSUPPORTED_IF(K > (1 << 30) || N > (1 << 30), "dense_fp8: K, N must be < 2^30");
+  return DWM_OK;
+}
+
+}  // namespace dwm
+
+using namespace dwm;
+
+extern "C" int dwm_dense_fp8_prepack(const uint8_t *w, int64_t K, int64_t N, uint8_t *out, void *stream) {
+  clear_error();
+  int rc = check_dense(1, K, N);
+  if (rc != DWM_OK) return rc;
+  DWM_CHECK_ARG(w && out, "dense_fp8_prepack: null pointer");
+  DWM_CHECK_ARG((uintptr_t)out % 16 == 0, "dense_fp8_prepack: output must be 16-byte aligned");
+  const int64_t total = (N / 16) * (K / 128) * 64;
+  hipLaunchKernelGGL(dense_fp8_prepack_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                     as_stream(stream), w, K, N, out);
+  return launch_status("dense_fp8_prepack");
+}
+
+extern "C" int dwm_dense_fp8_workspace_size(int64_t M, int64_t K, int64_t N, int64_t *bytes) {
+  clear_error();
+  int rc = check_dense(M, K, N);
+  if (rc != DWM_OK) return rc;
+  DWM_CHECK_ARG(bytes, "dense_fp8_workspace_size: null pointer");
+  const DensePlan p = dense_plan(M, K, N);
+  *bytes = p.ksplit > 1 ? (int64_t)p.ksplit * M * N * 4 : 0;
+  return DWM_OK;
+}
+
+extern "C" int dwm_dense_fp8_w8a16(const uint16_t *x, int64_t M, int64_t K, int64_t N, const uint8_t *w,
+                                   const float *s, uint16_t *out, void *workspace, int64_t workspace_bytes,
+                                   void *stream) {
+  clear_error();
+  int rc = check_dense(M, K, N);
+  if (rc != DWM_OK) return rc;
+  if (M == 0) return DWM_OK;
+  DWM_CHECK_ARG(x && w && s && out, "dense_fp8_w8a16: null pointer");
+  DWM_CHECK_ARG((uintptr_t)x % 16 == 0 && (uintptr_t)w % 16 == 0, "dense_fp8_w8a16: x and w must be 16-byte aligned");
+  return run_dense<false>(x, nullptr, M, K, N, w, s, (int)N, out, workspace, workspace_bytes, as_stream(stream));
+}
+
+extern "C" int dwm_dense_fp8_w8a8(const uint8_t *xq, const float *sx, int64_t M, int64_t K, int64_t N,
+                                  const uint8_t *w, const float *sw, uint16_t *out, void *workspace,
+                                  int64_t workspace_bytes, void *stream) {
+  clear_error();
+  int rc = check_dense(M, K, N);
+  if (rc != DWM_OK) return rc;
+  if (M == 0) return DWM_OK;
+  DWM_UNSUPPORTED_IF(N % 128 != 0, "dense_fp8_w8a8: N %% 128 == 0 required (128x128 weight blocks)");
+  DWM_CHECK_ARG(xq && sx && w && sw && out, "dense_fp8_w8a8: null pointer");
+  DWM_CHECK_ARG((uintptr_t)xq % 16 == 0 && (uintptr_t)w % 16 == 0, "dense_fp8_w8a8: xq and w must be 16-byte aligned");
+  return run_dense<true>(xq, sx, M, K, N, w, sw, (int)(N / 128), out, workspace, workspace_bytes, as_stream(stream));
+}

@@ -142,16 +142,18 @@ def _e4m3_codes(x: np.ndarray) -> np.ndarray:
 
 def make_dense_workload(M: int, K: int = DENSE_FP8["K"], N: int = DENSE_FP8["N"],
                         seed: int = DENSE_FP8["seed"]) -> DenseWorkload:
-    """Weights N(0,1) quantised per 128x128 block by absmax/448 to e4m3;
+    """Weights N(0,1) quantised per 128x128 block by absmax/448 to e4m3
+    (128 x 16 blocks when N is not a multiple of 128, for small test shapes);
     activations N(0,1) quantised per (token, 128-K group) the same way."""
     rng = np.random.Generator(np.random.PCG64(seed + M))
     w = rng.standard_normal((K, N), dtype=np.float32)
-    wb = w.reshape(K // 128, 128, N // 128, 128)
+    bn = 128 if N % 128 == 0 else 16
+    wb = w.reshape(K // 128, 128, N // bn, bn)
     sw = (np.abs(wb).max(axis=(1, 3)) / np.float32(448.0)).astype(np.float32)
     wq = _e4m3_codes((wb / sw[:, None, :, None]).reshape(K, N))
     x = rng.standard_normal((M, K), dtype=np.float32)
     xb = x.reshape(M, K // 128, 128)
     sx = (np.abs(xb).max(axis=2) / np.float32(448.0)).astype(np.float32)
     xq = _e4m3_codes((xb / sx[:, :, None]).reshape(M, K))
-    s16 = np.repeat(sw, 128, axis=1)[:, None, :].astype(np.float32)  # [K/128, 1, N]
+    s16 = np.repeat(sw, bn, axis=1)[:, None, :].astype(np.float32)  # [K/128, 1, N]
     return DenseWorkload(M, K, N, bf16_bits_from_f32(x), xq, sx, wq, sw, s16)

@@ -159,6 +159,41 @@ int dwm_moe_combine(const void *x, int x_dtype, int64_t x_rows, int64_t H, const
                     const void *w, int w_dtype, int64_t T, int topk, void *out, int out_dtype,
                     void *stream);
 
+/* ---------------------------------------------------------------------- */
+/* Dense FP8 block-quantised GEMM.                                         */
+/* ---------------------------------------------------------------------- */
+
+/* One-time relayout of an e4m3 weight [K, N] (row-major, the reference's
+ * layout) into the kernel's K-major 2 KiB chunks (16 columns x 128 K).
+ * The load-time analogue of storing the FP8 weight for try_dense_fp8
+ * (patches/tpu-inference/0006-dense-fp8-gemm.patch:141-176).
+ * Requires K % 128 == 0, N % 16 == 0; out holds K*N bytes. */
+int dwm_dense_fp8_prepack(const uint8_t *w, int64_t K, int64_t N, uint8_t *out, void *stream);
+
+/* Workspace bytes the next two entry points need for M x K x N (split-K
+ * partials for small M; 0 when none). */
+int dwm_dense_fp8_workspace_size(int64_t M, int64_t K, int64_t N, int64_t *bytes);
+
+/* W8A16: out[M, N] bf16 = sum over 128-row K blocks kb of
+ * dot(x[:, kb], w[kb, :]) (f32) * s[kb, n] (f32), f32 accumulation.
+ * Replaces dense_fp8.matmul / try_dense_fp8
+ * (kernels/tpu_inference/kernels/experimental/dense_fp8.py:15-76, 140-163).
+ *   x: [M, K] bf16; w: prepacked e4m3; s: [K/128, N] f32 (the reference's
+ *   [K/128, 1, N]). */
+int dwm_dense_fp8_w8a16(const uint16_t *x, int64_t M, int64_t K, int64_t N, const uint8_t *w,
+                        const float *s, uint16_t *out, void *workspace, int64_t workspace_bytes,
+                        void *stream);
+
+/* W8A8 block variant: out[m, n] = sum_kb sx[m, kb] * sw[kb, n/128] *
+ * dot(xq[m, kb], wq[kb, n]), bf16 output.  No reference kernel (the
+ * reference's dense path is W8A16); the per-token-per-128 activation and
+ * 128x128 weight block scales follow DeepSeek's block FP8 format.
+ *   xq: [M, K] e4m3; sx: [M, K/128] f32; w: prepacked e4m3;
+ *   sw: [K/128, N/128] f32.  Requires N % 128 == 0. */
+int dwm_dense_fp8_w8a8(const uint8_t *xq, const float *sx, int64_t M, int64_t K, int64_t N,
+                       const uint8_t *w, const float *sw, uint16_t *out, void *workspace,
+                       int64_t workspace_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -57,3 +57,28 @@ def abs_product_w8a16(x, w_codes, s):
     s = np.abs(np.asarray(s, np.float64).reshape(k // 128, 1, n))
     w = (w.reshape(k // 128, 128, n) * s).reshape(k, n)
     return np.abs(np.asarray(x, np.float64)) @ w
+
+
+def abs_product_w8a8(xq, sx, wq, sw):
+    """sum_k |xq_mk sx_m,kb| |wq_kn sw_kb,n/128| (float64), for the error bound."""
+    xv = np.abs(E4M3_VALUES[np.asarray(xq)].astype(np.float64))
+    wv = np.abs(E4M3_VALUES[np.asarray(wq)].astype(np.float64))
+    m, k = xv.shape
+    n = wv.shape[1]
+    xs = (xv.reshape(m, k // 128, 128) * np.abs(np.asarray(sx, np.float64))[:, :, None]).reshape(m, k)
+    swf = np.repeat(np.abs(np.asarray(sw, np.float64)), 128, axis=1)[:, :n]
+    ws = (wv.reshape(k // 128, 128, n) * swf[:, None, :]).reshape(k, n)
+    return xs @ ws
+
+
+def error_bound(y64, absprod, k, out_dtype="bfloat16"):
+    """Stated tolerance for a dense FP8 output element against float64:
+
+        |y - y64| <= u_out |y64| + (K + 3 K/128) 2^-24 sum_k |x_k w_k s_k|
+
+    u_out = 2^-8 for bf16 output; the second term covers any f32 order of
+    the 128-long partial dots, the f32 scale products and the sum over K
+    blocks (and the sx * sw product of the W8A8 variant).
+    """
+    u_out = 2.0 ** -8 if out_dtype == "bfloat16" else 2.0 ** -24
+    return u_out * np.abs(y64) + (k + 3 * (k // 128)) * 2.0 ** -24 * absprod
