@@ -1,17 +1,20 @@
 // FP4 weight formats: e2m1 -> gmm_v2 codes, the decode test hook, and the
 // load-time prepack into the layout the grouped-matmul kernel streams.
 //
-// Prepacked weight layout (per expert e, 16-column block nb, 128-deep K block kb):
-//   weight[((e * N/16 + nb) * K/128 + kb) * 1024 + lane * 16 + j]
-//   lane = 16*q + c (c: column nb*16 + c; q: K quarter), byte j holds the e2m1
-//   nibbles of k = kb*128 + 32*q + 2*j (low) and k + 1 (high).
-// A wave reads one contiguous 1 KiB chunk per (nb, kb): lane l gets the 32
-// consecutive K values of its column in one 32-element scale block.  That is
-// the bf16 MFMA 16x16x32 B-operand order the gmm kernel decodes into (8 K per
-// step, 4 steps) and the gfx950 scaled MFMA 16x16x128 fp4 operand order.
-// Prepacked scales: scale[((e * N/16 + nb) * KB4 + kb / 4) * 256 + lane * 4 + kb % 4]
-//   with KB4 = ceil(K / 512): the e8m0 code of the 32-block (k = kb*128 + 32q)
-//   of column nb*16 + c; bytes past K/128 are zero.
+// Prepacked weight layout: per expert e, 64-column group g (G = ceil(N/64)
+// groups; columns past N are padding with zero codes), 64-deep K step t
+// (T = K/64) and 32-column half j, one 1 KiB block
+//   weight[(((e * G + g) * T + t) * 2 + j) * 1024 + lane * 16 + i]
+//   lane = c + 32*h: column 64*g + 32*j + c; byte i holds the e2m1 nibbles of
+//   k = 64*t + 32*h + 2*i (low) and k + 1 (high).
+// Lane l's 16 bytes are the 32 consecutive K values of its column in one
+// 32-element scale block, which is the bf16 MFMA 32x32x16 B-operand order the
+// kernel decodes into (dword s of the lane feeds MFMA step s of the K step).
+// Prepacked scales: per (e, g, 128-deep step kb) 256 bytes
+//   scale[((e * G + g) * (K/128) + kb) * 256 + lane * 4 + 2*f + j]
+//   = e8m0 code of column 64*g + 32*j + c, K-block 4*kb + 2*f + h
+// (f: which 64-deep half of the 128-deep step), so one dword per lane holds
+// every scale a 64-column group needs for two K steps.
 #include "common.h"
 
 namespace dwm {
@@ -96,52 +99,57 @@ __global__ void fp4_decode_kernel(const uint8_t *packed, int format, int64_t nby
   out[i] = r;
 }
 
-// One thread per (e, nb, kb4, lane): up to 4 K-blocks of 128 (16 B each) and
-// one 4-byte scale word.
+// One thread per (e, g, kb, lane): the four 16-byte pieces of lane `lane` in
+// the two 64-deep steps of 128-deep step kb (both halves j) and its scale word.
 __global__ void gmm_fp4_prepack_kernel(const uint8_t *rhs, int format, const void *scale,
                                        int scale_dtype, int64_t E, int64_t K, int64_t N,
                                        uint8_t *wout, uint8_t *sout, int32_t *flags) {
-  const int64_t N16 = N / 16, KB = K / 128, KB4 = (KB + 3) / 4;
+  const int64_t G = (N + 63) / 64, KB = K / 128, T = K / 64;
   int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t total = E * N16 * KB4 * 64;
+  const int64_t total = E * G * KB * 64;
   if (t >= total) return;
   const int lane = (int)(t & 63);
   int64_t r = t >> 6;
-  const int64_t kb4 = r % KB4;
-  r /= KB4;
-  const int64_t nb = r % N16;
-  const int64_t e = r / N16;
-  const int q = lane >> 4, c = lane & 15;
-  const int64_t n = nb * 16 + c;
+  const int64_t kb = r % KB;
+  r /= KB;
+  const int64_t g = r % G;
+  const int64_t e = r / G;
+  const int c = lane & 31, h = lane >> 5;
   const int64_t half_n = N / 2;
   bool bad_scale = false, bad_code = false;
   uint32_t sword = 0;
-  for (int p = 0; p < 4; ++p) {
-    const int64_t kb = kb4 * 4 + p;
-    if (kb >= KB) break;
-    const int64_t k0 = kb * 128 + 32 * q;
-    uint32_t code = scale_to_code(scale, scale_dtype, (e * (K / 32) + (k0 >> 5)) * N + n, &bad_scale);
-    uint32_t words[4];
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      uint32_t word = 0;
+  for (int f = 0; f < 2; ++f) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int64_t k = k0 + 8 * w + i;
-        uint32_t byte = rhs[(e * K + k) * half_n + (n >> 1)];
-        uint32_t nib = (n & 1) ? (byte >> 4) : (byte & 0xFu);
-        nib = format == DWM_FP4_CODES ? code_to_e2m1(nib, &bad_code) : canon_e2m1(nib);
-        if (code == 0u) nib &= 8u;  // zero scale: keep only the sign -> +-0
-        word |= nib << (4 * i);
+    for (int j = 0; j < 2; ++j) {
+      const int64_t n = g * 64 + 32 * j + c;
+      const int64_t k0 = kb * 128 + 64 * f + 32 * h;
+      uint32_t code = 127u;
+      uint32_t words[4] = {0u, 0u, 0u, 0u};
+      if (n < N) {
+        code = scale_to_code(scale, scale_dtype, (e * (K / 32) + (k0 >> 5)) * N + n, &bad_scale);
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          uint32_t word = 0;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const int64_t k = k0 + 8 * w + i;
+            const uint32_t byte = rhs[(e * K + k) * half_n + (n >> 1)];
+            uint32_t nib = (n & 1) ? (byte >> 4) : (byte & 0xFu);
+            nib = format == DWM_FP4_CODES ? code_to_e2m1(nib, &bad_code) : canon_e2m1(nib);
+            if (code == 0u) nib &= 8u;  // zero scale: keep only the sign -> +-0
+            word |= nib << (4 * i);
+          }
+          words[w] = word;
+        }
+        if (code == 0u) code = 127u;
       }
-      words[w] = word;
+      sword |= (code & 0xFFu) << (8 * (2 * f + j));
+      const u32x4_t v = {words[0], words[1], words[2], words[3]};
+      *(u32x4_t *)(wout + (((e * G + g) * T + 2 * kb + f) * 2 + j) * 1024 + lane * 16) = v;
     }
-    if (code == 0u) code = 127u;
-    sword |= (code & 0xFFu) << (8 * p);
-    u32x4_t v = {words[0], words[1], words[2], words[3]};
-    *(u32x4_t *)(wout + ((e * N16 + nb) * KB + kb) * 1024 + lane * 16) = v;
   }
-  *(uint32_t *)(sout + ((e * N16 + nb) * KB4 + kb4) * 256 + lane * 4) = sword;
+  *(uint32_t *)(sout + ((e * G + g) * KB + kb) * 256 + lane * 4) = sword;
   if (bad_scale) atomicOr(flags, 1);
   if (bad_code) atomicOr(flags, 2);
 }
@@ -187,9 +195,9 @@ extern "C" int dwm_gmm_fp4_prepack_size(int64_t E, int64_t K, int64_t N, int64_t
                      "gmm_fp4: K %% 128 == 0 and N %% 16 == 0 required (K=%lld N=%lld)",
                      (long long)K, (long long)N);
   DWM_CHECK_ARG(weight_bytes && scale_bytes, "gmm_fp4_prepack_size: null output pointer");
-  const int64_t KB4 = (K / 128 + 3) / 4;
-  *weight_bytes = E * K * N / 2;
-  *scale_bytes = E * (N / 16) * KB4 * 256;
+  const int64_t G = (N + 63) / 64;
+  *weight_bytes = E * G * 64 * K / 2;
+  *scale_bytes = E * G * (K / 128) * 256;
   return DWM_OK;
 }
 
@@ -205,7 +213,7 @@ extern "C" int dwm_gmm_fp4_prepack(const uint8_t *rhs, int format, const void *s
                 "gmm_fp4_prepack: bad scale dtype %d", scale_dtype);
   if (E == 0) return DWM_OK;
   DWM_CHECK_ARG(rhs && scale && weight_out && scale_out && flags, "gmm_fp4_prepack: null pointer");
-  const int64_t total = E * (N / 16) * ((K / 128 + 3) / 4) * 64;
+  const int64_t total = E * ((N + 63) / 64) * (K / 128) * 64;
   const int64_t blocks = (total + 255) / 256;
   DWM_CHECK_ARG(blocks < (1ll << 31), "gmm_fp4_prepack: too large");
   hipLaunchKernelGGL(gmm_fp4_prepack_kernel, dim3((unsigned)blocks), dim3(256), 0,

@@ -2,30 +2,27 @@
 // activations, f32 accumulation: the tokamax gmm_v2 rhs_fp4_codes path
 // (patches/tokamax/0001-gmm_v2-fp4-emulation-v6e.patch:58-66, :100-151).
 //
-// Work decomposition: a block (4 waves) owns one (local group, 16*MB-row
-// tile) x (64*NBW-column tile); each wave owns NBW 16-column blocks of it.
-// Tiles are enumerated on the device from group_sizes (no host sync): the
-// tile total is (row tiles of every local group) x (column tiles); empty
-// groups own no tile and cost no weight traffic.  Blocks whose index is equal
-// mod 8 run on one XCD (the dispatcher's round robin), so each XCD gets a
-// contiguous run of tiles -- consecutive column tiles of the same row tile --
-// and the group's lhs rows stay in that XCD's L2.
+// Work decomposition: a block owns one (local group, 96-row tile) x
+// (512-column tile).  Tiles are enumerated on the device from group_sizes (no
+// host sync): the tile total is (row tiles of every local group) x (column
+// tiles); empty groups own no tile and cost no weight traffic.  Blocks whose
+// index is equal mod 8 run on one XCD (the dispatcher's round robin), so each
+// XCD gets a contiguous run of tiles -- consecutive column tiles of the same
+// row tile -- and the group's lhs rows are shared in that XCD's L2.
 //
-// Per 128-deep K step: the block stages its [rows x 128] bf16 lhs tile in
-// LDS (double buffered, padded rows, one barrier per step); each wave holds a
-// DEPTH-step register ring of its weight chunks (1 KiB per 16 columns x 128 K,
-// prepacked, see fp4.hip), decodes the current step in registers with the
-// gfx950 fp4 -> bf16 converter (which applies the e8m0 scale exactly) and
-// issues bf16 MFMA 16x16x32 for every 16-row block that holds rows.  The
-// dequantised weights are exact (e2m1 x power of two fits bf16), so the
-// products equal the reference's bf16(decode(q)) * bf16(scale) operands.
+// The block is warp-specialised (see the WsCfg comment): producer waves move
+// the lhs tile and the prepacked weights and scales (fp4.hip) from memory to
+// a ring of LDS stages with direct global -> LDS loads; consumer waves decode
+// the weights in registers with the gfx950 fp4 -> bf16 converter (which
+// applies the e8m0 scale exactly) and run bf16 MFMA 32x32x16 for every 32-row
+// block that holds rows.  The dequantised weights are exact (e2m1 x power of
+// two fits bf16), so the products equal the reference's
+// bf16(decode(q)) * bf16(scale) operands; only the f32 summation order differs.
 #include "common.h"
 
 namespace dwm {
 
-constexpr int kGmmThreads = 256;  // 4 waves
 constexpr int kMaxGroups = 1024;
-constexpr int kLdsRow = 136;      // bf16 per LDS row: 128 + 8 pad (272 B: conflict-free ds_read_b128)
 
 // Block-wide: exclusive row starts and row-tile starts of every group,
 // computed by wave 0.  s_tilestart[num_groups] receives the row-tile total.
@@ -54,165 +51,202 @@ __device__ __forceinline__ void group_prefix(const int32_t *group_sizes, int num
   }
 }
 
-template <int MB, int NBW, int DEPTH>
-__global__ __launch_bounds__(kGmmThreads) void gmm_fp4_bf16_kernel(
-    const uint16_t *__restrict__ lhs, int64_t M, int K, const uint8_t *__restrict__ wpk,
-    const uint8_t *__restrict__ spk, const int32_t *__restrict__ group_sizes, int num_groups,
-    const int32_t *__restrict__ group_offset, int64_t e_local, int N, void *__restrict__ out,
-    int out_f32) {
-  constexpr int MT = 16 * MB;
-  constexpr int NT = 64 * NBW;
-  __shared__ int s_rowstart[kMaxGroups];
-  __shared__ int s_tilestart[kMaxGroups + 1];
-  __shared__ int s_info[3];
-  __shared__ __attribute__((aligned(16))) uint16_t s_a[2][MT * kLdsRow];
+// s_waitcnt immediate and LDS pointer type for the direct global -> LDS loads.
+typedef __attribute__((address_space(3))) void lds_void_t;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int go = group_offset ? group_offset[0] : 0;
-  group_prefix<MT>(group_sizes, num_groups, go, e_local, s_rowstart, s_tilestart);
-  if (tid == 0) s_info[0] = -1;
-  __syncthreads();
-  const int n_tiles = (N + NT - 1) / NT;
-  const int64_t total = (int64_t)s_tilestart[num_groups] * n_tiles;
-  const int64_t per_xcd = (total + 7) / 8;
-  const int64_t j_x = blockIdx.x >> 3;
-  if (j_x >= per_xcd) return;  // block-uniform
-  const int64_t t = (int64_t)(blockIdx.x & 7) * per_xcd + j_x;
-  if (t >= total) return;
-  const int trow = (int)(t / n_tiles), nt = (int)(t % n_tiles);
-  for (int g = tid; g < num_groups; g += kGmmThreads) {
-    if (s_tilestart[g] <= trow && trow < s_tilestart[g + 1]) {
-      const int tt = trow - s_tilestart[g];
-      s_info[0] = g;
-      s_info[1] = s_rowstart[g] + tt * MT;
-      s_info[2] = min(MT, group_sizes[g] - tt * MT);
+// s_waitcnt immediate (gfx9 encoding): vmcnt <= vm, lgkmcnt == 0, expcnt untouched.
+__host__ __device__ constexpr int waitcnt_vm_lgkm0(int vm) { return (vm & 15) | ((vm >> 4) << 14) | (7 << 4); }
+
+// ---------------------------------------------------------------------------
+// Warp-specialised tiles.
+//
+// A block of 12 waves owns (group, 32*MB rows) x 512 columns.  Waves 0..7
+// (consumers, two per SIMD) each own 64 columns: they read the lhs tile and
+// their weight codes and scales from LDS, decode, and run the 32x32x16 MFMAs.
+// Waves 8..11 (producers, one per SIMD) only move data: global -> LDS loads
+// (global_load_lds) of the lhs tile, weights and scales, three 64-deep K
+// steps ahead through a four-stage LDS ring.  One workgroup barrier per step
+// hands a stage from producers to consumers and the previous one back.  Each
+// role issues one kind of memory operation, so the compiler's waits stay
+// exact, and the consumers carry no load rings in registers.
+//
+// Weight layout (64-column groups): for expert e, group g (columns 64 g ..
+// 64 g + 63, N padded to a multiple of 64 with zero codes), 64-deep K step t
+// and half j: 1 KiB where lane l = c + 32 h holds the 32 codes of column
+// 64 g + 32 j + c at k = 64 t + 32 h .. + 31, two per byte, low nibble first.
+// Scale layout: for (e, g, 128-deep step kb) 256 bytes; byte 2 f + j of lane
+// l = c + 32 h is the e8m0 code of column 64 g + 32 j + c, K-block
+// 4 kb + 2 f + h.  MFMA step s of K step t takes lane (c, h)'s codes
+// k = 64 t + 32 h + 8 s .. + 7 and the lhs chunk with the same k.
+// Block shape: CW consumer waves owning JW 32-column blocks each (a tile of
+// 32 JW CW columns = GT 64-column groups), NP producer waves, NS LDS stages.
+// With PF the producers publish steps t and t + 1 at the barrier of step t
+// and the consumers read step t + 1's weights ahead; without it only step t.
+template <int MB, int CW, int JW, int NP, int NS, bool PF>
+struct WsCfg {
+  static constexpr int CONS = CW, JWAVE = JW, NPROD = NP, STAGES = NS;
+  static constexpr bool PREFETCH = PF;
+  static constexpr int GT = JW * CW / 2;                 // 64-column groups per tile
+  static constexpr int THREADS = 64 * (CW + NP);
+  static constexpr int NT = 64 * GT;
+  static constexpr int A = 0;                           // 32 MB rows x 128 bytes (8 XOR-swizzled 16-byte chunks)
+  static constexpr int W = 32 * MB * 128;               // group i of the tile: 2 KiB at W + 2048 i
+  static constexpr int S = W + GT * 2048;               // group i: 256 bytes at S + 256 i
+  static constexpr int STAGE = S + GT * 256;
+  static constexpr int A_LOADS = 4 * MB / NP;           // 1 KiB lhs loads per producer per step
+  static constexpr int G_LOADS = GT / NP;               // groups per producer
+  static constexpr int LOADS = A_LOADS + 3 * G_LOADS;   // + (2 weight + 1 scale) per group
+  static constexpr int AHEAD = PF ? 2 : 1;              // steps published per barrier
+  static constexpr int PENDING = LOADS * (NS - 1 - AHEAD);
+  static_assert(A_LOADS * NP == 4 * MB && G_LOADS * NP == GT, "loads split evenly over the producers");
+  static_assert(PENDING < 64 && NS - 1 - AHEAD >= 1, "vmcnt range / stage count");
+  static_assert(JW % 2 == 0, "consumers own whole 64-column groups");
+};
+
+template <class C, int MB>
+__device__ __forceinline__ void ws_producer(const uint16_t *__restrict__ lhs, int64_t row0, int rows, int K, int T,
+                                            int KB, const uint8_t *__restrict__ wexp,
+                                            const uint8_t *__restrict__ sexp, int g0, int G, uint8_t *s_lds,
+                                            int pw) {
+  constexpr int NP = C::NPROD;
+  const int lane = threadIdx.x & 63;
+  // lhs load i of producer pw: rows 8 (pw + NP i) .. + 7 of the tile; lane l
+  // fills physical chunk l % 8 of row + l / 8 with logical chunk
+  // (l % 8) ^ (row % 8).  Rows past the tile repeat its last row (every load
+  // keeps all lanes, so each step issues the same number of loads).
+  const uint8_t *const abase = (const uint8_t *)(lhs + row0 * K);
+  uint32_t aoff[C::A_LOADS];
+#pragma unroll
+  for (int i = 0; i < C::A_LOADS; ++i) {
+    const int r = 8 * (pw + NP * i) + (lane >> 3);
+    const int rs = r < rows ? r : rows - 1;
+    aoff[i] = (uint32_t)rs * (uint32_t)K * 2u + ((((lane & 7) ^ (r & 7))) << 4);
+  }
+  const uint8_t *wsrc[C::G_LOADS];
+  const uint8_t *ssrc[C::G_LOADS];
+#pragma unroll
+  for (int c = 0; c < C::G_LOADS; ++c) {
+    const int g = min(g0 + pw + NP * c, G - 1);  // groups past N feed unstored columns
+    wsrc[c] = wexp + (int64_t)g * T * 2048 + lane * 16;
+    ssrc[c] = sexp + (int64_t)g * KB * 256 + lane * 4;
+  }
+  auto issue = [&](int stage, int t) {
+    uint8_t *const st = s_lds + stage * C::STAGE;
+    const uint8_t *const a = abase + (int64_t)t * 128;
+#pragma unroll
+    for (int i = 0; i < C::A_LOADS; ++i)
+      __builtin_amdgcn_global_load_lds((const void *)(a + aoff[i]),
+                                       (lds_void_t *)(st + C::A + (pw + NP * i) * 1024), 16, 0, 0);
+#pragma unroll
+    for (int c = 0; c < C::G_LOADS; ++c) {
+      const int gi = pw + NP * c;
+      const uint8_t *const w = wsrc[c] + (int64_t)t * 2048;
+      __builtin_amdgcn_global_load_lds((const void *)w, (lds_void_t *)(st + C::W + gi * 2048), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void *)(w + 1024), (lds_void_t *)(st + C::W + gi * 2048 + 1024), 16,
+                                       0, 0);
+      __builtin_amdgcn_global_load_lds((const void *)(ssrc[c] + (int64_t)(t >> 1) * 256),
+                                       (lds_void_t *)(st + C::S + gi * 256), 4, 0, 0);
     }
+  };
+  constexpr int NS = C::STAGES;
+#pragma unroll
+  for (int t = 0; t < NS - 1; ++t) issue(t, min(t, T - 1));
+  int refill = NS - 1;  // stage of step t + NS - 1
+  for (int t = 0; t < T; ++t) {
+    // Steps t .. t + AHEAD - 1 have landed once at most the loads of the
+    // later steps are pending.
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(C::PENDING));
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    // The consumers are done with step t - 1: refill its stage with step
+    // t + NS - 1 (clamped to the last step, so every step issues the same loads).
+    issue(refill, min(t + NS - 1, T - 1));
+    refill = refill == NS - 1 ? 0 : refill + 1;
   }
-  __syncthreads();
-  const int g = s_info[0];
-  if (g < 0) return;
-  const int64_t row0 = s_info[1];
-  if (row0 >= M) return;
-  const int rows = (int)min((int64_t)s_info[2], M - row0);
-  const int act_mb = (rows + 15) >> 4;
-  const int64_t e = g - go;
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
+}
 
-  const int N16 = N >> 4, KB = K >> 7, KB4 = (KB + 3) >> 2;
-  const int nb0 = nt * (NBW * 4) + wave * NBW;
-  const uint8_t *wp[NBW];
-  const uint8_t *sp[NBW];
-  bool nvalid[NBW];
+template <class C, int AM>
+__device__ __forceinline__ void ws_consumer(int T, const uint8_t *s_lds, int cw, int64_t row0, int rows,
+                                            int64_t col0, int N, void *__restrict__ out, int out_f32) {
+  constexpr int JW = C::JWAVE, GPC = JW / 2, NS = C::STAGES;
+  const int lane = threadIdx.x & 63, c32 = lane & 31, h = lane >> 5;
+  f32x16_t acc[AM][JW];
 #pragma unroll
-  for (int j = 0; j < NBW; ++j) {
-    const int nbg = nb0 + j;
-    nvalid[j] = nbg < N16;
-    const int64_t nbc = nvalid[j] ? nbg : 0;
-    wp[j] = wpk + ((e * N16 + nbc) * KB) * 1024 + lane * 16;
-    sp[j] = spk + ((e * N16 + nbc) * KB4) * 256 + lane * 4;
-  }
-
-  f32x4_t acc[MB][NBW];
+  for (int mb = 0; mb < AM; ++mb)
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb)
+    for (int j = 0; j < JW; ++j)
 #pragma unroll
-    for (int j = 0; j < NBW; ++j) acc[mb][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-
-  // lhs tile staging: 16*act_mb rows x 16 chunks of 16 B; chunk tid + 256*i
-  // is row 16*i + tid/16, so the row-block test is block-uniform.
-  const int srow = tid >> 4, scol = (tid & 15) * 8;
-  u32x4_t areg[MB];
-  auto load_a = [&](int kb) {
+      for (int r = 0; r < 16; ++r) acc[mb][j][r] = 0.0f;
+  const int arow = C::A + c32 * 128;
+  const int x = c32 & 7;
+  const int woff = C::W + cw * GPC * 2048 + lane * 16;
+  const int soff = C::S + cw * GPC * 256 + lane * 4;
+  // With PREFETCH the weights and scales of step t + 1 (published at the
+  // barrier of step t) are read one step ahead.
+  u32x4_t wn[JW];
+  uint32_t sn[GPC];
+  auto read_ws = [&](const uint8_t *st) {
 #pragma unroll
-    for (int i = 0; i < MB; ++i) {
-      if (i < act_mb) {
-        int64_t grow = row0 + 16 * i + srow;
-        if (grow >= M) grow = M - 1;  // rows past the tile feed only unstored outputs
-        areg[i] = *(const u32x4_t *)(lhs + grow * K + (int64_t)kb * 128 + scol);
+    for (int gl = 0; gl < GPC; ++gl) {
+      wn[2 * gl] = *(const u32x4_t *)(st + woff + gl * 2048);
+      wn[2 * gl + 1] = *(const u32x4_t *)(st + woff + gl * 2048 + 1024);
+      sn[gl] = *(const uint32_t *)(st + soff + gl * 256);
+    }
+  };
+  int cur = 0;  // stage of step t
+  for (int t = 0; t < T; ++t) {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    const uint8_t *const st = s_lds + cur * C::STAGE;
+    const int nxt = cur == NS - 1 ? 0 : cur + 1;
+    if (!C::PREFETCH || t == 0) read_ws(st);
+    u32x4_t w[JW];
+    float sc[JW];
+#pragma unroll
+    for (int gl = 0; gl < GPC; ++gl) {
+      w[2 * gl] = wn[2 * gl];
+      w[2 * gl + 1] = wn[2 * gl + 1];
+      const uint32_t sd = sn[gl] >> (16 * (t & 1));
+      sc[2 * gl] = e8m0_to_f32(sd & 0xFFu);
+      sc[2 * gl + 1] = e8m0_to_f32((sd >> 8) & 0xFFu);
+    }
+    if (C::PREFETCH && t + 1 < T) read_ws(s_lds + nxt * C::STAGE);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      u32x4_t b[JW];
+#pragma unroll
+      for (int j = 0; j < JW; ++j) {
+        b[j][0] = cvt_fp4x2_bf16<0>(w[j][s], sc[j]);
+        b[j][1] = cvt_fp4x2_bf16<1>(w[j][s], sc[j]);
+        b[j][2] = cvt_fp4x2_bf16<2>(w[j][s], sc[j]);
+        b[j][3] = cvt_fp4x2_bf16<3>(w[j][s], sc[j]);
+      }
+      const int ach = (((4 * h + s) ^ x) << 4);
+#pragma unroll
+      for (int mb = 0; mb < AM; ++mb) {
+        const u32x4_t a = *(const u32x4_t *)(st + arow + mb * 32 * 128 + ach);
+#pragma unroll
+        for (int j = 0; j < JW; ++j)
+          acc[mb][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                               __builtin_bit_cast(bf16x8_t, b[j]), acc[mb][j], 0, 0, 0);
       }
     }
-  };
-  auto store_a = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < MB; ++i)
-      if (i < act_mb) *(u32x4_t *)(&s_a[buf][(16 * i + srow) * kLdsRow + scol]) = areg[i];
-  };
-
-  u32x4_t wbuf[DEPTH][NBW];
-  uint32_t sbuf[DEPTH][NBW];
-  auto load_w = [&](int slot, int kb) {
-#pragma unroll
-    for (int j = 0; j < NBW; ++j) {
-      wbuf[slot][j] = *(const u32x4_t *)(wp[j] + (int64_t)kb * 1024);
-      sbuf[slot][j] = sp[j][(int64_t)(kb >> 2) * 256 + (kb & 3)];
-    }
-  };
-
-  load_a(0);
-#pragma unroll
-  for (int d = 0; d < DEPTH; ++d)
-    if (d < KB) load_w(d, d);
-  store_a(0);
-  __syncthreads();
-
-  const int arow = lane & 15, acol = 32 * (lane >> 4);
-  for (int kb0 = 0; kb0 < KB; kb0 += DEPTH) {
-#pragma unroll
-    for (int d = 0; d < DEPTH; ++d) {
-      const int kb = kb0 + d;
-      if (kb < KB) {
-        const int buf = kb & 1;
-        const bool more = kb + 1 < KB;
-        if (more) load_a(kb + 1);
-        u32x4_t wcur[NBW];
-        float sc[NBW];
-#pragma unroll
-        for (int j = 0; j < NBW; ++j) {
-          wcur[j] = wbuf[d][j];
-          sc[j] = e8m0_to_f32(sbuf[d][j]);
-        }
-        if (kb + DEPTH < KB) load_w(d, kb + DEPTH);
-        const uint16_t *abase = &s_a[buf][arow * kLdsRow + acol];
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          u32x4_t bfrag[NBW];
-#pragma unroll
-          for (int j = 0; j < NBW; ++j) {
-            const uint32_t w = wcur[j][s];
-            bfrag[j][0] = cvt_fp4x2_bf16<0>(w, sc[j]);
-            bfrag[j][1] = cvt_fp4x2_bf16<1>(w, sc[j]);
-            bfrag[j][2] = cvt_fp4x2_bf16<2>(w, sc[j]);
-            bfrag[j][3] = cvt_fp4x2_bf16<3>(w, sc[j]);
-          }
-#pragma unroll
-          for (int mb = 0; mb < MB; ++mb) {
-            if (mb < act_mb) {
-              const u32x4_t a = *(const u32x4_t *)(abase + mb * 16 * kLdsRow + 8 * s);
-#pragma unroll
-              for (int j = 0; j < NBW; ++j)
-                acc[mb][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                    __builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, bfrag[j]), acc[mb][j],
-                    0, 0, 0);
-            }
-          }
-        }
-        if (more) store_a(buf ^ 1);
-        __syncthreads();
-      }
-    }
+    cur = nxt;
   }
-
-  // Epilogue: C layout of mfma 16x16: reg r -> row 4*(lane/16) + r, col lane%16.
-  const int qrow = 4 * (lane >> 4);
+  const int hrow = 4 * h;
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
-    if (mb >= act_mb) continue;
+  for (int mb = 0; mb < AM; ++mb) {
 #pragma unroll
-    for (int j = 0; j < NBW; ++j) {
-      if (!nvalid[j]) continue;
-      const int64_t col = (int64_t)(nb0 + j) * 16 + (lane & 15);
+    for (int j = 0; j < JW; ++j) {
+      const int64_t col = col0 + 32 * j + c32;
+      if (col >= N) continue;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int lrow = mb * 16 + qrow + r;
+      for (int r = 0; r < 16; ++r) {
+        const int lrow = mb * 32 + 8 * (r >> 2) + hrow + (r & 3);
         if (lrow < rows) {
           const int64_t o = (row0 + lrow) * N + col;
           if (out_f32) ((float *)out)[o] = acc[mb][j][r];
@@ -221,6 +255,68 @@ __global__ __launch_bounds__(kGmmThreads) void gmm_fp4_bf16_kernel(
       }
     }
   }
+}
+
+template <class C, int MB>
+__global__ __launch_bounds__(C::THREADS) void gmm_fp4_ws_kernel(
+    const uint16_t *__restrict__ lhs, int64_t M, int K, const uint8_t *__restrict__ wpk,
+    const uint8_t *__restrict__ spk, const int32_t *__restrict__ group_sizes, int num_groups,
+    const int32_t *__restrict__ group_offset, int64_t e_local, int N, void *__restrict__ out,
+    int out_f32) {
+  constexpr int MT = 32 * MB;
+  constexpr int NT = C::NT;
+  constexpr int CW = C::CONS;
+  static_assert(C::STAGE >= (2 * kMaxGroups + 1) * 4, "group prefix aliases the first stage");
+  __shared__ __attribute__((aligned(1024))) uint8_t s_lds[C::STAGES * C::STAGE];
+  __shared__ int s_info[3];
+  int *s_rowstart = (int *)s_lds;
+  int *s_tilestart = s_rowstart + kMaxGroups;
+
+  const int tid = threadIdx.x, wave = tid >> 6;
+  const int go = group_offset ? group_offset[0] : 0;
+  group_prefix<MT>(group_sizes, num_groups, go, e_local, s_rowstart, s_tilestart);
+  if (tid == 0) s_info[0] = -1;
+  __syncthreads();
+  const int n_tiles = (N + NT - 1) / NT;
+  const int64_t total = (int64_t)s_tilestart[num_groups] * n_tiles;
+  const int64_t per_xcd = (total + 7) / 8;
+  const int64_t j_x = blockIdx.x >> 3;
+  const int64_t t = (int64_t)(blockIdx.x & 7) * per_xcd + j_x;
+  const bool has_tile = j_x < per_xcd && t < total;
+  if (has_tile) {
+    const int trow = (int)(t / n_tiles);
+    for (int g = tid; g < num_groups; g += C::THREADS) {
+      if (s_tilestart[g] <= trow && trow < s_tilestart[g + 1]) {
+        const int tt = trow - s_tilestart[g];
+        s_info[0] = g;
+        s_info[1] = s_rowstart[g] + tt * MT;
+        s_info[2] = min(MT, group_sizes[g] - tt * MT);
+      }
+    }
+  }
+  __syncthreads();  // also retires the prefix reads before the stages overwrite them
+  const int g = s_info[0];
+  if (!has_tile || g < 0) return;
+  const int nt = (int)(t % n_tiles);
+  const int64_t row0 = s_info[1];
+  if (row0 >= M) return;
+  const int rows = (int)min((int64_t)s_info[2], M - row0);
+  const int64_t e = g - go;
+  const int T = K >> 6, KB = K >> 7, G = (N + 63) >> 6;
+  const int g0 = nt * C::GT;  // first 64-column group of the tile
+  if (wave >= CW) {
+    ws_producer<C, MB>(lhs, row0, rows, K, T, KB, wpk + e * G * T * 2048, spk + e * G * KB * 256, g0, G, s_lds,
+                       wave - CW);
+    return;
+  }
+  const int act_mb = (rows + 31) >> 5;
+  const int64_t col0 = (int64_t)(g0 + wave * (C::JWAVE / 2)) * 64;
+  // Every consumer runs exactly one barrier per K step (the producers' count),
+  // whatever its row-block count.
+  if (act_mb <= 1 || MB == 1) ws_consumer<C, 1>(T, s_lds, wave, row0, rows, col0, N, out, out_f32);
+  else if (act_mb == 2 || MB == 2) ws_consumer<C, (MB >= 2 ? 2 : 1)>(T, s_lds, wave, row0, rows, col0, N, out, out_f32);
+  else if (act_mb == 3 || MB == 3) ws_consumer<C, (MB >= 3 ? 3 : 1)>(T, s_lds, wave, row0, rows, col0, N, out, out_f32);
+  else ws_consumer<C, MB>(T, s_lds, wave, row0, rows, col0, N, out, out_f32);
 }
 
 // zero_initialize: zero rows outside [start(go), start(go + E_local)).
@@ -256,17 +352,19 @@ __global__ __launch_bounds__(256) void gmm_zero_rows_kernel(const int32_t *group
   }
 }
 
-template <int MB, int NBW, int DEPTH>
-static int launch_gmm(const uint16_t *lhs, int64_t M, int64_t K, const uint8_t *w, const uint8_t *s,
-                      const int32_t *gs, int ng, const int32_t *go, int64_t e_local, int64_t N,
-                      void *out, int out_f32, hipStream_t st) {
-  constexpr int MT = 16 * MB, NT = 64 * NBW;
+template <int MB, int CW, int JW, int NP, int NS, bool PF>
+static int launch_gmm_ws(const uint16_t *lhs, int64_t M, int64_t K, const uint8_t *w, const uint8_t *s,
+                         const int32_t *gs, int ng, const int32_t *go, int64_t e_local, int64_t N, void *out,
+                         int out_f32, hipStream_t st) {
+  using C = WsCfg<MB, CW, JW, NP, NS, PF>;
+  constexpr int MT = 32 * MB, NT = C::NT;
   const int64_t n_tiles = (N + NT - 1) / NT;
   const int64_t max_tiles = ((M + MT - 1) / MT + e_local) * n_tiles;
   const int64_t grid = (max_tiles + 7) / 8 * 8;
   DWM_UNSUPPORTED_IF(grid > (1ll << 31) - 1, "gmm_fp4: too many tiles (%lld)", (long long)grid);
-  hipLaunchKernelGGL((gmm_fp4_bf16_kernel<MB, NBW, DEPTH>), dim3((unsigned)grid), dim3(kGmmThreads), 0, st,
-                     lhs, M, (int)K, w, s, gs, ng, go, e_local, (int)N, out, out_f32);
+  DWM_UNSUPPORTED_IF(K > (1 << 24), "gmm_fp4: K <= 2^24 required");
+  hipLaunchKernelGGL((gmm_fp4_ws_kernel<C, MB>), dim3((unsigned)grid), dim3(C::THREADS), 0, st, lhs, M, (int)K, w,
+                     s, gs, ng, go, e_local, (int)N, out, out_f32);
   return launch_status("gmm_fp4");
 }
 
@@ -301,9 +399,10 @@ extern "C" int dwm_gmm_fp4(const uint16_t *lhs, int64_t M, int64_t K, const uint
   }
   if (E_local == 0 || num_groups == 0) return DWM_OK;
   const int out_f32 = out_dtype == DWM_F32;
-  // 96-row x 256-column tiles, one-step weight prefetch: 240 VGPRs and 60 KB
-  // of LDS keep two blocks (8 waves) per CU, measured fastest on the decode
-  // and prefill workloads among the (rows, columns, depth) variants tried.
-  return launch_gmm<6, 4, 1>(lhs, M, K, weight, scale, group_sizes, num_groups, group_offset, E_local, N,
-                             out, out_f32, st);
+  // 96-row x 512-column tiles, 8 consumer + 4 producer waves, four 64-deep
+  // K stages (120 KB of LDS, 138 VGPRs: one block of 12 waves per CU).
+  // Measured fastest on the decode and prefill workloads among the tile,
+  // wave-split and pipeline-depth variants tried.
+  return launch_gmm_ws<3, 8, 2, 4, 4, false>(lhs, M, K, weight, scale, group_sizes, num_groups, group_offset,
+                                             E_local, N, out, out_f32, st);
 }

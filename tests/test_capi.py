@@ -60,7 +60,11 @@ def test_prepack_size_query():
     rc, _ = _rc("dwm_gmm_fp4_prepack_size", 32, 7168, 4096, ctypes.byref(wb), ctypes.byref(sb))
     assert rc == _lib.OK
     assert wb.value == 32 * 7168 * 4096 // 2
-    assert sb.value == 32 * (4096 // 16) * ((7168 // 128 + 3) // 4) * 256
+    assert sb.value == 32 * (4096 // 64) * (7168 // 128) * 256
+    rc, _ = _rc("dwm_gmm_fp4_prepack_size", 2, 256, 80, ctypes.byref(wb), ctypes.byref(sb))
+    assert rc == _lib.OK
+    assert wb.value == 2 * 128 * 256 // 2  # N padded to 128 columns
+    assert sb.value == 2 * 2 * 2 * 256
     rc, _ = _rc("dwm_gmm_fp4_prepack_size", 1, 192, 64, ctypes.byref(wb), ctypes.byref(sb))
     assert rc == _lib.ERR_UNSUPPORTED
 

@@ -62,27 +62,34 @@ def test_decode_flags_code_255(dev):
 
 def test_prepack_layout_matches_definition(dev, rng):
     """Every prepacked byte equals the documented layout of the reference
-    [E, K, N/2] weight, and every scale byte its [E, K/32, N] code."""
+    [E, K, N/2] weight, and every scale byte its [E, K/32, N] code; columns
+    past N (padding to 64) hold zero codes and scale code 127."""
     from dw_tpu_amd import prepack_fp4
-    E, K, N = 2, 640, 48  # K/128 = 5 (partial last scale word), N/16 = 3
+    E, K, N = 2, 640, 80  # K/64 = 10 steps, N = 64 + 16: the second group is 3/4 padding
+    G, T, KB = 2, K // 64, K // 128
     rhs = rng.integers(0, 256, (E, K, N // 2), dtype=np.uint8)
     sc = rng.integers(1, 255, (E, K // 32, 1, N), dtype=np.uint8)
     w = prepack_fp4(torch.from_numpy(rhs).to(dev), torch.from_numpy(sc).to(dev))
-    wp = w.weight.cpu().numpy().reshape(E, N // 16, K // 128, 64, 16)
-    sp = w.scale.cpu().numpy().reshape(E, N // 16, 2, 64, 4)
+    wp = w.weight.cpu().numpy().reshape(E, G, T, 2, 64, 16)
+    sp = w.scale.cpu().numpy().reshape(E, G, KB, 64, 4)
     nib = fp4.unpack_nibbles(rhs)  # [E, K, N]
     nib = np.where(nib == 8, 0, nib)  # -0 -> +0
     for e in range(E):
-        for nb in range(N // 16):
-            for kb in range(K // 128):
-                for lane in range(64):
-                    q, c = divmod(lane, 16)
-                    n = nb * 16 + c
-                    ks = kb * 128 + 32 * q + np.arange(32)
-                    want = fp4.pack_nibbles(nib[e, ks, n][None])[0]
-                    assert np.array_equal(wp[e, nb, kb, lane], want)
-                    assert sp[e, nb, kb // 4, lane, kb % 4] == sc[e, (kb * 128 + 32 * q) // 32, 0, n]
-    assert np.all(sp[:, :, 1, :, 1:] == 0)  # padding past K/128
+        for g in range(G):
+            for t in range(T):
+                for j in range(2):
+                    for lane in range(64):
+                        c, h = lane % 32, lane // 32
+                        n = 64 * g + 32 * j + c
+                        ks = 64 * t + 32 * h + np.arange(32)
+                        if n < N:
+                            want = fp4.pack_nibbles(nib[e, ks, n][None])[0]
+                            code = sc[e, (64 * t + 32 * h) // 32, 0, n]
+                        else:
+                            want = np.zeros(16, np.uint8)
+                            code = 127
+                        assert np.array_equal(wp[e, g, t, j, lane], want)
+                        assert sp[e, g, t // 2, lane, 2 * (t % 2) + j] == code
 
 
 def test_prepack_rejects_bad_scales(dev):
