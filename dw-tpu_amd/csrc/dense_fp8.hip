@@ -19,9 +19,11 @@
 // 16 B loads per lane; lane (c, q) holds 32 consecutive K of one column, the
 // MFMA 16x16x32 B-operand order (8 K per step, 4 steps).
 //
-// Small M: the K loop is split over `ksplit` blocks per tile; each writes an
-// f32 partial [ks][M][N] to the workspace and dense_fp8_reduce_kernel sums
-// the splits in order and rounds once (deterministic).
+// M <= 16: dense_fp8_skinny_kernel (waves split K inside one block, partial
+// sums added in LDS in wave order).  Larger M with few tiles: the K loop is
+// split over `ksplit` blocks per tile; each writes an f32 partial [ks][M][N]
+// to the workspace and dense_fp8_reduce_kernel sums the splits in order and
+// rounds once (deterministic).
 #include "common.h"
 
 namespace dwm {
@@ -240,6 +242,102 @@ __global__ __launch_bounds__(kDenseThreads) void dense_fp8_kernel(
   }
 }
 
+// Skinny M (<= 16 rows, decode): one block owns 16 columns and KS waves split
+// its K steps.  Each wave streams its contiguous prepacked weight chunks
+// through a D-deep register ring and loads its lhs fragments straight from
+// L2 (only rows < M); there is no LDS staging and no barrier in the K loop.
+// The waves' f32 partial sums are added in LDS in wave order (deterministic)
+// and rounded once, in the same launch.
+template <int KS, int D, bool A8>
+__global__ __launch_bounds__(64 * KS) void dense_fp8_skinny_kernel(
+    const void *__restrict__ xin, const float *__restrict__ sx, int M, int K, int N,
+    const uint8_t *__restrict__ wpk, const float *__restrict__ sw, int sw_ld, uint16_t *__restrict__ out) {
+  __shared__ f32x4_t s_red[KS - 1][64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int KB = K >> 7;
+  const int nb = blockIdx.x;
+  const int kb_per = (KB + KS - 1) / KS;
+  const int kb_begin = wave * kb_per;
+  const int kb_end = min(KB, kb_begin + kb_per);
+  const int r = lane & 15, q = lane >> 4;
+  const bool rok = r < M;
+  const int64_t col = (int64_t)nb * 16 + r;  // C layout: column lane % 16, rows 4 q .. 4 q + 3
+  const uint8_t *const wp = wpk + (int64_t)nb * KB * 2048 + lane * 32;
+  // lhs fragment of MFMA step s: row r, k = 128 kb + 32 q + 8 s .. + 7
+  const uint8_t *const xrow = (const uint8_t *)xin + (int64_t)(rok ? r : 0) * K * (A8 ? 1 : 2) + 32 * q * (A8 ? 1 : 2);
+  u32x4_t wlo[D], whi[D];
+  auto load_w = [&](int slot, int kb) {
+    const u32x4_t *p = (const u32x4_t *)(wp + (int64_t)kb * 2048);
+    wlo[slot] = p[0];
+    whi[slot] = p[1];
+  };
+#pragma unroll
+  for (int d = 0; d < D; ++d)
+    if (kb_begin + d < kb_end) load_w(d, kb_begin + d);
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  for (int kb0 = kb_begin; kb0 < kb_end; kb0 += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const int kb = kb0 + d;
+      if (kb >= kb_end) break;
+      u32x4_t a[4];
+      if (rok) {
+        if (A8) {
+          const u32x4_t *xp = (const u32x4_t *)(xrow + (int64_t)kb * 128);
+          const u32x4_t v0 = xp[0], v1 = xp[1];
+#pragma unroll
+          for (int s = 0; s < 4; ++s) {
+            const uint32_t w0 = s < 2 ? v0[2 * s] : v1[2 * s - 4];
+            const uint32_t w1 = s < 2 ? v0[2 * s + 1] : v1[2 * s - 3];
+            a[s] = u32x4_t{cvt_fp8x2_bf16<false>(w0), cvt_fp8x2_bf16<true>(w0), cvt_fp8x2_bf16<false>(w1),
+                           cvt_fp8x2_bf16<true>(w1)};
+          }
+        } else {
+          const u32x4_t *xp = (const u32x4_t *)(xrow + (int64_t)kb * 256);
+#pragma unroll
+          for (int s = 0; s < 4; ++s) a[s] = xp[s];
+        }
+      } else {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) a[s] = u32x4_t{0u, 0u, 0u, 0u};
+      }
+      const u32x4_t lo = wlo[d], hi = whi[d];
+      if (kb + D < kb_end) load_w(d, kb + D);
+      f32x4_t part = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const uint32_t w0 = s < 2 ? lo[2 * s] : hi[2 * s - 4];
+        const uint32_t w1 = s < 2 ? lo[2 * s + 1] : hi[2 * s - 3];
+        const u32x4_t b = {cvt_fp8x2_bf16<false>(w0), cvt_fp8x2_bf16<true>(w0), cvt_fp8x2_bf16<false>(w1),
+                           cvt_fp8x2_bf16<true>(w1)};
+        part = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a[s]),
+                                                       __builtin_bit_cast(bf16x8_t, b), part, 0, 0, 0);
+      }
+      // acc += part * scale (f32 multiply, then f32 add)
+      const float wscale = A8 ? sw[(int64_t)kb * sw_ld + (col >> 7)] : sw[(int64_t)kb * sw_ld + col];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float f = wscale;
+        if (A8) {
+          const int m = min(4 * q + i, M - 1);
+          f = sx[(int64_t)m * KB + kb] * wscale;
+        }
+        acc[i] = acc[i] + part[i] * f;
+      }
+    }
+  }
+  if (wave > 0) s_red[wave - 1][lane] = acc;
+  __syncthreads();
+  if (wave > 0) return;
+#pragma unroll
+  for (int w = 0; w < KS - 1; ++w) acc = acc + s_red[w][lane];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int m = 4 * q + i;
+    if (m < M) out[(int64_t)m * N + col] = f32_to_bf16_bits(acc[i]);
+  }
+}
+
 // out = bf16(sum_{ks} partial[ks]) in split order.
 __global__ void dense_fp8_reduce_kernel(const float *partial, int ksplit, int64_t MN, uint16_t *out) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < MN; i += (int64_t)gridDim.x * blockDim.x) {
@@ -279,6 +377,13 @@ template <bool A8>
 static int run_dense(const void *x, const float *sx, int64_t M, int64_t K, int64_t N, const uint8_t *w,
                      const float *sw, int sw_ld, uint16_t *out, void *workspace, int64_t workspace_bytes,
                      hipStream_t st) {
+  if (M <= 16) {
+    // 16 waves split K, two weight steps in flight per wave (64 KB per
+    // block); measured fastest of 4/8/16 waves x 2/4/8 steps at K=7168, N=4096.
+    hipLaunchKernelGGL((dense_fp8_skinny_kernel<16, 2, A8>), dim3((unsigned)(N / 16)), dim3(1024), 0, st, x, sx,
+                       (int)M, (int)K, (int)N, w, sw, sw_ld, out);
+    return launch_status("dense_fp8");
+  }
   const DensePlan p = dense_plan(M, K, N);
   float *partial = nullptr;
   if (p.ksplit > 1) {
@@ -328,7 +433,7 @@ extern "C" int dwm_dense_fp8_workspace_size(int64_t M, int64_t K, int64_t N, int
   if (rc != DWM_OK) return rc;
   DWM_CHECK_ARG(bytes, "dense_fp8_workspace_size: null pointer");
   const DensePlan p = dense_plan(M, K, N);
-  *bytes = p.ksplit > 1 ? (int64_t)p.ksplit * M * N * 4 : 0;
+  *bytes = (M > 16 && p.ksplit > 1) ? (int64_t)p.ksplit * M * N * 4 : 0;
   return DWM_OK;
 }
 
