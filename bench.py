@@ -66,7 +66,8 @@ class GmmBench:
             w = self.weights[i]
             self.args.append((ctypes.c_void_p(self.lhs[i].data_ptr()), wl.M, wl.K, ctypes.c_void_p(w.weight.data_ptr()),
                               ctypes.c_void_p(w.scale.data_ptr()), ctypes.c_void_p(self.gs.data_ptr()), wl.E, None,
-                              wl.E, wl.N, ctypes.c_void_p(self.out[i].data_ptr()), _lib.BF16, 0, self.stream))
+                              wl.E, wl.N, ctypes.c_void_p(self.out[i].data_ptr()), _lib.BF16, 0, _lib.ACT_NONE,
+                              self.stream))
         self.fn = self.lib.dwm_gmm_fp4
 
     def step(self, i):
@@ -163,6 +164,45 @@ def bench_dispatch_combine(dev, steps, warmup):
     res["combine"] = {"ms": round(ms, 5), "GB_s": round(gb / (ms * 1e-3) / 1e9, 1), "T": wl.T, "topk": wl.topk,
                       "H": wl.N, "hbm_frac": round(gb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
     return res
+
+
+def bench_moe_block(dev, steps, warmup):
+    """The decode-size expert block through ``moe_block``: 256 tokens x top-8
+    over 32 experts (decode_gate_up routing), dispatch + row gather of hidden
+    [256, 7168] + gmm1 [2048, 7168] x [7168, 2x2048] with the fused
+    silu_and_mul_with_clamp (out [2048, 2048]) + gmm2 [2048, 2048] x
+    [2048, 7168] + combine to [256, 7168].  Two weight copies are rotated."""
+    import numpy as np
+    import torch
+    from dw_tpu_amd import fp4_weight_to_codes, moe_block
+    from dw_tpu_amd.workloads import make_gmm_workload
+    wl = make_gmm_workload("decode_gate_up", with_data=False)
+    H, I, E = wl.K, wl.N // 2, wl.E
+    rng = np.random.Generator(np.random.PCG64(12))
+    copies = 2
+    w13s, w2s = [], []
+    for _ in range(copies):
+        r13 = torch.randint(0, 256, (E, H, I), dtype=torch.uint8, device=dev)   # [E, H, 2I] packed
+        s13 = torch.randint(121, 130, (E, H // 32, 1, 2 * I), dtype=torch.uint8, device=dev)
+        w13s.append(fp4_weight_to_codes(r13, s13, gate_up=True))
+        r2 = torch.randint(0, 256, (E, I, H // 2), dtype=torch.uint8, device=dev)
+        s2 = torch.randint(118, 124, (E, I // 32, 1, H), dtype=torch.uint8, device=dev)
+        w2s.append(fp4_weight_to_codes(r2, s2))
+        del r13, s13, r2, s2
+    hidden = torch.from_numpy(rng.standard_normal((wl.T, H), dtype=np.float32)).to(torch.bfloat16).to(dev)
+    ids = torch.from_numpy(wl.topk_ids).to(dev)
+    wts = torch.from_numpy(wl.topk_weights).to(dev)
+    ms = time_steps(lambda i: moe_block(hidden, ids, wts, w13s[i % copies], w2s[i % copies], E), steps, warmup)
+    nonempty = int((wl.group_sizes > 0).sum())
+    n = wl.M
+    wbytes = nonempty * (H * 2 * I // 2 + H // 32 * 2 * I + I * H // 2 + I // 32 * H)
+    act_bytes = wl.T * H * 2 + n * H * 2 * 2 + n * I * 2 * 2 + n * H * 2 + wl.T * H * 2
+    flops = 2 * n * H * 2 * I + 2 * n * I * H
+    gbs = (wbytes + act_bytes) / (ms * 1e-3) / 1e9
+    return {"moe_block_decode": {"ms": round(ms, 5), "GB_s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+                                 "TFLOP_s": round(flops / (ms * 1e-3) / 1e12, 1), "bytes": wbytes + act_bytes,
+                                 "flops": flops, "T": wl.T, "topk": wl.topk, "H": H, "I": I, "E": E,
+                                 "nonempty_groups": nonempty}}
 
 
 def bench_dense(dev, steps, warmup, ms_list=(1, 16, 128, 1024, 4096)):
@@ -306,6 +346,9 @@ def main():
         torch.cuda.empty_cache()
         log("bench: dispatch / gather / combine")
         extra.update(bench_dispatch_combine(dev, args.steps, args.warmup))
+        log("bench: moe block (decode)")
+        extra.update(bench_moe_block(dev, args.steps, args.warmup))
+        torch.cuda.empty_cache()
         log("bench: dense fp8")
         extra.update(bench_dense(dev, args.steps, args.warmup))
     cpu = None

@@ -101,9 +101,13 @@ __global__ void fp4_decode_kernel(const uint8_t *packed, int format, int64_t nby
 
 // One thread per (e, g, kb, lane): the four 16-byte pieces of lane `lane` in
 // the two 64-deep steps of 128-deep step kb (both halves j) and its scale word.
+// With gate_up, packed column 64 g + 32 j + c takes source column
+// j * N/2 + 32 g + c: half 0 of every group is 32 gate columns and half 1 the
+// matching up columns of a [w1 | w3] weight, so the kernel's fused activation
+// finds both in one wave.
 __global__ void gmm_fp4_prepack_kernel(const uint8_t *rhs, int format, const void *scale,
                                        int scale_dtype, int64_t E, int64_t K, int64_t N,
-                                       uint8_t *wout, uint8_t *sout, int32_t *flags) {
+                                       uint8_t *wout, uint8_t *sout, int32_t *flags, int gate_up) {
   const int64_t G = (N + 63) / 64, KB = K / 128, T = K / 64;
   int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t total = E * G * KB * 64;
@@ -122,11 +126,12 @@ __global__ void gmm_fp4_prepack_kernel(const uint8_t *rhs, int format, const voi
   for (int f = 0; f < 2; ++f) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const int64_t n = g * 64 + 32 * j + c;
+      const int64_t np = g * 64 + 32 * j + c;  // packed column
+      const int64_t n = gate_up ? j * (N / 2) + 32 * g + c : np;
       const int64_t k0 = kb * 128 + 64 * f + 32 * h;
       uint32_t code = 127u;
       uint32_t words[4] = {0u, 0u, 0u, 0u};
-      if (n < N) {
+      if (np < N) {
         code = scale_to_code(scale, scale_dtype, (e * (K / 32) + (k0 >> 5)) * N + n, &bad_scale);
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
@@ -201,23 +206,36 @@ extern "C" int dwm_gmm_fp4_prepack_size(int64_t E, int64_t K, int64_t N, int64_t
   return DWM_OK;
 }
 
-extern "C" int dwm_gmm_fp4_prepack(const uint8_t *rhs, int format, const void *scale,
-                                   int scale_dtype, int64_t E, int64_t K, int64_t N,
-                                   uint8_t *weight_out, uint8_t *scale_out, int32_t *flags,
-                                   void *stream) {
+static int gmm_fp4_prepack_impl(const uint8_t *rhs, int format, const void *scale, int scale_dtype, int64_t E,
+                                int64_t K, int64_t N, uint8_t *weight_out, uint8_t *scale_out, int32_t *flags,
+                                int gate_up, void *stream) {
   int64_t wb, sb;
   int st = dwm_gmm_fp4_prepack_size(E, K, N, &wb, &sb);
   if (st != DWM_OK) return st;
   DWM_CHECK_ARG(format == DWM_FP4_E2M1 || format == DWM_FP4_CODES, "gmm_fp4_prepack: bad format %d", format);
   DWM_CHECK_ARG(scale_dtype == DWM_U8 || scale_dtype == DWM_F32 || scale_dtype == DWM_BF16,
                 "gmm_fp4_prepack: bad scale dtype %d", scale_dtype);
+  DWM_UNSUPPORTED_IF(gate_up && N % 64 != 0, "gmm_fp4_prepack_gate_up: N %% 64 == 0 required (N=%lld)",
+                     (long long)N);
   if (E == 0) return DWM_OK;
   DWM_CHECK_ARG(rhs && scale && weight_out && scale_out && flags, "gmm_fp4_prepack: null pointer");
   const int64_t total = E * ((N + 63) / 64) * (K / 128) * 64;
   const int64_t blocks = (total + 255) / 256;
   DWM_CHECK_ARG(blocks < (1ll << 31), "gmm_fp4_prepack: too large");
-  hipLaunchKernelGGL(gmm_fp4_prepack_kernel, dim3((unsigned)blocks), dim3(256), 0,
-                     as_stream(stream), rhs, format, scale, scale_dtype, E, K, N, weight_out,
-                     scale_out, flags);
+  hipLaunchKernelGGL(gmm_fp4_prepack_kernel, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream), rhs, format,
+                     scale, scale_dtype, E, K, N, weight_out, scale_out, flags, gate_up);
   return launch_status("gmm_fp4_prepack");
+}
+
+extern "C" int dwm_gmm_fp4_prepack(const uint8_t *rhs, int format, const void *scale,
+                                   int scale_dtype, int64_t E, int64_t K, int64_t N,
+                                   uint8_t *weight_out, uint8_t *scale_out, int32_t *flags,
+                                   void *stream) {
+  return gmm_fp4_prepack_impl(rhs, format, scale, scale_dtype, E, K, N, weight_out, scale_out, flags, 0, stream);
+}
+
+extern "C" int dwm_gmm_fp4_prepack_gate_up(const uint8_t *rhs, int format, const void *scale, int scale_dtype,
+                                           int64_t E, int64_t K, int64_t N, uint8_t *weight_out,
+                                           uint8_t *scale_out, int32_t *flags, void *stream) {
+  return gmm_fp4_prepack_impl(rhs, format, scale, scale_dtype, E, K, N, weight_out, scale_out, flags, 1, stream);
 }

@@ -23,6 +23,7 @@
 namespace dwm {
 
 constexpr int kMaxGroups = 1024;
+constexpr float kSwigluLimit = 10.0f;  // DeepSeek V4 swiglu_limit of silu_and_mul_with_clamp
 
 // Block-wide: exclusive row starts and row-tile starts of every group,
 // computed by wave 0.  s_tilestart[num_groups] receives the row-tile total.
@@ -167,7 +168,14 @@ __device__ __forceinline__ void ws_producer(const uint16_t *__restrict__ lhs, in
   __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
 }
 
-template <class C, int AM>
+// silu_and_mul_with_clamp on one (gate, up) accumulator pair, in f32.
+__device__ __forceinline__ float silu_mul_clamp(float gate, float up) {
+  const float g = fminf(gate, kSwigluLimit);
+  const float u = fminf(fmaxf(up, -kSwigluLimit), kSwigluLimit);
+  return g / (1.0f + expf(-g)) * u;
+}
+
+template <class C, int AM, bool ACT>
 __device__ __forceinline__ void ws_consumer(int T, const uint8_t *s_lds, int cw, int64_t row0, int rows,
                                             int64_t col0, int N, void *__restrict__ out, int out_f32) {
   constexpr int JW = C::JWAVE, GPC = JW / 2, NS = C::STAGES;
@@ -238,6 +246,28 @@ __device__ __forceinline__ void ws_consumer(int T, const uint8_t *s_lds, int cw,
     cur = nxt;
   }
   const int hrow = 4 * h;
+  if constexpr (ACT) {
+    // Fused activation: half 0 of each group is the gate, half 1 the up
+    // projection of the same 32 output columns (gate_up prepack), and the
+    // output has N / 2 columns.
+    static_assert(JW == 2, "one gate/up group per consumer wave");
+    const int64_t n_out = N / 2;
+    const int64_t col = col0 / 2 + c32;
+#pragma unroll
+    for (int mb = 0; mb < AM; ++mb) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int lrow = mb * 32 + 8 * (r >> 2) + hrow + (r & 3);
+        if (lrow < rows && col < n_out) {
+          const float v = silu_mul_clamp(acc[mb][0][r], acc[mb][1][r]);
+          const int64_t o = (row0 + lrow) * n_out + col;
+          if (out_f32) ((float *)out)[o] = v;
+          else ((uint16_t *)out)[o] = f32_to_bf16_bits(v);
+        }
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int mb = 0; mb < AM; ++mb) {
 #pragma unroll
@@ -257,7 +287,7 @@ __device__ __forceinline__ void ws_consumer(int T, const uint8_t *s_lds, int cw,
   }
 }
 
-template <class C, int MB>
+template <class C, int MB, bool ACT>
 __global__ __launch_bounds__(C::THREADS) void gmm_fp4_ws_kernel(
     const uint16_t *__restrict__ lhs, int64_t M, int K, const uint8_t *__restrict__ wpk,
     const uint8_t *__restrict__ spk, const int32_t *__restrict__ group_sizes, int num_groups,
@@ -313,10 +343,10 @@ __global__ __launch_bounds__(C::THREADS) void gmm_fp4_ws_kernel(
   const int64_t col0 = (int64_t)(g0 + wave * (C::JWAVE / 2)) * 64;
   // Every consumer runs exactly one barrier per K step (the producers' count),
   // whatever its row-block count.
-  if (act_mb <= 1 || MB == 1) ws_consumer<C, 1>(T, s_lds, wave, row0, rows, col0, N, out, out_f32);
-  else if (act_mb == 2 || MB == 2) ws_consumer<C, (MB >= 2 ? 2 : 1)>(T, s_lds, wave, row0, rows, col0, N, out, out_f32);
-  else if (act_mb == 3 || MB == 3) ws_consumer<C, (MB >= 3 ? 3 : 1)>(T, s_lds, wave, row0, rows, col0, N, out, out_f32);
-  else ws_consumer<C, MB>(T, s_lds, wave, row0, rows, col0, N, out, out_f32);
+  if (act_mb <= 1 || MB == 1) ws_consumer<C, 1, ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32);
+  else if (act_mb == 2 || MB == 2) ws_consumer<C, (MB >= 2 ? 2 : 1), ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32);
+  else if (act_mb == 3 || MB == 3) ws_consumer<C, (MB >= 3 ? 3 : 1), ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32);
+  else ws_consumer<C, MB, ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32);
 }
 
 // zero_initialize: zero rows outside [start(go), start(go + E_local)).
@@ -352,7 +382,7 @@ __global__ __launch_bounds__(256) void gmm_zero_rows_kernel(const int32_t *group
   }
 }
 
-template <int MB, int CW, int JW, int NP, int NS, bool PF>
+template <int MB, int CW, int JW, int NP, int NS, bool PF, bool ACT = false>
 static int launch_gmm_ws(const uint16_t *lhs, int64_t M, int64_t K, const uint8_t *w, const uint8_t *s,
                          const int32_t *gs, int ng, const int32_t *go, int64_t e_local, int64_t N, void *out,
                          int out_f32, hipStream_t st) {
@@ -363,7 +393,7 @@ static int launch_gmm_ws(const uint16_t *lhs, int64_t M, int64_t K, const uint8_
   const int64_t grid = (max_tiles + 7) / 8 * 8;
   DWM_UNSUPPORTED_IF(grid > (1ll << 31) - 1, "gmm_fp4: too many tiles (%lld)", (long long)grid);
   DWM_UNSUPPORTED_IF(K > (1 << 24), "gmm_fp4: K <= 2^24 required");
-  hipLaunchKernelGGL((gmm_fp4_ws_kernel<C, MB>), dim3((unsigned)grid), dim3(C::THREADS), 0, st, lhs, M, (int)K, w,
+  hipLaunchKernelGGL((gmm_fp4_ws_kernel<C, MB, ACT>), dim3((unsigned)grid), dim3(C::THREADS), 0, st, lhs, M, (int)K, w,
                      s, gs, ng, go, e_local, (int)N, out, out_f32);
   return launch_status("gmm_fp4");
 }
@@ -375,12 +405,15 @@ using namespace dwm;
 extern "C" int dwm_gmm_fp4(const uint16_t *lhs, int64_t M, int64_t K, const uint8_t *weight,
                            const uint8_t *scale, const int32_t *group_sizes, int num_groups,
                            const int32_t *group_offset, int64_t E_local, int64_t N, void *out,
-                           int out_dtype, int zero_init, void *stream) {
+                           int out_dtype, int zero_init, int fuse_act, void *stream) {
   clear_error();
   DWM_CHECK_ARG(M >= 0 && K > 0 && N > 0 && E_local >= 0 && num_groups >= 0,
                 "gmm_fp4: bad sizes M=%lld K=%lld N=%lld E_local=%lld groups=%d", (long long)M,
                 (long long)K, (long long)N, (long long)E_local, num_groups);
   DWM_CHECK_ARG(out_dtype == DWM_BF16 || out_dtype == DWM_F32, "gmm_fp4: bad out dtype %d", out_dtype);
+  DWM_CHECK_ARG(fuse_act == DWM_ACT_NONE || fuse_act == DWM_ACT_SILU_MUL_CLAMP, "gmm_fp4: bad fuse_act %d", fuse_act);
+  DWM_UNSUPPORTED_IF(fuse_act != DWM_ACT_NONE && N % 64 != 0, "gmm_fp4: fuse_act needs N %% 64 == 0 (N=%lld)",
+                     (long long)N);
   DWM_UNSUPPORTED_IF(K % 128 != 0 || N % 16 != 0, "gmm_fp4: K %% 128 == 0 and N %% 16 == 0 required");
   DWM_UNSUPPORTED_IF(num_groups > kMaxGroups, "gmm_fp4: at most %d groups (got %d)", kMaxGroups, num_groups);
   DWM_UNSUPPORTED_IF(K > (1 << 30) || N > (1 << 30), "gmm_fp4: K, N must be < 2^30");
@@ -392,8 +425,9 @@ extern "C" int dwm_gmm_fp4(const uint16_t *lhs, int64_t M, int64_t K, const uint
   hipStream_t st = as_stream(stream);
   const int elem = out_dtype == DWM_F32 ? 4 : 2;
   if (zero_init) {
+    const int64_t n_out = fuse_act != DWM_ACT_NONE ? N / 2 : N;
     hipLaunchKernelGGL(gmm_zero_rows_kernel, dim3((unsigned)((M + 63) / 64)), dim3(256), 0, st,
-                       group_sizes, num_groups, group_offset, E_local, M, N, out, elem);
+                       group_sizes, num_groups, group_offset, E_local, M, n_out, out, elem);
     int rc = launch_status("gmm_fp4 zero rows");
     if (rc != DWM_OK) return rc;
   }
@@ -403,6 +437,9 @@ extern "C" int dwm_gmm_fp4(const uint16_t *lhs, int64_t M, int64_t K, const uint
   // K stages (120 KB of LDS, 138 VGPRs: one block of 12 waves per CU).
   // Measured fastest on the decode and prefill workloads among the tile,
   // wave-split and pipeline-depth variants tried.
+  if (fuse_act == DWM_ACT_SILU_MUL_CLAMP)
+    return launch_gmm_ws<3, 8, 2, 4, 4, false, true>(lhs, M, K, weight, scale, group_sizes, num_groups,
+                                                     group_offset, E_local, N, out, out_f32, st);
   return launch_gmm_ws<3, 8, 2, 4, 4, false>(lhs, M, K, weight, scale, group_sizes, num_groups, group_offset,
                                              E_local, N, out, out_f32, st);
 }

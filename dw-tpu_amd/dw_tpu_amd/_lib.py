@@ -13,10 +13,11 @@ import torch
 LIB_NAME = "libdwtpu_moe.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
-# enum dwm_status / dwm_dtype / dwm_fp4_format
+# enum dwm_status / dwm_dtype / dwm_fp4_format / dwm_act
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_HIP = 0, 1, 2, 3
 BF16, F32, U8 = 0, 1, 2
 FP4_E2M1, FP4_CODES = 0, 1
+ACT_NONE, ACT_SILU_MUL_CLAMP = 0, 1
 
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int
@@ -30,7 +31,8 @@ SIGNATURES = {
     "dwm_fp4_decode": [_p, _i32, _i64, _p, _p, _p, _p],
     "dwm_gmm_fp4_prepack_size": [_i64, _i64, _i64, _p, _p],
     "dwm_gmm_fp4_prepack": [_p, _i32, _p, _i32, _i64, _i64, _i64, _p, _p, _p, _p],
-    "dwm_gmm_fp4": [_p, _i64, _i64, _p, _p, _p, _i32, _p, _i64, _i64, _p, _i32, _i32, _p],
+    "dwm_gmm_fp4_prepack_gate_up": [_p, _i32, _p, _i32, _i64, _i64, _i64, _p, _p, _p, _p],
+    "dwm_gmm_fp4": [_p, _i64, _i64, _p, _p, _p, _i32, _p, _i64, _i64, _p, _i32, _i32, _i32, _p],
     "dwm_moe_dispatch_workspace_size": [_i64, _i32, _p],
     "dwm_moe_dispatch": [_p, _i64, _i32, _i32, _p, _p, _p, _p, _p, _p, _p, _p],
     "dwm_row_gather": [_p, _i64, _i64, _p, _i64, _p, _p],

@@ -15,15 +15,16 @@ from .gmm_v2 import Fp4Weight, gmm_v2, prepack_fp4
 
 
 def fp4_weight_to_codes(weight: torch.Tensor, weight_scale: torch.Tensor,
-                        rhs_fp4_codes: bool = False) -> Fp4Weight:
+                        rhs_fp4_codes: bool = False, gate_up: bool = False) -> Fp4Weight:
     """Stored fp4 expert weight [E, K, N/2] (+ block scales) -> ``Fp4Weight``.
 
     The reference re-encodes e2m1 to uint4 codes here (exact); this build
     also relayouts into the kernel's K-major tiles (exact, same bytes).
+    ``gate_up``: a [w1 | w3] weight that gmm1 runs with the fused activation.
     """
     if isinstance(weight, Fp4Weight):
         return weight
-    return prepack_fp4(weight, weight_scale, rhs_fp4_codes=rhs_fp4_codes)
+    return prepack_fp4(weight, weight_scale, rhs_fp4_codes=rhs_fp4_codes, gate_up=gate_up)
 
 
 def gmm_wrapper(lhs, rhs, rhs_scale, rhs_bias, group_sizes, group_offset, fuse_act=None,

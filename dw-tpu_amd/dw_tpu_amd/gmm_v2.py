@@ -89,13 +89,16 @@ class Fp4Weight:
     """Prepacked fp4 expert weights [E, K, N] with e8m0 block-32 scales along K.
 
     ``weight`` and ``scale`` are uint8 device tensors in the kernel layout
-    (documented in dw-tpu_amd/csrc/fp4.hip).
+    (documented in dw-tpu_amd/csrc/fp4.hip).  ``gate_up`` weights ([w1 | w3]
+    with gate and up columns interleaved by the prepack) run only with the
+    fused ``silu_and_mul_with_clamp`` activation.
     """
     weight: torch.Tensor
     scale: torch.Tensor
     num_experts: int
     k: int
     n: int
+    gate_up: bool = False
 
     @property
     def shape(self):
@@ -106,14 +109,16 @@ class Fp4Weight:
         return self.weight.device
 
 
-def prepack_fp4(rhs: torch.Tensor, rhs_scale: torch.Tensor, rhs_fp4_codes: bool = False) -> Fp4Weight:
+def prepack_fp4(rhs: torch.Tensor, rhs_scale: torch.Tensor, rhs_fp4_codes: bool = False,
+                gate_up: bool = False) -> Fp4Weight:
     """One-time relayout of packed fp4 expert weights and their scales.
 
     rhs: [E, K, N/2] packed bytes -- e2m1 nibbles (uint8 or
     float4_e2m1fn_x2), or gmm_v2 codes when ``rhs_fp4_codes``.
     rhs_scale: [E, K/32, 1, N] or [E, K/32, N]: uint8 e8m0 codes, or f32 /
     bf16 powers of two (the lossless e8m0 set, e8m0_scale.py:25-34).
-    Synchronises the stream once to check the scales (load time).
+    ``gate_up``: rhs is a [w1 | w3] gate/up weight for the fused activation
+    (N % 64 == 0).  Synchronises the stream once to check the scales (load time).
     """
     if rhs_fp4_codes and rhs.dtype != torch.uint8:
         raise ValueError(f"rhs_fp4_codes expects uint4 rhs, got {rhs.dtype}.")
@@ -141,7 +146,8 @@ def prepack_fp4(rhs: torch.Tensor, rhs_scale: torch.Tensor, rhs_fp4_codes: bool 
     sout = torch.zeros(sb.value, dtype=torch.uint8, device=src.device)
     flags = torch.zeros(1, dtype=torch.int32, device=src.device)
     fmt = _lib.FP4_CODES if rhs_fp4_codes else _lib.FP4_E2M1
-    _lib.call("dwm_gmm_fp4_prepack", _lib.ptr(src), fmt, _lib.ptr(sc), _lib.dtype_code(sc.dtype), e, k, n,
+    entry = "dwm_gmm_fp4_prepack_gate_up" if gate_up else "dwm_gmm_fp4_prepack"
+    _lib.call(entry, _lib.ptr(src), fmt, _lib.ptr(sc), _lib.dtype_code(sc.dtype), e, k, n,
               _lib.ptr(wout), _lib.ptr(sout), _lib.ptr(flags), _lib.stream_handle(src.device))
     f = int(flags.item())
     if f & 1:
@@ -149,7 +155,7 @@ def prepack_fp4(rhs: torch.Tensor, rhs_scale: torch.Tensor, rhs_fp4_codes: bool 
                          "(code 255, a negative, subnormal or non-power-of-two scale)")
     if f & 2:
         raise ValueError("rhs holds uint4 code 8 (q = -8), which e2m1_to_codes never produces")
-    return Fp4Weight(wout, sout, e, k, n)
+    return Fp4Weight(wout, sout, e, k, n, gate_up)
 
 
 def gmm_v2(lhs: torch.Tensor,
@@ -176,12 +182,17 @@ def gmm_v2(lhs: torch.Tensor,
     device tensor (first local group).  Returns [M, N] in
     ``preferred_element_type`` (bf16 default, or float32).  Rows outside the
     local groups are zero when ``zero_initialize`` and unspecified otherwise.
-    Tiling / VMEM arguments of the TPU kernel are accepted and ignored.
+    ``fuse_act="silu_and_mul_with_clamp"``: rhs is a [w1 | w3] gate/up
+    weight (an ``Fp4Weight`` prepacked with ``gate_up=True``, or raw bytes
+    prepacked so per call) and the result is [M, N/2] =
+    silu(min(gate, 10)) * clip(up, -10, 10) of the f32 accumulators, rounded
+    once.  Tiling / VMEM arguments of the TPU kernel are accepted and ignored.
     """
     if rhs_bias is not None:
         raise NotImplementedError("gmm_v2: rhs_bias is not supported by the fp4 kernel")
-    if fuse_act is not None:
+    if fuse_act not in (None, "silu_and_mul_with_clamp"):
         raise NotImplementedError(f"gmm_v2: fused activation {fuse_act!r} is not supported")
+    fused = fuse_act is not None
     if transpose_rhs:
         raise NotImplementedError("gmm_v2: transpose_rhs is not supported")
     if lhs_quant_dtype is not None:
@@ -191,7 +202,10 @@ def gmm_v2(lhs: torch.Tensor,
             raise ValueError("gmm_v2: a prepacked Fp4Weight carries its own scales; pass rhs_scale=None")
         w = rhs
     else:
-        w = prepack_fp4(rhs, rhs_scale, rhs_fp4_codes=rhs_fp4_codes)
+        w = prepack_fp4(rhs, rhs_scale, rhs_fp4_codes=rhs_fp4_codes, gate_up=fused)
+    if w.gate_up != fused:
+        raise ValueError("gmm_v2: gate/up-prepacked weights run only (and always) with the fused activation"
+                         if w.gate_up else "gmm_v2: the fused activation needs weights prepacked with gate_up=True")
     out_dtype = lhs.dtype if preferred_element_type is None else preferred_element_type
     if lhs.dtype != torch.bfloat16:
         raise ValueError(f"gmm_v2: lhs must be bfloat16, got {lhs.dtype}")
@@ -213,8 +227,9 @@ def gmm_v2(lhs: torch.Tensor,
     else:
         go = group_offset.reshape(-1)[:1].to(device=dev, dtype=torch.int32).contiguous()
     m = lhs.shape[0]
-    out = torch.empty((m, w.n), dtype=out_dtype, device=dev)
+    out = torch.empty((m, w.n // 2 if fused else w.n), dtype=out_dtype, device=dev)
     _lib.call("dwm_gmm_fp4", _lib.ptr(lhs), m, w.k, _lib.ptr(w.weight), _lib.ptr(w.scale), _lib.ptr(gs),
               gs.numel(), _lib.ptr(go), w.num_experts, w.n, _lib.ptr(out), _lib.dtype_code(out_dtype),
-              1 if zero_initialize else 0, _lib.stream_handle(dev))
+              1 if zero_initialize else 0, _lib.ACT_SILU_MUL_CLAMP if fused else _lib.ACT_NONE,
+              _lib.stream_handle(dev))
     return out

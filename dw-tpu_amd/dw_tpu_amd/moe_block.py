@@ -1,0 +1,58 @@
+"""The routed-expert block around the FP4 gmm: dispatch, row gather, gmm1
+with the fused ``silu_and_mul_with_clamp`` activation, gmm2 and the
+routing-weighted combine -- the local (one-GPU) body of the reference's
+``moe_gmm_local`` (patches/tpu-inference-ext/0103-...:77-78 for gmm1 with the
+activation, 0106-...:239-250 for gmm2 and its f32 variant) with the fast
+dispatch / combine of moe_fast_dispatch.py:188-194 and
+moe_fast_combine.py:201-207.
+
+Rounding points follow the reference: gmm1 accumulates in f32 and the
+activation of the accumulators is rounded once to bf16 (fused-moe-fp4
+0901-...:420-423); gmm2 accumulates in f32 and rounds once (0901-...:446-449)
+or stays f32 (``f32_reduce``, 0106-...:243-250); the combine sums in f32 in
+top-k order and rounds once (moe_fast_combine.py:44-54).
+"""
+from dataclasses import dataclass
+
+import torch
+
+from .fused_moe_gmm import gmm_wrapper
+from .gmm_v2 import Fp4Weight, gmm_v2
+from .moe_fast_combine import fast_combine
+from .moe_fast_dispatch import moe_dispatch, row_gather
+
+
+@dataclass
+class MoeBlockOutputs:
+    """The block's result and its intermediates (device tensors)."""
+    out: torch.Tensor       # [T, H] combined
+    dispatch: object        # moe_fast_dispatch.Dispatch
+    x: torch.Tensor         # [T * topk, H] gathered rows (expert order)
+    h: torch.Tensor         # [T * topk, I] activation of gmm1 (bf16)
+    y: torch.Tensor         # [T * topk, H] gmm2 output (bf16 or f32)
+
+
+def moe_block(hidden: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.Tensor, w13: Fp4Weight,
+              w2: Fp4Weight, num_experts: int, group_offset=None, f32_reduce: bool = False,
+              return_intermediates: bool = False):
+    """hidden [T, H] bf16; topk_ids [T, topk] int32; topk_weights [T, topk]
+    f32 or bf16; w13: gate/up weights [E, H, 2I] prepacked with
+    ``gate_up=True``; w2: down weights [E, I, H].  Returns [T, H] bf16 (or
+    ``MoeBlockOutputs`` with ``return_intermediates``)."""
+    if not w13.gate_up:
+        raise ValueError("moe_block: w13 must be prepacked with gate_up=True")
+    if w13.k != hidden.shape[1] or w2.k != w13.n // 2 or w2.n != hidden.shape[1]:
+        raise ValueError(f"moe_block: shapes do not chain: hidden {tuple(hidden.shape)}, w13 {w13.shape}, w2 {w2.shape}")
+    topk = topk_ids.shape[1]
+    d = moe_dispatch(topk_ids, num_experts)
+    x = row_gather(hidden, d.token_indices_sorted)
+    h = gmm_wrapper(x, w13, None, None, d.group_sizes, group_offset, fuse_act="silu_and_mul_with_clamp")
+    # With a group_offset (an expert-parallel shard) rows of other shards'
+    # experts are zeroed before the combine, as the reference does
+    # (patches/tpu-inference-ext/0103-...:94-97: 0 * NaN would poison it).
+    y = gmm_v2(h, w2, d.group_sizes, group_offset=group_offset, zero_initialize=group_offset is not None,
+               preferred_element_type=torch.float32 if f32_reduce else None)
+    out = fast_combine(y, d.topk_argsort_revert_indices, topk_weights, topk, out_dtype=hidden.dtype)
+    if return_intermediates:
+        return MoeBlockOutputs(out, d, x, h, y)
+    return out

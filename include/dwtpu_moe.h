@@ -38,6 +38,15 @@ enum dwm_dtype {
   DWM_U8 = 2 /* e8m0 exponent codes for scales */
 };
 
+/* Activation fused into the grouped matmul's epilogue (gmm_v2 fuse_act). */
+enum dwm_act {
+  DWM_ACT_NONE = 0,
+  /* silu(min(gate, 10)) * clip(up, -10, 10) on the f32 accumulators, gate =
+   * columns [0, N/2) and up = [N/2, N) of a [w1 | w3] weight
+   * (patches/tpu-inference-experimental/fused-moe-fp4/0901-...:60-64). */
+  DWM_ACT_SILU_MUL_CLAMP = 1
+};
+
 /* Packed 4-bit weight formats (two per byte, element 2j in the low nibble). */
 enum dwm_fp4_format {
   DWM_FP4_E2M1 = 0, /* OCP e2m1 nibbles (torch float4_e2m1fn_x2 bytes) */
@@ -99,6 +108,16 @@ int dwm_gmm_fp4_prepack(const uint8_t *rhs, int format, const void *scale, int s
                         int64_t E, int64_t K, int64_t N, uint8_t *weight_out,
                         uint8_t *scale_out, int32_t *flags, void *stream);
 
+/* The same relayout for a gate/up weight [w1 | w3] (the GMM_EP
+ * [E, hidden, 2 * inter] layout, patches/tpu-inference-experimental/
+ * fused-moe-fp4/0901-...:250-254) that dwm_gmm_fp4 will run with
+ * DWM_ACT_SILU_MUL_CLAMP: gate and up columns are interleaved by 32 so each
+ * output column's pair is computed together.  Requires N % 64 == 0.  Such
+ * weights must be used with the fused activation. */
+int dwm_gmm_fp4_prepack_gate_up(const uint8_t *rhs, int format, const void *scale, int scale_dtype,
+                                int64_t E, int64_t K, int64_t N, uint8_t *weight_out,
+                                uint8_t *scale_out, int32_t *flags, void *stream);
+
 /* Ragged grouped matmul on prepacked weights:
  *   for g in [group_offset, group_offset + E_local):
  *     out[off_g : off_g + size_g] = lhs[off_g : off_g + size_g] @ dequant(rhs[g - group_offset])
@@ -115,11 +134,17 @@ int dwm_gmm_fp4_prepack(const uint8_t *rhs, int format, const void *scale, int s
  *   group_offset: device int32[1] or NULL (= 0).
  *   out_dtype:    DWM_BF16 or DWM_F32 (the MOE_F32_REDUCE variant,
  *                 patches/tpu-inference-ext/0106-...:243-250).
- * Requires K % 128 == 0, N % 16 == 0, num_groups <= 1024. */
+ *   fuse_act:     DWM_ACT_NONE, or DWM_ACT_SILU_MUL_CLAMP with weights from
+ *                 dwm_gmm_fp4_prepack_gate_up: out is then [M, N/2], the
+ *                 activation of the f32 accumulators rounded once (gmm_v2's
+ *                 fuse_act as gmm1 of moe_gmm_local uses it,
+ *                 patches/tpu-inference-ext/0103-...:77-78).
+ * Requires K % 128 == 0, N % 16 == 0 (N % 64 == 0 with fuse_act),
+ * num_groups <= 1024. */
 int dwm_gmm_fp4(const uint16_t *lhs, int64_t M, int64_t K, const uint8_t *weight,
                 const uint8_t *scale, const int32_t *group_sizes, int num_groups,
                 const int32_t *group_offset, int64_t E_local, int64_t N, void *out,
-                int out_dtype, int zero_init, void *stream);
+                int out_dtype, int zero_init, int fuse_act, void *stream);
 
 /* ---------------------------------------------------------------------- */
 /* MoE dispatch and combine.                                               */

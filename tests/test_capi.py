@@ -43,16 +43,23 @@ def _rc(name, *args):
 def test_gmm_argument_checks_need_no_gpu():
     null = None
     # K not a multiple of 64 -> unsupported (fail-closed fallback)
-    rc, msg = _rc("dwm_gmm_fp4", null, 8, 192, null, null, null, 4, null, 4, 64, null, _lib.BF16, 0, null)
+    rc, msg = _rc("dwm_gmm_fp4", null, 8, 192, null, null, null, 4, null, 4, 64, null, _lib.BF16, 0, 0, null)
     assert rc == _lib.ERR_UNSUPPORTED and "K" in msg
-    rc, msg = _rc("dwm_gmm_fp4", null, 8, 128, null, null, null, 4, null, 4, 64, null, 7, 0, null)
+    rc, msg = _rc("dwm_gmm_fp4", null, 8, 128, null, null, null, 4, null, 4, 64, null, 7, 0, 0, null)
     assert rc == _lib.ERR_INVALID and "dtype" in msg
-    rc, msg = _rc("dwm_gmm_fp4", null, 8, 128, null, null, null, 4, null, 4, 64, null, _lib.BF16, 0, null)
+    rc, msg = _rc("dwm_gmm_fp4", null, 8, 128, null, null, null, 4, null, 4, 64, null, _lib.BF16, 0, 0, null)
     assert rc == _lib.ERR_INVALID and "null" in msg
-    rc, _ = _rc("dwm_gmm_fp4", null, 0, 128, null, null, null, 4, null, 4, 64, null, _lib.BF16, 0, null)
+    rc, _ = _rc("dwm_gmm_fp4", null, 0, 128, null, null, null, 4, null, 4, 64, null, _lib.BF16, 0, 0, null)
     assert rc == _lib.OK  # M == 0: nothing to do
-    rc, msg = _rc("dwm_gmm_fp4", null, 8, 128, null, null, null, 2000, null, 4, 64, null, _lib.BF16, 0, null)
+    rc, msg = _rc("dwm_gmm_fp4", null, 8, 128, null, null, null, 2000, null, 4, 64, null, _lib.BF16, 0, 0, null)
     assert rc == _lib.ERR_UNSUPPORTED and "groups" in msg
+    rc, msg = _rc("dwm_gmm_fp4", null, 8, 128, null, null, null, 4, null, 4, 64, null, _lib.BF16, 0, 5, null)
+    assert rc == _lib.ERR_INVALID and "fuse_act" in msg
+    rc, msg = _rc("dwm_gmm_fp4", null, 8, 128, null, null, null, 4, null, 4, 80, null, _lib.BF16, 0,
+                  _lib.ACT_SILU_MUL_CLAMP, null)
+    assert rc == _lib.ERR_UNSUPPORTED and "fuse_act" in msg
+    rc, msg = _rc("dwm_gmm_fp4_prepack_gate_up", null, 0, null, _lib.U8, 1, 128, 80, null, null, null, null)
+    assert rc == _lib.ERR_UNSUPPORTED and "64" in msg
 
 
 def test_prepack_size_query():
