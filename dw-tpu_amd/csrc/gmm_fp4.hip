@@ -5,10 +5,13 @@
 // Work decomposition: a block owns one (local group, 96-row tile) x
 // (512-column tile).  Tiles are enumerated on the device from group_sizes (no
 // host sync): the tile total is (row tiles of every local group) x (column
-// tiles); empty groups own no tile and cost no weight traffic.  Blocks whose
-// index is equal mod 8 run on one XCD (the dispatcher's round robin), so each
-// XCD gets a contiguous run of tiles -- consecutive column tiles of the same
-// row tile -- and the group's lhs rows are shared in that XCD's L2.
+// tiles); empty groups own no tile and cost no weight traffic.  Tiles are
+// listed by cost class (32-row MFMA blocks holding rows, largest first) so
+// the dispatcher, which hands blocks to free CUs in index order, balances
+// multi-round launches.  Blocks whose index is equal mod 8 run on one XCD
+// (the dispatcher's round robin); each class is cut into one contiguous run
+// per XCD -- consecutive column tiles of the same row tile -- so the group's
+// lhs rows are shared in that XCD's L2.
 //
 // The block is warp-specialised (see the WsCfg comment): producer waves move
 // the lhs tile and the prepacked weights and scales (fp4.hip) from memory to
@@ -25,30 +28,48 @@ namespace dwm {
 constexpr int kMaxGroups = 1024;
 constexpr float kSwigluLimit = 10.0f;  // DeepSeek V4 swiglu_limit of silu_and_mul_with_clamp
 
-// Block-wide: exclusive row starts and row-tile starts of every group,
-// computed by wave 0.  s_tilestart[num_groups] receives the row-tile total.
-template <int MT>
-__device__ __forceinline__ void group_prefix(const int32_t *group_sizes, int num_groups, int go,
-                                             int64_t e_local, int *s_rowstart, int *s_tilestart) {
+// Row tiles are ordered by cost.  A local group of sz rows has sz / MT full
+// row tiles and, when sz % MT != 0, one partial tile; a row tile's class is
+// its count of 32-row MFMA blocks (1 .. MB), the full tiles' class being MB.
+// Wave 0 computes the exclusive row starts of every group and, per class
+// (index 0 = MB blocks, largest first), the exclusive prefix over groups of
+// that class's row tiles; s_cls[a * kClsStride + num_groups] is the class
+// total.
+constexpr int kClsStride = kMaxGroups + 1;
+
+template <int MB>
+__device__ __forceinline__ void tile_classes(const int32_t *group_sizes, int num_groups, int go, int64_t e_local,
+                                             int *s_rowstart, int *s_cls) {
+  constexpr int MT = 32 * MB;
   const int lane = threadIdx.x & 63;
   if ((threadIdx.x >> 6) == 0) {
-    int row_carry = 0, tile_carry = 0;
+    int row_carry = 0;
+    int carry[MB];
+#pragma unroll
+    for (int a = 0; a < MB; ++a) carry[a] = 0;
     for (int base = 0; base < num_groups; base += 64) {
       const int g = base + lane;
       int sz = g < num_groups ? group_sizes[g] : 0;
       sz = sz > 0 ? sz : 0;
       const bool local = g >= go && (int64_t)g < (int64_t)go + e_local;
-      const int nt = local ? (sz + MT - 1) / MT : 0;
+      const int n_full = local ? sz / MT : 0;
+      const int rem = local ? sz % MT : 0;
+      const int rem_cls = (rem + 31) >> 5;  // 0 when there is no partial tile
       const int ri = wave_inclusive_scan(sz);
-      const int ti = wave_inclusive_scan(nt);
-      if (g < num_groups) {
-        s_rowstart[g] = row_carry + ri - sz;
-        s_tilestart[g] = tile_carry + ti - nt;
-      }
+      if (g < num_groups) s_rowstart[g] = row_carry + ri - sz;
       row_carry += __shfl(ri, 63, 64);
-      tile_carry += __shfl(ti, 63, 64);
+#pragma unroll
+      for (int a = 0; a < MB; ++a) {
+        const int cnt = (a == 0 ? n_full : 0) + (rem_cls == MB - a ? 1 : 0);
+        const int ci = wave_inclusive_scan(cnt);
+        if (g < num_groups) s_cls[a * kClsStride + g] = carry[a] + ci - cnt;
+        carry[a] += __shfl(ci, 63, 64);
+      }
     }
-    if (lane == 0) s_tilestart[num_groups] = tile_carry;
+    if (lane == 0) {
+#pragma unroll
+      for (int a = 0; a < MB; ++a) s_cls[a * kClsStride + num_groups] = carry[a];
+    }
   }
 }
 
@@ -58,6 +79,11 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 // s_waitcnt immediate (gfx9 encoding): vmcnt <= vm, lgkmcnt == 0, expcnt untouched.
 __host__ __device__ constexpr int waitcnt_vm_lgkm0(int vm) { return (vm & 15) | ((vm >> 4) << 14) | (7 << 4); }
 
+// lhs tile rows hold 8 16-byte chunks; chunk c of row r sits at physical
+// chunk c ^ ((r >> 1) & 7), so that the 16 lanes of one LDS cycle (16
+// consecutive rows, one logical chunk) hit 16 distinct 16-byte bank groups.
+__device__ __forceinline__ int lhs_swizzle(int r) { return (r >> 1) & 7; }
+
 // ---------------------------------------------------------------------------
 // Warp-specialised tiles.
 //
@@ -65,11 +91,14 @@ __host__ __device__ constexpr int waitcnt_vm_lgkm0(int vm) { return (vm & 15) | 
 // (consumers, two per SIMD) each own 64 columns: they read the lhs tile and
 // their weight codes and scales from LDS, decode, and run the 32x32x16 MFMAs.
 // Waves 8..11 (producers, one per SIMD) only move data: global -> LDS loads
-// (global_load_lds) of the lhs tile, weights and scales, three 64-deep K
-// steps ahead through a four-stage LDS ring.  One workgroup barrier per step
-// hands a stage from producers to consumers and the previous one back.  Each
-// role issues one kind of memory operation, so the compiler's waits stay
-// exact, and the consumers carry no load rings in registers.
+// (global_load_lds) of the lhs tile, weights and scales through a ring of LDS
+// stages.  One workgroup barrier per 64-deep K step publishes two steps
+// (t and t + 1) to the consumers and hands the stage of step t - 1 back to
+// the producers.  Each role issues one kind of memory operation, so the
+// compiler's waits stay exact, and the consumers carry no load rings in
+// registers.  The consumers read step t + 1's weights, scales and first lhs
+// fragments during step t, and each group of MFMAs' lhs fragments during the
+// previous group, so no MFMA waits on a fresh LDS read.
 //
 // Weight layout (64-column groups): for expert e, group g (columns 64 g ..
 // 64 g + 63, N padded to a multiple of 64 with zero codes), 64-deep K step t
@@ -81,47 +110,54 @@ __host__ __device__ constexpr int waitcnt_vm_lgkm0(int vm) { return (vm & 15) | 
 // k = 64 t + 32 h + 8 s .. + 7 and the lhs chunk with the same k.
 // Block shape: CW consumer waves owning JW 32-column blocks each (a tile of
 // 32 JW CW columns = GT 64-column groups), NP producer waves, NS LDS stages.
-// With PF the producers publish steps t and t + 1 at the barrier of step t
-// and the consumers read step t + 1's weights ahead; without it only step t.
-template <int MB, int CW, int JW, int NP, int NS, bool PF>
+template <int MB, int CW, int JW, int NP, int NS>
 struct WsCfg {
   static constexpr int CONS = CW, JWAVE = JW, NPROD = NP, STAGES = NS;
-  static constexpr bool PREFETCH = PF;
   static constexpr int GT = JW * CW / 2;                 // 64-column groups per tile
   static constexpr int THREADS = 64 * (CW + NP);
   static constexpr int NT = 64 * GT;
-  static constexpr int A = 0;                           // 32 MB rows x 128 bytes (8 XOR-swizzled 16-byte chunks)
+  static constexpr int A = 0;                           // 32 MB rows x 128 bytes (8 swizzled 16-byte chunks)
   static constexpr int W = 32 * MB * 128;               // group i of the tile: 2 KiB at W + 2048 i
   static constexpr int S = W + GT * 2048;               // group i: 256 bytes at S + 256 i
   static constexpr int STAGE = S + GT * 256;
-  static constexpr int A_LOADS = 4 * MB / NP;           // 1 KiB lhs loads per producer per step
+  static constexpr int A_LOADS = 4 * MB / NP;           // 1 KiB lhs loads (8 rows) per producer per step
   static constexpr int G_LOADS = GT / NP;               // groups per producer
-  static constexpr int LOADS = A_LOADS + 3 * G_LOADS;   // + (2 weight + 1 scale) per group
-  static constexpr int AHEAD = PF ? 2 : 1;              // steps published per barrier
-  static constexpr int PENDING = LOADS * (NS - 1 - AHEAD);
+  static constexpr int AHEAD = 2;                       // steps published per barrier
+  static constexpr int EP_STRIDE = 72;                  // epilogue staging row stride (floats)
   static_assert(A_LOADS * NP == 4 * MB && G_LOADS * NP == GT, "loads split evenly over the producers");
-  static_assert(PENDING < 64 && NS - 1 - AHEAD >= 1, "vmcnt range / stage count");
-  static_assert(JW % 2 == 0, "consumers own whole 64-column groups");
+  static_assert(NS - 1 - AHEAD >= 1, "stage count");
+  static_assert(JW == 2, "one 64-column group per consumer wave");
+  static_assert(CW * 32 * EP_STRIDE * 4 <= NS * STAGE, "epilogue staging fits the stages");
 };
 
-template <class C, int MB>
+// Producer wave pw: NA of its A_LOADS lhs row groups hold rows of the tile;
+// the others are zero in every stage and never loaded.
+template <class C, int NA>
 __device__ __forceinline__ void ws_producer(const uint16_t *__restrict__ lhs, int64_t row0, int rows, int K, int T,
                                             int KB, const uint8_t *__restrict__ wexp,
                                             const uint8_t *__restrict__ sexp, int g0, int G, uint8_t *s_lds,
                                             int pw) {
-  constexpr int NP = C::NPROD;
+  constexpr int NP = C::NPROD, NS = C::STAGES;
+  constexpr int LOADS = NA + 3 * C::G_LOADS;
+  constexpr int PENDING = LOADS * (NS - 1 - C::AHEAD);
+  static_assert(PENDING < 64, "vmcnt range");
   const int lane = threadIdx.x & 63;
-  // lhs load i of producer pw: rows 8 (pw + NP i) .. + 7 of the tile; lane l
-  // fills physical chunk l % 8 of row + l / 8 with logical chunk
-  // (l % 8) ^ (row % 8).  Rows past the tile repeat its last row (every load
-  // keeps all lanes, so each step issues the same number of loads).
-  const uint8_t *const abase = (const uint8_t *)(lhs + row0 * K);
-  uint32_t aoff[C::A_LOADS];
+  // Row groups pw + NP i, i >= NA, lie past the tile's rows: zero them.
 #pragma unroll
-  for (int i = 0; i < C::A_LOADS; ++i) {
+  for (int i = NA; i < C::A_LOADS; ++i)
+#pragma unroll
+    for (int st = 0; st < NS; ++st)
+      *(u32x4_t *)(s_lds + st * C::STAGE + C::A + (pw + NP * i) * 1024 + lane * 16) = u32x4_t{0u, 0u, 0u, 0u};
+  // lhs load i: rows 8 (pw + NP i) .. + 7 of the tile; lane l fills physical
+  // chunk l % 8 of row + l / 8 with logical chunk (l % 8) ^ swizzle(row).
+  // Rows past the tile repeat its last row.
+  const uint8_t *const abase = (const uint8_t *)(lhs + row0 * K);
+  uint32_t aoff[NA > 0 ? NA : 1];
+#pragma unroll
+  for (int i = 0; i < NA; ++i) {
     const int r = 8 * (pw + NP * i) + (lane >> 3);
     const int rs = r < rows ? r : rows - 1;
-    aoff[i] = (uint32_t)rs * (uint32_t)K * 2u + ((((lane & 7) ^ (r & 7))) << 4);
+    aoff[i] = (uint32_t)rs * (uint32_t)K * 2u + ((((lane & 7) ^ lhs_swizzle(r))) << 4);
   }
   const uint8_t *wsrc[C::G_LOADS];
   const uint8_t *ssrc[C::G_LOADS];
@@ -135,7 +171,7 @@ __device__ __forceinline__ void ws_producer(const uint16_t *__restrict__ lhs, in
     uint8_t *const st = s_lds + stage * C::STAGE;
     const uint8_t *const a = abase + (int64_t)t * 128;
 #pragma unroll
-    for (int i = 0; i < C::A_LOADS; ++i)
+    for (int i = 0; i < NA; ++i)
       __builtin_amdgcn_global_load_lds((const void *)(a + aoff[i]),
                                        (lds_void_t *)(st + C::A + (pw + NP * i) * 1024), 16, 0, 0);
 #pragma unroll
@@ -149,14 +185,13 @@ __device__ __forceinline__ void ws_producer(const uint16_t *__restrict__ lhs, in
                                        (lds_void_t *)(st + C::S + gi * 256), 4, 0, 0);
     }
   };
-  constexpr int NS = C::STAGES;
 #pragma unroll
   for (int t = 0; t < NS - 1; ++t) issue(t, min(t, T - 1));
   int refill = NS - 1;  // stage of step t + NS - 1
   for (int t = 0; t < T; ++t) {
     // Steps t .. t + AHEAD - 1 have landed once at most the loads of the
     // later steps are pending.
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(C::PENDING));
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(PENDING));
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
@@ -165,7 +200,10 @@ __device__ __forceinline__ void ws_producer(const uint16_t *__restrict__ lhs, in
     issue(refill, min(t + NS - 1, T - 1));
     refill = refill == NS - 1 ? 0 : refill + 1;
   }
+  // Every load has landed before the stages are reused for the epilogue.
   __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
 }
 
 // silu_and_mul_with_clamp on one (gate, up) accumulator pair, in f32.
@@ -175,10 +213,30 @@ __device__ __forceinline__ float silu_mul_clamp(float gate, float up) {
   return g / (1.0f + expf(-g)) * u;
 }
 
+// Stores 8 consecutive output values of one row (16-byte bf16 or 2 x 16-byte f32 stores).
+__device__ __forceinline__ void store8(void *__restrict__ out, int64_t o, const float *v, int out_f32) {
+  if (out_f32) {
+    u32x4_t lo, hi;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      lo[i] = __builtin_bit_cast(uint32_t, v[i]);
+      hi[i] = __builtin_bit_cast(uint32_t, v[4 + i]);
+    }
+    *(u32x4_t *)((float *)out + o) = lo;
+    *(u32x4_t *)((float *)out + o + 4) = hi;
+  } else {
+    u32x4_t p;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      p[i] = (uint32_t)f32_to_bf16_bits(v[2 * i]) | ((uint32_t)f32_to_bf16_bits(v[2 * i + 1]) << 16);
+    *(u32x4_t *)((uint16_t *)out + o) = p;
+  }
+}
+
 template <class C, int AM, bool ACT>
-__device__ __forceinline__ void ws_consumer(int T, const uint8_t *s_lds, int cw, int64_t row0, int rows,
+__device__ __forceinline__ void ws_consumer(int T, uint8_t *s_lds, int cw, int64_t row0, int rows,
                                             int64_t col0, int N, void *__restrict__ out, int out_f32) {
-  constexpr int JW = C::JWAVE, GPC = JW / 2, NS = C::STAGES;
+  constexpr int JW = C::JWAVE, NS = C::STAGES;
   const int lane = threadIdx.x & 63, c32 = lane & 31, h = lane >> 5;
   f32x16_t acc[AM][JW];
 #pragma unroll
@@ -188,20 +246,21 @@ __device__ __forceinline__ void ws_consumer(int T, const uint8_t *s_lds, int cw,
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[mb][j][r] = 0.0f;
   const int arow = C::A + c32 * 128;
-  const int x = c32 & 7;
-  const int woff = C::W + cw * GPC * 2048 + lane * 16;
-  const int soff = C::S + cw * GPC * 256 + lane * 4;
-  // With PREFETCH the weights and scales of step t + 1 (published at the
-  // barrier of step t) are read one step ahead.
-  u32x4_t wn[JW];
-  uint32_t sn[GPC];
-  auto read_ws = [&](const uint8_t *st) {
+  const int x = lhs_swizzle(c32);  // rows mb * 32 + c32 share it
+  const int woff = C::W + cw * 2048 + lane * 16;
+  const int soff = C::S + cw * 256 + lane * 4;
+  // Next step's weights and scales, and the lhs fragments of the next MFMA group.
+  u32x4_t wn[JW], an[AM];
+  uint32_t sn;
+  auto read_w = [&](const uint8_t *st) {
+    wn[0] = *(const u32x4_t *)(st + woff);
+    wn[1] = *(const u32x4_t *)(st + woff + 1024);
+    sn = *(const uint32_t *)(st + soff);
+  };
+  auto read_a = [&](const uint8_t *st, int s) {
+    const int ach = (((4 * h + s) ^ x) << 4);
 #pragma unroll
-    for (int gl = 0; gl < GPC; ++gl) {
-      wn[2 * gl] = *(const u32x4_t *)(st + woff + gl * 2048);
-      wn[2 * gl + 1] = *(const u32x4_t *)(st + woff + gl * 2048 + 1024);
-      sn[gl] = *(const uint32_t *)(st + soff + gl * 256);
-    }
+    for (int mb = 0; mb < AM; ++mb) an[mb] = *(const u32x4_t *)(st + arow + mb * 32 * 128 + ach);
   };
   int cur = 0;  // stage of step t
   for (int t = 0; t < T; ++t) {
@@ -211,20 +270,32 @@ __device__ __forceinline__ void ws_consumer(int T, const uint8_t *s_lds, int cw,
     asm volatile("" ::: "memory");
     const uint8_t *const st = s_lds + cur * C::STAGE;
     const int nxt = cur == NS - 1 ? 0 : cur + 1;
-    if (!C::PREFETCH || t == 0) read_ws(st);
+    // Step t + 1 was published at this barrier and its stage is not refilled
+    // before the next one.  In the last step the reads of "step T" fetch
+    // stale stage contents that are never used.
+    const uint8_t *const sx = s_lds + nxt * C::STAGE;
+    if (t == 0) {
+      read_w(st);
+      read_a(st, 0);
+    }
     u32x4_t w[JW];
     float sc[JW];
-#pragma unroll
-    for (int gl = 0; gl < GPC; ++gl) {
-      w[2 * gl] = wn[2 * gl];
-      w[2 * gl + 1] = wn[2 * gl + 1];
-      const uint32_t sd = sn[gl] >> (16 * (t & 1));
-      sc[2 * gl] = e8m0_to_f32(sd & 0xFFu);
-      sc[2 * gl + 1] = e8m0_to_f32((sd >> 8) & 0xFFu);
+    w[0] = wn[0];
+    w[1] = wn[1];
+    {
+      const uint32_t sd = sn >> (16 * (t & 1));
+      sc[0] = e8m0_to_f32(sd & 0xFFu);
+      sc[1] = e8m0_to_f32((sd >> 8) & 0xFFu);
     }
-    if (C::PREFETCH && t + 1 < T) read_ws(s_lds + nxt * C::STAGE);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
+      u32x4_t a[AM];
+#pragma unroll
+      for (int mb = 0; mb < AM; ++mb) a[mb] = an[mb];
+      __builtin_amdgcn_sched_barrier(0);
+      if (s < 3) read_a(st, s + 1);
+      else read_a(sx, 0);
+      if (s == 0) read_w(sx);
       u32x4_t b[JW];
 #pragma unroll
       for (int j = 0; j < JW; ++j) {
@@ -233,56 +304,60 @@ __device__ __forceinline__ void ws_consumer(int T, const uint8_t *s_lds, int cw,
         b[j][2] = cvt_fp4x2_bf16<2>(w[j][s], sc[j]);
         b[j][3] = cvt_fp4x2_bf16<3>(w[j][s], sc[j]);
       }
-      const int ach = (((4 * h + s) ^ x) << 4);
 #pragma unroll
-      for (int mb = 0; mb < AM; ++mb) {
-        const u32x4_t a = *(const u32x4_t *)(st + arow + mb * 32 * 128 + ach);
+      for (int mb = 0; mb < AM; ++mb)
 #pragma unroll
         for (int j = 0; j < JW; ++j)
-          acc[mb][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+          acc[mb][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a[mb]),
                                                                __builtin_bit_cast(bf16x8_t, b[j]), acc[mb][j], 0, 0, 0);
-      }
+      __builtin_amdgcn_sched_barrier(0);
     }
     cur = nxt;
   }
-  const int hrow = 4 * h;
-  if constexpr (ACT) {
-    // Fused activation: half 0 of each group is the gate, half 1 the up
-    // projection of the same 32 output columns (gate_up prepack), and the
-    // output has N / 2 columns.
-    static_assert(JW == 2, "one gate/up group per consumer wave");
-    const int64_t n_out = N / 2;
-    const int64_t col = col0 / 2 + c32;
-#pragma unroll
-    for (int mb = 0; mb < AM; ++mb) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int lrow = mb * 32 + 8 * (r >> 2) + hrow + (r & 3);
-        if (lrow < rows && col < n_out) {
-          const float v = silu_mul_clamp(acc[mb][0][r], acc[mb][1][r]);
-          const int64_t o = (row0 + lrow) * n_out + col;
-          if (out_f32) ((float *)out)[o] = v;
-          else ((uint16_t *)out)[o] = f32_to_bf16_bits(v);
-        }
-      }
-    }
-    return;
-  }
+  // One more barrier: every wave is done with the stages and every load has
+  // landed, so each consumer stages its results in a private LDS region and
+  // writes whole 8-column runs of a row.
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  constexpr int ES = C::EP_STRIDE;
+  float *const ep = (float *)(s_lds + cw * 32 * ES * 4);
+  constexpr int CO = ACT ? 32 : 64;  // output columns of this wave
+  const int64_t n_out = ACT ? N / 2 : N;
+  const int64_t ocol0 = ACT ? col0 / 2 : col0;
 #pragma unroll
   for (int mb = 0; mb < AM; ++mb) {
+    // The 32x32 accumulator layout: register r of lane (c32, h) is row
+    // 8 (r / 4) + 4 h + r % 4, column c32.
 #pragma unroll
-    for (int j = 0; j < JW; ++j) {
-      const int64_t col = col0 + 32 * j + c32;
-      if (col >= N) continue;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int lrow = mb * 32 + 8 * (r >> 2) + hrow + (r & 3);
-        if (lrow < rows) {
-          const int64_t o = (row0 + lrow) * N + col;
-          if (out_f32) ((float *)out)[o] = acc[mb][j][r];
-          else ((uint16_t *)out)[o] = f32_to_bf16_bits(acc[mb][j][r]);
-        }
+    for (int r = 0; r < 16; ++r) {
+      const int lr = 8 * (r >> 2) + 4 * h + (r & 3);
+      if constexpr (ACT) {
+        // Half 0 of the group is the gate, half 1 the up projection of the
+        // same 32 output columns (gate_up prepack).
+        ep[lr * ES + c32] = silu_mul_clamp(acc[mb][0][r], acc[mb][1][r]);
+      } else {
+        ep[lr * ES + c32] = acc[mb][0][r];
+        ep[lr * ES + 32 + c32] = acc[mb][1][r];
       }
+    }
+    // Lane q of chunk i covers row q / (CO / 8), columns 8 (q % (CO / 8)) .. + 7.
+#pragma unroll
+    for (int i = 0; i < 32 * CO / 8 / 64; ++i) {
+      const int q = lane + 64 * i;
+      const int lr = q / (CO / 8), c8 = q % (CO / 8);
+      const int row = mb * 32 + lr;
+      const int64_t col = ocol0 + 8 * c8;
+      float v[8];
+      const f32x4_t lo = *(const f32x4_t *)(ep + lr * ES + 8 * c8);
+      const f32x4_t hi = *(const f32x4_t *)(ep + lr * ES + 8 * c8 + 4);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        v[k] = lo[k];
+        v[4 + k] = hi[k];
+      }
+      if (row < rows && col < n_out) store8(out, (row0 + row) * n_out + col, v, out_f32);
     }
   }
 }
@@ -296,38 +371,61 @@ __global__ __launch_bounds__(C::THREADS) void gmm_fp4_ws_kernel(
   constexpr int MT = 32 * MB;
   constexpr int NT = C::NT;
   constexpr int CW = C::CONS;
-  static_assert(C::STAGE >= (2 * kMaxGroups + 1) * 4, "group prefix aliases the first stage");
+  static_assert(C::STAGES * C::STAGE >= (kMaxGroups + MB * kClsStride) * 4, "tile classes alias the stages");
   __shared__ __attribute__((aligned(1024))) uint8_t s_lds[C::STAGES * C::STAGE];
   __shared__ int s_info[3];
   int *s_rowstart = (int *)s_lds;
-  int *s_tilestart = s_rowstart + kMaxGroups;
+  int *s_cls = s_rowstart + kMaxGroups;
 
   const int tid = threadIdx.x, wave = tid >> 6;
   const int go = group_offset ? group_offset[0] : 0;
-  group_prefix<MT>(group_sizes, num_groups, go, e_local, s_rowstart, s_tilestart);
+  tile_classes<MB>(group_sizes, num_groups, go, e_local, s_rowstart, s_cls);
   if (tid == 0) s_info[0] = -1;
   __syncthreads();
+  // Work list: the (row tile, column tile) pairs of class 0 (MB blocks), then
+  // class 1, ... (longest first, so the dispatcher's in-order refill of free
+  // CUs balances them).  Each class is cut into 8 contiguous runs, one per
+  // XCD (blocks equal mod 8 run on one XCD), so a row tile's column tiles
+  // share that XCD's L2.
   const int n_tiles = (N + NT - 1) / NT;
-  const int64_t total = (int64_t)s_tilestart[num_groups] * n_tiles;
-  const int64_t per_xcd = (total + 7) / 8;
-  const int64_t j_x = blockIdx.x >> 3;
-  const int64_t t = (int64_t)(blockIdx.x & 7) * per_xcd + j_x;
-  const bool has_tile = j_x < per_xcd && t < total;
-  if (has_tile) {
-    const int trow = (int)(t / n_tiles);
-    for (int g = tid; g < num_groups; g += C::THREADS) {
-      if (s_tilestart[g] <= trow && trow < s_tilestart[g + 1]) {
-        const int tt = trow - s_tilestart[g];
-        s_info[0] = g;
-        s_info[1] = s_rowstart[g] + tt * MT;
-        s_info[2] = min(MT, group_sizes[g] - tt * MT);
+  const int xcd = blockIdx.x & 7;
+  int64_t j = blockIdx.x >> 3;
+  int cls = -1;
+  int64_t entry = 0;
+#pragma unroll
+  for (int a = 0; a < MB; ++a) {
+    const int64_t n_a = (int64_t)s_cls[a * kClsStride + num_groups] * n_tiles;
+    const int64_t per = (n_a + 7) / 8;
+    const int64_t lo = xcd * per, hi = min(lo + per, n_a);
+    const int64_t len = hi > lo ? hi - lo : 0;
+    if (cls < 0) {
+      if (j < len) {
+        cls = a;
+        entry = lo + j;
+      } else {
+        j -= len;
       }
     }
   }
-  __syncthreads();  // also retires the prefix reads before the stages overwrite them
+  const int trow = cls >= 0 ? (int)(entry / n_tiles) : -1;
+  if (cls >= 0) {
+    const int *const cs = s_cls + cls * kClsStride;
+    for (int g = tid; g < num_groups; g += C::THREADS) {
+      if (cs[g] <= trow && trow < cs[g + 1]) {
+        const int sz = group_sizes[g];
+        // Class 0 holds the full tiles (then a partial one of MB blocks);
+        // the other classes hold one partial tile per group.
+        const int tt = cls == 0 ? trow - cs[g] : sz / MT;
+        s_info[0] = g;
+        s_info[1] = s_rowstart[g] + tt * MT;
+        s_info[2] = min(MT, sz - tt * MT);
+      }
+    }
+  }
+  __syncthreads();  // also retires the class reads before the stages overwrite them
   const int g = s_info[0];
-  if (!has_tile || g < 0) return;
-  const int nt = (int)(t % n_tiles);
+  if (cls < 0 || g < 0) return;
+  const int nt = (int)(entry % n_tiles);
   const int64_t row0 = s_info[1];
   if (row0 >= M) return;
   const int rows = (int)min((int64_t)s_info[2], M - row0);
@@ -335,13 +433,20 @@ __global__ __launch_bounds__(C::THREADS) void gmm_fp4_ws_kernel(
   const int T = K >> 6, KB = K >> 7, G = (N + 63) >> 6;
   const int g0 = nt * C::GT;  // first 64-column group of the tile
   if (wave >= CW) {
-    ws_producer<C, MB>(lhs, row0, rows, K, T, KB, wpk + e * G * T * 2048, spk + e * G * KB * 256, g0, G, s_lds,
-                       wave - CW);
+    const int pw = wave - CW;
+    const uint8_t *const wexp = wpk + e * G * T * 2048;
+    const uint8_t *const sexp = spk + e * G * KB * 256;
+    // Row groups pw + NP i with 8 (pw + NP i) < rows are loaded.
+    const int na = min(C::A_LOADS, (rows + 8 * C::NPROD - 1 - 8 * pw) / (8 * C::NPROD));
+    if (na >= C::A_LOADS) ws_producer<C, C::A_LOADS>(lhs, row0, rows, K, T, KB, wexp, sexp, g0, G, s_lds, pw);
+    else if (na == 2) ws_producer<C, (C::A_LOADS > 2 ? 2 : C::A_LOADS)>(lhs, row0, rows, K, T, KB, wexp, sexp, g0, G, s_lds, pw);
+    else if (na == 1) ws_producer<C, (C::A_LOADS > 1 ? 1 : C::A_LOADS)>(lhs, row0, rows, K, T, KB, wexp, sexp, g0, G, s_lds, pw);
+    else ws_producer<C, 0>(lhs, row0, rows, K, T, KB, wexp, sexp, g0, G, s_lds, pw);
     return;
   }
   const int act_mb = (rows + 31) >> 5;
-  const int64_t col0 = (int64_t)(g0 + wave * (C::JWAVE / 2)) * 64;
-  // Every consumer runs exactly one barrier per K step (the producers' count),
+  const int64_t col0 = (int64_t)(g0 + wave) * 64;
+  // Every consumer runs exactly T + 1 barriers (the producers' count),
   // whatever its row-block count.
   if (act_mb <= 1 || MB == 1) ws_consumer<C, 1, ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32);
   else if (act_mb == 2 || MB == 2) ws_consumer<C, (MB >= 2 ? 2 : 1), ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32);
@@ -382,15 +487,16 @@ __global__ __launch_bounds__(256) void gmm_zero_rows_kernel(const int32_t *group
   }
 }
 
-template <int MB, int CW, int JW, int NP, int NS, bool PF, bool ACT = false>
+template <int MB, int CW, int JW, int NP, int NS, bool ACT = false>
 static int launch_gmm_ws(const uint16_t *lhs, int64_t M, int64_t K, const uint8_t *w, const uint8_t *s,
                          const int32_t *gs, int ng, const int32_t *go, int64_t e_local, int64_t N, void *out,
                          int out_f32, hipStream_t st) {
-  using C = WsCfg<MB, CW, JW, NP, NS, PF>;
+  using C = WsCfg<MB, CW, JW, NP, NS>;
   constexpr int MT = 32 * MB, NT = C::NT;
   const int64_t n_tiles = (N + NT - 1) / NT;
   const int64_t max_tiles = ((M + MT - 1) / MT + e_local) * n_tiles;
-  const int64_t grid = (max_tiles + 7) / 8 * 8;
+  // Per XCD at most ceil(n_a / 8) tiles of each class: <= max_tiles / 8 + MB.
+  const int64_t grid = ((max_tiles + 7) / 8 + MB) * 8;
   DWM_UNSUPPORTED_IF(grid > (1ll << 31) - 1, "gmm_fp4: too many tiles (%lld)", (long long)grid);
   DWM_UNSUPPORTED_IF(K > (1 << 24), "gmm_fp4: K <= 2^24 required");
   hipLaunchKernelGGL((gmm_fp4_ws_kernel<C, MB, ACT>), dim3((unsigned)grid), dim3(C::THREADS), 0, st, lhs, M, (int)K, w,
@@ -420,8 +526,9 @@ extern "C" int dwm_gmm_fp4(const uint16_t *lhs, int64_t M, int64_t K, const uint
   if (M == 0) return DWM_OK;
   DWM_CHECK_ARG(lhs && out && (num_groups == 0 || group_sizes), "gmm_fp4: null pointer");
   DWM_CHECK_ARG(E_local == 0 || (weight && scale), "gmm_fp4: null weight pointer");
-  DWM_CHECK_ARG((uintptr_t)lhs % 16 == 0 && (uintptr_t)weight % 16 == 0 && (uintptr_t)scale % 4 == 0,
-                "gmm_fp4: lhs and weight must be 16-byte aligned, scale 4-byte aligned");
+  DWM_CHECK_ARG((uintptr_t)lhs % 16 == 0 && (uintptr_t)weight % 16 == 0 && (uintptr_t)out % 16 == 0 &&
+                    (uintptr_t)scale % 4 == 0,
+                "gmm_fp4: lhs, weight and out must be 16-byte aligned, scale 4-byte aligned");
   hipStream_t st = as_stream(stream);
   const int elem = out_dtype == DWM_F32 ? 4 : 2;
   if (zero_init) {
@@ -434,12 +541,12 @@ extern "C" int dwm_gmm_fp4(const uint16_t *lhs, int64_t M, int64_t K, const uint
   if (E_local == 0 || num_groups == 0) return DWM_OK;
   const int out_f32 = out_dtype == DWM_F32;
   // 96-row x 512-column tiles, 8 consumer + 4 producer waves, four 64-deep
-  // K stages (120 KB of LDS, 138 VGPRs: one block of 12 waves per CU).
+  // K stages (120 KB of LDS, under 168 VGPRs: one block of 12 waves per CU).
   // Measured fastest on the decode and prefill workloads among the tile,
   // wave-split and pipeline-depth variants tried.
   if (fuse_act == DWM_ACT_SILU_MUL_CLAMP)
-    return launch_gmm_ws<3, 8, 2, 4, 4, false, true>(lhs, M, K, weight, scale, group_sizes, num_groups,
-                                                     group_offset, E_local, N, out, out_f32, st);
-  return launch_gmm_ws<3, 8, 2, 4, 4, false>(lhs, M, K, weight, scale, group_sizes, num_groups, group_offset,
-                                             E_local, N, out, out_f32, st);
+    return launch_gmm_ws<3, 8, 2, 4, 4, true>(lhs, M, K, weight, scale, group_sizes, num_groups, group_offset,
+                                              E_local, N, out, out_f32, st);
+  return launch_gmm_ws<3, 8, 2, 4, 4>(lhs, M, K, weight, scale, group_sizes, num_groups, group_offset, E_local, N,
+                                      out, out_f32, st);
 }
