@@ -15,6 +15,12 @@ events on the stream the kernels run on.  `extra` reports the other workloads
 `cpu_baseline` times the numpy oracle of the same math on a bounded sample of
 experts on this host.
 
+The default warmup (200 launches, ~30 ms of decode work) brings the GPU to
+its sustained clock before the timed region: the power manager ramps the
+clock up over the first tens of milliseconds of load, and a 5-launch warmup
+times part of that ramp (decode_gate_up: 0.179 ms/step after 5 warmup
+launches, 0.153 ms after 200).
+
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--extra all|none]
 """
 import argparse
@@ -307,7 +313,7 @@ def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--extra", choices=["all", "none"], default="all")
     ap.add_argument("--cpu-budget", type=float, default=15.0,
                     help="seconds of CPU-baseline work (0 skips it)")
