@@ -211,6 +211,52 @@ def bench_moe_block(dev, steps, warmup):
                                  "nonempty_groups": nonempty}}
 
 
+def bench_formats(dev, steps, warmup):
+    """Checkpoint weight formats (load-time kernels) at the decode shapes:
+    an MXFP4 expert checkpoint of the gate/up weight (32 experts, N = 4096,
+    K = 7168: [E, N, K/2] codes + [E, N, K/32] scales -> [E, K, N/2] +
+    [E, K/32, N]) and a DeepSeek FP8 128x128-block weight (N = 4096,
+    K = 7168, [N, K] -> [K, N]), through the C ABI with preallocated outputs.
+    Bytes = every input and output byte once."""
+    import torch
+    from dw_tpu_amd import _lib
+    lib = _lib.load()
+    st = _lib.stream_handle(dev)
+    res = {}
+    E, N, K = 32, 4096, 7168
+    blocks = torch.randint(0, 256, (E, N, K // 2), dtype=torch.uint8, device=dev)
+    scales = torch.randint(110, 135, (E, N, K // 32), dtype=torch.uint8, device=dev)
+    codes = torch.empty((E, K, N // 2), dtype=torch.uint8, device=dev)
+    scode = torch.empty((E, K // 32, N), dtype=torch.uint8, device=dev)
+    status = torch.empty(2, dtype=torch.int32, device=dev)
+    args = (_lib.ptr(blocks), _lib.ptr(scales), E, N, K, 0, _lib.ptr(codes), _lib.ptr(scode), _lib.ptr(status), st)
+
+    def run_mx(i):
+        if lib.dwm_mxfp4_requant(*args):
+            raise RuntimeError(lib.dwm_last_error().decode())
+    ms = time_steps(run_mx, steps, min(warmup, 20))
+    b = 2 * (blocks.numel() + scales.numel())
+    res["mxfp4_requant"] = {"ms": round(ms, 5), "GB_s": round(b / (ms * 1e-3) / 1e9, 1),
+                            "hbm_frac": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "bytes": b,
+                            "E": E, "N": N, "K": K}
+    del blocks, scales, codes, scode
+    w = torch.randint(0, 0x7E, (N, K), dtype=torch.uint8, device=dev)
+    wsc = torch.full((N // 128, K // 128), 2.0 ** -8, dtype=torch.float32, device=dev)
+    w_out = torch.empty((K, N), dtype=torch.uint8, device=dev)
+    s_out = torch.empty((K // 128, N), dtype=torch.float32, device=dev)
+    args8 = (_lib.ptr(w), _lib.ptr(wsc), K, N, 1, _lib.ptr(w_out), _lib.ptr(s_out), _lib.ptr(status), st)
+
+    def run_f8(i):
+        if lib.dwm_fp8_block_requant(*args8):
+            raise RuntimeError(lib.dwm_last_error().decode())
+    ms = time_steps(run_f8, steps, warmup)
+    b = 2 * w.numel() + 4 * (wsc.numel() + s_out.numel())
+    res["fp8_block_requant"] = {"ms": round(ms, 5), "GB_s": round(b / (ms * 1e-3) / 1e9, 1),
+                                "hbm_frac": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "bytes": b,
+                                "N": N, "K": K}
+    return res
+
+
 def bench_dense(dev, steps, warmup, ms_list=(1, 16, 128, 1024, 4096)):
     """Dense FP8 GEMM (K=7168, N=4096) at each M, W8A16 and W8A8, through
     the C ABI with prepacked weights; 10 rotated weight copies (~290 MB) keep
@@ -357,6 +403,9 @@ def main():
         torch.cuda.empty_cache()
         log("bench: dense fp8")
         extra.update(bench_dense(dev, args.steps, args.warmup))
+        torch.cuda.empty_cache()
+        log("bench: checkpoint formats")
+        extra.update(bench_formats(dev, args.steps, args.warmup))
     cpu = None
     if args.cpu_budget > 0:
         log("bench: cpu baseline")

@@ -1,0 +1,277 @@
+// Checkpoint weight formats -> inputs of the hot path (load time).
+//
+// * MXFP4 expert weights (OCP MX: e2m1 codes two per byte along K, one ue8m0
+//   scale per 32 K-values; layout [E, N, K/2] + [E, N, K/32]) -> the fp4
+//   gmm's e2m1 codes [E, K, N/2] (two per byte along N) and e8m0 scale codes
+//   [E, K/32, N]: the reference dequantizes the checkpoint and requantizes it
+//   at block 32 with power-of-two scales (quantize_tensor with
+//   power_of_two_scale, patches/tpu-inference/0001-dsv4-v6e-enablement.patch:
+//   338-349, called for block-32 e2m1 at 0001-...:558-562), then stores the
+//   scales as e8m0 codes when lossless (e8m0_encode,
+//   kernels/tpu_inference/layers/common/quantization/e8m0_scale.py:28-35).
+// * FP8 weights with 128 x 128 block scales -> e4m3 [K, N] with power-of-two
+//   f32 scales per (128-deep K-block, column), the dense fp8 kernel's layout
+//   (0001-...:499-512).
+//
+// Both are one pass over HBM: a block owns a 128 (K) x 64 (N) tile, computes
+// each (column, K-block) group's requantization in registers (every f32 step
+// in the order the reference takes it: x = code * scale, scale' =
+// pow2ceil(absmax / max), code' = rne(x * (1 / scale'))), and transposes the
+// tile through LDS so both the reads and the writes are whole 16-byte runs.
+#include "common.h"
+
+namespace dwm {
+
+// e2m1 nibble -> f32 (sign bit 3; magnitudes 0, .5, 1, 1.5, 2, 3, 4, 6).
+__device__ __forceinline__ float e2m1_f32(uint32_t c) {
+  const uint32_t e = (c >> 1) & 3u, m = c & 1u;
+  const uint32_t mag = e == 0 ? (m ? 0x3F000000u : 0u) : (((e + 126u) << 23) | (m << 22));
+  return __builtin_bit_cast(float, mag | ((c & 8u) << 28));
+}
+
+// e4m3fn code -> f32 (bias 7, subnormals m * 2^-9, 0x7F / 0xFF NaN).
+__device__ __forceinline__ float e4m3_f32(uint32_t c) {
+  const uint32_t e = (c >> 3) & 15u, m = c & 7u;
+  const uint32_t sign = (c & 0x80u) << 24;
+  if (e == 15 && m == 7) return __builtin_bit_cast(float, 0x7FC00000u | sign);
+  if (e == 0) return __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, (float)m * 0.001953125f) | sign);
+  return __builtin_bit_cast(float, sign | ((e + 120u) << 23) | (m << 20));
+}
+
+// f32 -> e2m1 nibble, round to nearest even, saturating at 6; the sign of q
+// (also of -0 and of values rounding to 0) sets bit 3.
+__device__ __forceinline__ uint32_t rne_e2m1(float q) {
+  const float a = fabsf(q);
+  const uint32_t c = (a > 0.25f) + (a >= 0.75f) + (a > 1.25f) + (a >= 1.75f) + (a > 2.5f) + (a >= 3.5f) + (a > 5.0f);
+  return c | ((__builtin_bit_cast(uint32_t, q) >> 28) & 8u);
+}
+
+// f32 -> e4m3fn code, round to nearest even; magnitudes >= 464 (and NaN) give
+// 0x7F (NaN) with the sign of q.
+__device__ __forceinline__ uint32_t rne_e4m3(float q) {
+  const uint32_t bits = __builtin_bit_cast(uint32_t, q);
+  const uint32_t sign = (bits >> 24) & 0x80u;
+  const float a = fabsf(q);
+  if (!(a < 464.0f)) return sign | 0x7Fu;
+  if (a < 0.015625f) {  // below 2^-6: multiples of 2^-9 (the step to 2^-6 lands on code 8)
+    return sign | (uint32_t)rintf(a * 512.0f);
+  }
+  const uint32_t ab = bits & 0x7FFFFFFFu;
+  int32_t ex = (int32_t)(ab >> 23) - 127;
+  uint32_t keep = (ab >> 20) & 7u;
+  const uint32_t rem = ab & 0xFFFFFu;
+  if (rem > 0x80000u || (rem == 0x80000u && (keep & 1u))) {
+    if (++keep == 8u) {
+      keep = 0;
+      ++ex;
+    }
+  }
+  return sign | ((uint32_t)(ex + 7) << 3) | keep;
+}
+
+// 2^ceil(log2(s)) for finite s > 0, exactly as frexp gives it (mantissa in
+// [0.5, 1): a power of two maps to itself); s <= 0 is returned unchanged.
+__device__ __forceinline__ float pow2_ceil_f32(float s) {
+  if (!(s > 0.0f)) return s;
+  const uint32_t b = __builtin_bit_cast(uint32_t, s);
+  int32_t e;  // s in (2^(e-1), 2^e]
+  const uint32_t ef = b >> 23, m = b & 0x7FFFFFu;
+  if (ef != 0) {
+    e = (int32_t)ef - 127 + (m != 0 ? 1 : 0);
+  } else {  // subnormal: m * 2^-149
+    const int32_t p = 31 - __builtin_clz(m);
+    e = p - 149 + ((m & (m - 1)) != 0 ? 1 : 0);
+  }
+  if (e > 127) return __builtin_bit_cast(float, 0x7F800000u);
+  if (e >= -126) return __builtin_bit_cast(float, (uint32_t)(e + 127) << 23);
+  return __builtin_bit_cast(float, 1u << (e + 149));
+}
+
+// 1 / s for a power of two s (exact, or infinite); zero and an infinite
+// reciprocal give 0 (a zero block stays zero).
+__device__ __forceinline__ float inv_or_zero(float s) {
+  if (s == 0.0f) return 0.0f;
+  const float inv = 1.0f / s;
+  return __builtin_isinf(inv) ? 0.0f : inv;
+}
+
+__global__ void format_status_zero_kernel(int32_t *status) {
+  if (threadIdx.x < 2) status[threadIdx.x] = 0;
+}
+
+// Wave-aggregated count of lanes with `flag` into *counter.
+__device__ __forceinline__ void count_flags(bool flag, int32_t *counter) {
+  const uint64_t m = __ballot(flag);
+  if ((threadIdx.x & 63) == 0 && m != 0) atomicAdd(counter, (int32_t)__popcll(m));
+}
+
+// ---- MXFP4 --------------------------------------------------------------
+// Block (kt, nt, e): K rows kt*128 .. +127, columns nt*64 .. +63 (before the
+// optional w13 de-interleave).  Thread t: column n = nt*64 + t/4, K-block
+// kt*4 + t%4.
+__global__ __launch_bounds__(256) void mxfp4_requant_kernel(const uint8_t *__restrict__ blocks,
+                                                            const uint8_t *__restrict__ scales, int64_t N, int64_t K,
+                                                            int interleave, uint8_t *__restrict__ codes_out,
+                                                            uint8_t *__restrict__ scale_out,
+                                                            int32_t *__restrict__ status) {
+  __shared__ uint8_t s_code[128][64];
+  const int t = threadIdx.x, nl = t >> 2, kbl = t & 3;
+  const int64_t e = blockIdx.z, kt = blockIdx.x, nt = blockIdx.y;
+  const int64_t n = nt * 64 + nl;
+  const int64_t kb = kt * 4 + kbl;
+  const u32x4_t in = *(const u32x4_t *)(blocks + (e * N + n) * (K / 2) + kb * 16);
+  const uint32_t sc = scales[(e * N + n) * (K / 32) + kb];
+  // Checkpoint scale 2^(sc - 127): code 0 is 2^-127 (subnormal), 255 is NaN.
+  const float s = sc == 255u ? __builtin_bit_cast(float, 0x7FC00000u)
+                             : __builtin_bit_cast(float, sc == 0u ? 0x00400000u : sc << 23);
+  float x[32];
+  float amax = 0.0f;
+  bool finite = true;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    const uint32_t c = (in[i >> 3] >> (4 * (i & 7))) & 0xFu;
+    x[i] = e2m1_f32(c) * s;
+    finite = finite && __builtin_isfinite(x[i]);
+    amax = fmaxf(amax, fabsf(x[i]));
+  }
+  const float scale = pow2_ceil_f32(finite ? amax / 6.0f : 0.0f);
+  const float inv = inv_or_zero(scale);
+  const int cn = interleave ? ((nl & 1) ? 32 + (nl >> 1) : (nl >> 1)) : nl;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) s_code[kbl * 32 + i][cn] = finite ? (uint8_t)rne_e2m1(x[i] * inv) : 0;
+  const uint32_t sb = __builtin_bit_cast(uint32_t, scale);
+  const uint32_t scode = finite ? (sb >> 23) & 0xFFu : 255u;
+  const bool lossy = finite && (((sb & 0x807FFFFFu) != 0) || ((sb >> 23) & 0xFFu) == 255u);
+  const int64_t nout = interleave ? ((n & 1) ? N / 2 + (n >> 1) : (n >> 1)) : n;
+  scale_out[(e * (K / 32) + kb) * N + nout] = (uint8_t)scode;
+  count_flags(lossy, status);
+  count_flags(!finite, status + 1);
+  __syncthreads();
+  // Row kl of the tile, 32 codes of half h -> 16 bytes.
+  const int kl = t >> 1, h = t & 1;
+  u32x4_t o;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    uint32_t v = 0;
+#pragma unroll
+    for (int b = 0; b < 8; ++b) v |= (uint32_t)s_code[kl][h * 32 + w * 8 + b] << (4 * b);
+    o[w] = v;
+  }
+  const int64_t col = interleave ? (h ? N / 2 : 0) + nt * 32 : nt * 64 + h * 32;
+  *(u32x4_t *)(codes_out + (e * K + kt * 128 + kl) * (N / 2) + col / 2) = o;
+}
+
+// ---- FP8 128 x 128 -> 1 x 128 ---------------------------------------------
+// Block (kb, nt): K rows kb*128 .. +127, columns nt*64 .. +63.  The tile is
+// staged [k][n] in LDS; thread t then owns column t/4, rows 32*(t%4) .. +31.
+__global__ __launch_bounds__(256) void fp8_block_requant_kernel(const uint8_t *__restrict__ w,
+                                                                const float *__restrict__ scale, int64_t K, int64_t N,
+                                                                int input_nk, uint8_t *__restrict__ w_out,
+                                                                float *__restrict__ scale_out,
+                                                                int32_t *__restrict__ status) {
+  __shared__ __attribute__((aligned(16))) uint8_t s_t[128][64];
+  const int t = threadIdx.x;
+  const int64_t kb = blockIdx.x, nt = blockIdx.y;
+  if (input_nk) {
+    const int nl = t >> 2, part = t & 3;
+    const uint8_t *src = w + (nt * 64 + nl) * K + kb * 128 + part * 32;
+    const u32x4_t a = *(const u32x4_t *)src, b = *(const u32x4_t *)(src + 16);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      s_t[part * 32 + i][nl] = (uint8_t)(a[i >> 2] >> (8 * (i & 3)));
+      s_t[part * 32 + 16 + i][nl] = (uint8_t)(b[i >> 2] >> (8 * (i & 3)));
+    }
+  } else {
+    const int kl = t >> 1, h = t & 1;
+    const uint8_t *src = w + (kb * 128 + kl) * N + nt * 64 + h * 32;
+    *(u32x4_t *)&s_t[kl][h * 32] = *(const u32x4_t *)src;
+    *(u32x4_t *)&s_t[kl][h * 32 + 16] = *(const u32x4_t *)(src + 16);
+  }
+  __syncthreads();
+  const int nl = t >> 2, part = t & 3;
+  const int64_t n = nt * 64 + nl;
+  const float bs = input_nk ? scale[(n / 128) * (K / 128) + kb] : scale[kb * (N / 128) + n / 128];
+  float x[32];
+  float amax = 0.0f;
+  bool finite = true;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    x[i] = e4m3_f32(s_t[part * 32 + i][nl]) * bs;
+    finite = finite && __builtin_isfinite(x[i]);
+    amax = fmaxf(amax, fabsf(x[i]));
+  }
+  // The four threads of a column are adjacent lanes.
+  amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+  amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+  int fin = finite ? 1 : 0;
+  fin &= __shfl_xor(fin, 1, 64);
+  fin &= __shfl_xor(fin, 2, 64);
+  const bool all_finite = fin != 0;
+  const float s2 = pow2_ceil_f32(all_finite ? amax / 448.0f : 0.0f);
+  const float inv = inv_or_zero(s2);
+  bool exact = true;
+  uint8_t q[32];
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    const uint32_t c = all_finite ? rne_e4m3(x[i] * inv) : 0u;
+    q[i] = (uint8_t)c;
+    exact = exact && (e4m3_f32(c) * s2 == x[i]);
+  }
+  int ex = exact ? 1 : 0;
+  ex &= __shfl_xor(ex, 1, 64);
+  ex &= __shfl_xor(ex, 2, 64);
+  __syncthreads();  // every thread has read its inputs before codes overwrite the tile
+#pragma unroll
+  for (int i = 0; i < 32; ++i) s_t[part * 32 + i][nl] = q[i];
+  if (part == 0) scale_out[kb * N + n] = all_finite ? s2 : __builtin_bit_cast(float, 0x7FC00000u);
+  count_flags(part == 0 && all_finite && !ex, status);
+  count_flags(part == 0 && !all_finite, status + 1);
+  __syncthreads();
+  const int kl = t >> 1, h = t & 1;
+  uint8_t *dst = w_out + (kb * 128 + kl) * N + nt * 64 + h * 32;
+  *(u32x4_t *)dst = *(const u32x4_t *)&s_t[kl][h * 32];
+  *(u32x4_t *)(dst + 16) = *(const u32x4_t *)&s_t[kl][h * 32 + 16];
+}
+
+}  // namespace dwm
+
+using namespace dwm;
+
+extern "C" int dwm_mxfp4_requant(const uint8_t *blocks, const uint8_t *scales, int64_t E, int64_t N, int64_t K,
+                                 int w13_interleave, uint8_t *codes_out, uint8_t *scale_codes_out, int32_t *status,
+                                 void *stream) {
+  clear_error();
+  DWM_CHECK_ARG(E >= 0 && N >= 0 && K >= 0, "mxfp4_requant: bad sizes E=%lld N=%lld K=%lld", (long long)E,
+                (long long)N, (long long)K);
+  DWM_UNSUPPORTED_IF(K % 128 != 0 || N % 64 != 0, "mxfp4_requant: K %% 128 == 0 and N %% 64 == 0 required");
+  DWM_UNSUPPORTED_IF(w13_interleave && N % 128 != 0, "mxfp4_requant: w13_interleave needs N %% 128 == 0");
+  DWM_UNSUPPORTED_IF(K / 128 > 0x7FFFFFFF || N / 64 > 65535 || E > 65535, "mxfp4_requant: too large");
+  DWM_CHECK_ARG(status != nullptr, "mxfp4_requant: null status");
+  hipStream_t st = as_stream(stream);
+  hipLaunchKernelGGL(format_status_zero_kernel, dim3(1), dim3(64), 0, st, status);
+  if (E == 0 || N == 0 || K == 0) return launch_status("mxfp4_requant");
+  DWM_CHECK_ARG(blocks && scales && codes_out && scale_codes_out, "mxfp4_requant: null pointer");
+  DWM_CHECK_ARG((uintptr_t)blocks % 16 == 0 && (uintptr_t)codes_out % 16 == 0,
+                "mxfp4_requant: blocks and codes_out must be 16-byte aligned");
+  hipLaunchKernelGGL(mxfp4_requant_kernel, dim3((unsigned)(K / 128), (unsigned)(N / 64), (unsigned)E), dim3(256), 0,
+                     st, blocks, scales, N, K, w13_interleave ? 1 : 0, codes_out, scale_codes_out, status);
+  return launch_status("mxfp4_requant");
+}
+
+extern "C" int dwm_fp8_block_requant(const uint8_t *w, const float *scale, int64_t K, int64_t N, int input_nk,
+                                     uint8_t *w_out, float *scale_out, int32_t *status, void *stream) {
+  clear_error();
+  DWM_CHECK_ARG(K >= 0 && N >= 0, "fp8_block_requant: bad sizes K=%lld N=%lld", (long long)K, (long long)N);
+  DWM_UNSUPPORTED_IF(K % 128 != 0 || N % 128 != 0, "fp8_block_requant: K %% 128 == 0 and N %% 128 == 0 required");
+  DWM_UNSUPPORTED_IF(K / 128 > 0x7FFFFFFF || N / 64 > 65535, "fp8_block_requant: too large");
+  DWM_CHECK_ARG(status != nullptr, "fp8_block_requant: null status");
+  hipStream_t st = as_stream(stream);
+  hipLaunchKernelGGL(format_status_zero_kernel, dim3(1), dim3(64), 0, st, status);
+  if (K == 0 || N == 0) return launch_status("fp8_block_requant");
+  DWM_CHECK_ARG(w && scale && w_out && scale_out, "fp8_block_requant: null pointer");
+  DWM_CHECK_ARG((uintptr_t)w % 16 == 0 && (uintptr_t)w_out % 16 == 0 && (uintptr_t)scale % 4 == 0,
+                "fp8_block_requant: w and w_out must be 16-byte aligned");
+  hipLaunchKernelGGL(fp8_block_requant_kernel, dim3((unsigned)(K / 128), (unsigned)(N / 64)), dim3(256), 0, st, w,
+                     scale, K, N, input_nk ? 1 : 0, w_out, scale_out, status);
+  return launch_status("fp8_block_requant");
+}

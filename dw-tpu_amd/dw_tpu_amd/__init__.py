@@ -3,6 +3,7 @@ and the dense FP8 GEMM, behind the reference's (jamesdborin/dw-tpu) call
 signatures.  Kernels are hand-written HIP for gfx950 in ``../csrc``, reached
 through the C ABI of ``include/dwtpu_moe.h`` (``libdwtpu_moe.so``)."""
 from . import _lib
+from .checkpoint_formats import RequantStatus, fp8_block_requant, load_mxfp4_moe_weight, mxfp4_requant
 from .e8m0_scale import e8m0_decode, e8m0_encode
 from .fused_moe_gmm import fp4_weight_to_codes, gmm_wrapper
 from .gmm_v2 import Fp4Weight, decode_codes, e2m1_to_codes, gmm_v2, needs_fp4_emulation, prepack_fp4
@@ -12,7 +13,7 @@ from .moe_fast_dispatch import (Dispatch, dispatch_gather_pallas, fast_dispatch_
                                 row_gather, sorted_token_indices)
 
 __all__ = [
-    "Dispatch", "Fp4Weight", "combine_pallas", "combine_xla", "decode_codes", "dispatch_gather_pallas",
+    "Dispatch", "Fp4Weight", "RequantStatus", "fp8_block_requant", "load_mxfp4_moe_weight", "mxfp4_requant", "combine_pallas", "combine_xla", "decode_codes", "dispatch_gather_pallas",
     "e2m1_to_codes", "e8m0_decode", "e8m0_encode", "fast_combine", "fast_dispatch_gather",
     "MoeBlockOutputs", "fp4_weight_to_codes", "gmm_v2", "gmm_wrapper", "moe_block", "moe_dispatch",
     "needs_fp4_emulation", "prepack_fp4",

@@ -41,6 +41,8 @@ SIGNATURES = {
     "dwm_dense_fp8_workspace_size": [_i64, _i64, _i64, _p],
     "dwm_dense_fp8_w8a16": [_p, _i64, _i64, _i64, _p, _p, _p, _p, _i64, _p],
     "dwm_dense_fp8_w8a8": [_p, _p, _i64, _i64, _i64, _p, _p, _p, _p, _i64, _p],
+    "dwm_mxfp4_requant": [_p, _p, _i64, _i64, _i64, _i32, _p, _p, _p, _p],
+    "dwm_fp8_block_requant": [_p, _p, _i64, _i64, _i32, _p, _p, _p, _p],
 }
 _RESTYPES = {"dwm_last_error": ctypes.c_char_p}
 

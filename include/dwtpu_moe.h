@@ -219,6 +219,51 @@ int dwm_dense_fp8_w8a8(const uint8_t *xq, const float *sx, int64_t M, int64_t K,
                        const uint8_t *w, const float *sw, uint16_t *out, void *workspace,
                        int64_t workspace_bytes, void *stream);
 
+/* ---------------------------------------------------------------------- */
+/* Checkpoint weight formats (load time).                                  */
+/* ---------------------------------------------------------------------- */
+
+/* MXFP4 expert weights (OCP MX: e2m1 codes two per byte along K, low nibble
+ * first; one ue8m0 scale per 32 K-values, code 0 = 2^-127, 255 = NaN) ->
+ * the fp4 gmm's inputs, requantized at block 32 with power-of-two scales
+ * and the scales stored as e8m0 codes (code 0 = +0.0).  Replaces the
+ * reference's load path: quantize_tensor(e2m1, dequantized checkpoint, K,
+ * 32, power_of_two_scale=True) (patches/tpu-inference/
+ * 0001-dsv4-v6e-enablement.patch:338-349, called at :558-562 from
+ * quantize_moe_weights :239-268) followed by e8m0_encode
+ * (kernels/tpu_inference/layers/common/quantization/e8m0_scale.py:28-35,
+ * patches/tpu-inference-ext/0403-moe-e8m0-scales.patch:118-128).
+ *   blocks:  [E, N, K/2] bytes; scales: [E, N, K/32] e8m0 codes.
+ *   w13_interleave: columns stored w1, w3, w1, w3, ... are written
+ *     [w1 | w3] (quantize_moe_weights' w13_interleave).
+ *   codes_out: [E, K, N/2] bytes (e2m1 two per byte along N, the input of
+ *     dwm_gmm_fp4_prepack); scale_codes_out: [E, K/32, N] e8m0 codes.
+ *   status: device int32[2], set by the call: [0] = groups whose scale is
+ *     not e8m0-encodable (e8m0_encode's lossless flag is status[0] == 0),
+ *     [1] = groups holding a NaN or infinity (written as codes 0, scale
+ *     code 255).
+ * Requires K % 128 == 0, N % 64 == 0 (N % 128 == 0 with w13_interleave). */
+int dwm_mxfp4_requant(const uint8_t *blocks, const uint8_t *scales, int64_t E, int64_t N, int64_t K,
+                      int w13_interleave, uint8_t *codes_out, uint8_t *scale_codes_out, int32_t *status,
+                      void *stream);
+
+/* FP8 weights with 128 x 128 block scales (DeepSeek checkpoints) -> e4m3
+ * [K, N] with power-of-two f32 scales per (128-deep K-block, column), the
+ * layout of dwm_dense_fp8_prepack / the reference's [K/128, 1, N] scales.
+ * Exact when the block scales are powers of two (ue8m0).  Replaces the
+ * reference's requantization to 1 x 128 K-blocks with power_of_two_scale
+ * (patches/tpu-inference/0001-dsv4-v6e-enablement.patch:499-512, checked by
+ * its test at :110-129).
+ *   w: e4m3 [N, K] (input_nk != 0, the checkpoint's [out, in]) or [K, N];
+ *   scale: f32 [N/128, K/128] (input_nk) or [K/128, N/128].
+ *   w_out: [K, N] e4m3; scale_out: [K/128, N] f32.
+ *   status: device int32[2], set by the call: [0] = (K-block, column) groups
+ *     the requantization does not reproduce exactly, [1] = groups holding a
+ *     NaN or infinity (written as codes 0, scale NaN).
+ * Requires K % 128 == 0, N % 128 == 0. */
+int dwm_fp8_block_requant(const uint8_t *w, const float *scale, int64_t K, int64_t N, int input_nk,
+                          uint8_t *w_out, float *scale_out, int32_t *status, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -92,6 +92,27 @@ def test_dispatch_and_combine_argument_checks():
     assert rc == _lib.ERR_INVALID  # odd count
 
 
+def test_checkpoint_format_argument_checks():
+    null = None
+    st = ctypes.c_void_p(8)  # never dereferenced: the checks fail before any launch
+    rc, msg = _rc("dwm_mxfp4_requant", null, null, 2, 128, 96, 0, null, null, st, null)
+    assert rc == _lib.ERR_UNSUPPORTED and "K" in msg
+    rc, msg = _rc("dwm_mxfp4_requant", null, null, 2, 96, 128, 0, null, null, st, null)
+    assert rc == _lib.ERR_UNSUPPORTED and "N" in msg
+    rc, msg = _rc("dwm_mxfp4_requant", null, null, 2, 64, 128, 1, null, null, st, null)
+    assert rc == _lib.ERR_UNSUPPORTED and "interleave" in msg
+    rc, msg = _rc("dwm_mxfp4_requant", null, null, 2, 64, 128, 0, null, null, null, null)
+    assert rc == _lib.ERR_INVALID and "status" in msg
+    rc, msg = _rc("dwm_mxfp4_requant", null, null, -1, 64, 128, 0, null, null, st, null)
+    assert rc == _lib.ERR_INVALID and "sizes" in msg
+    rc, msg = _rc("dwm_fp8_block_requant", null, null, 256, 192, 1, null, null, st, null)
+    assert rc == _lib.ERR_UNSUPPORTED and "N" in msg
+    rc, msg = _rc("dwm_fp8_block_requant", null, null, 200, 256, 1, null, null, st, null)
+    assert rc == _lib.ERR_UNSUPPORTED and "K" in msg
+    rc, msg = _rc("dwm_fp8_block_requant", null, null, 256, 256, 1, null, null, null, null)
+    assert rc == _lib.ERR_INVALID and "status" in msg
+
+
 def test_python_layer_rejects_host_tensors():
     import torch
     from dw_tpu_amd import e2m1_to_codes
