@@ -211,6 +211,36 @@ def bench_moe_block(dev, steps, warmup):
                                  "nonempty_groups": nonempty}}
 
 
+def bench_routing(dev, steps, warmup):
+    """The router (dwm_route_topk) at the decode workload's routing (256
+    tokens, 32 experts, top-8 softmax) and at a DeepSeek-V4-like prefill
+    (8192 tokens, 256 experts, top-8 sqrtsoftplus + correction bias +
+    renormalize), f32 logits, bf16 weights.  Bytes = logits + ids + weights."""
+    import torch
+    from dw_tpu_amd import _lib
+    lib = _lib.load()
+    st = _lib.stream_handle(dev)
+    res = {}
+    for name, T, E, k, fn, biased in (("route_decode", 256, 32, 8, 0, False),
+                                      ("route_prefill_dsv4", 8192, 256, 8, 2, True)):
+        g = torch.Generator(device="cpu").manual_seed(T + E)
+        logits = torch.randn((T, E), generator=g).to(dev)
+        bias = (torch.randn((E,), generator=g) * 0.1).to(dev) if biased else None
+        w = torch.empty((T, k), dtype=torch.bfloat16, device=dev)
+        ids = torch.empty((T, k), dtype=torch.int32, device=dev)
+        args = (_lib.ptr(logits), _lib.F32, T, E, k, fn, _lib.ptr(bias), None, 1 if biased else 0, None,
+                _lib.ptr(w), _lib.BF16, _lib.ptr(ids), st)
+
+        def run(i, args=args):
+            if lib.dwm_route_topk(*args):
+                raise RuntimeError(lib.dwm_last_error().decode())
+        ms = time_steps(run, steps, warmup)
+        b = T * E * 4 + T * k * 6 + (E * 4 if biased else 0)
+        res[name] = {"ms": round(ms, 5), "GB_s": round(b / (ms * 1e-3) / 1e9, 1), "bytes": b, "T": T, "E": E,
+                     "topk": k}
+    return res
+
+
 def bench_formats(dev, steps, warmup):
     """Checkpoint weight formats (load-time kernels) at the decode shapes:
     an MXFP4 expert checkpoint of the gate/up weight (32 experts, N = 4096,
@@ -404,6 +434,8 @@ def main():
         log("bench: dense fp8")
         extra.update(bench_dense(dev, args.steps, args.warmup))
         torch.cuda.empty_cache()
+        log("bench: router")
+        extra.update(bench_routing(dev, args.steps, args.warmup))
         log("bench: checkpoint formats")
         extra.update(bench_formats(dev, args.steps, args.warmup))
     cpu = None

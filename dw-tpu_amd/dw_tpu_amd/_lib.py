@@ -13,11 +13,12 @@ import torch
 LIB_NAME = "libdwtpu_moe.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
-# enum dwm_status / dwm_dtype / dwm_fp4_format / dwm_act
+# enum dwm_status / dwm_dtype / dwm_fp4_format / dwm_act / dwm_score
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_HIP = 0, 1, 2, 3
 BF16, F32, U8 = 0, 1, 2
 FP4_E2M1, FP4_CODES = 0, 1
 ACT_NONE, ACT_SILU_MUL_CLAMP = 0, 1
+SCORE_FNS = {"softmax": 0, "sigmoid": 1, "sqrtsoftplus": 2}
 
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int
@@ -43,6 +44,8 @@ SIGNATURES = {
     "dwm_dense_fp8_w8a8": [_p, _p, _i64, _i64, _i64, _p, _p, _p, _p, _i64, _p],
     "dwm_mxfp4_requant": [_p, _p, _i64, _i64, _i64, _i32, _p, _p, _p, _p],
     "dwm_fp8_block_requant": [_p, _p, _i64, _i64, _i32, _p, _p, _p, _p],
+    "dwm_route_topk": [_p, _i32, _i64, _i64, _i32, _i32, _p, _p, _i32, _p, _p, _i32, _p, _p],
+    "dwm_dedupe_topk": [_p, _p, _i64, _i32, _i64, _p, _p, _p],
 }
 _RESTYPES = {"dwm_last_error": ctypes.c_char_p}
 

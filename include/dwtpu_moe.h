@@ -47,6 +47,14 @@ enum dwm_act {
   DWM_ACT_SILU_MUL_CLAMP = 1
 };
 
+/* Router score functions (apply_scoring_fn, called at
+ * patches/tpu-inference-experimental/fused-moe-fp4/0901-...:667). */
+enum dwm_score {
+  DWM_SCORE_SOFTMAX = 0,      /* exp(x - max) / sum over the experts */
+  DWM_SCORE_SIGMOID = 1,      /* 1 / (1 + exp(-x)) */
+  DWM_SCORE_SQRTSOFTPLUS = 2  /* sqrt(log(1 + exp(x))), the DeepSeek V4 router score */
+};
+
 /* Packed 4-bit weight formats (two per byte, element 2j in the low nibble). */
 enum dwm_fp4_format {
   DWM_FP4_E2M1 = 0, /* OCP e2m1 nibbles (torch float4_e2m1fn_x2 bytes) */
@@ -263,6 +271,35 @@ int dwm_mxfp4_requant(const uint8_t *blocks, const uint8_t *scales, int64_t E, i
  * Requires K % 128 == 0, N % 128 == 0. */
 int dwm_fp8_block_requant(const uint8_t *w, const float *scale, int64_t K, int64_t N, int input_nk,
                           uint8_t *w_out, float *scale_out, int32_t *status, void *stream);
+
+/* ---------------------------------------------------------------------- */
+/* Router (the producer of topk_ids / topk_weights).                       */
+/* ---------------------------------------------------------------------- */
+
+/* Top-k routing "exactly as fused_moe_func" (_fused_moe_fp4_routing,
+ * patches/tpu-inference-experimental/fused-moe-fp4/0901-...:656-687):
+ * scores = score_fn(logits) in f32; experts = hash_ids when given, else the
+ * top k of scores + bias when bias is given, else of scores (larger first,
+ * ties to the lower expert id, as lax.top_k); weights = the experts'
+ * (unbiased) scores; renormalize divides by their sum over k in order;
+ * tokens t >= *num_valid_tokens get expert 0 and weight 0; weights are cast
+ * to weights_dtype (bf16 round to nearest even, or f32).
+ *   logits: [T, E] bf16 or f32; bias: f32 [E] or NULL; hash_ids: int32
+ *   [T, topk] or NULL; num_valid_tokens: device int32[1] or NULL (all valid).
+ *   weights_out: [T, topk]; ids_out: int32 [T, topk].
+ * Requires E <= 1024, topk <= min(E, 64). */
+int dwm_route_topk(const void *logits, int logits_dtype, int64_t T, int64_t E, int topk, int score_fn,
+                   const float *bias, const int32_t *hash_ids, int renormalize,
+                   const int32_t *num_valid_tokens, void *weights_out, int weights_dtype, int32_t *ids_out,
+                   void *stream);
+
+/* dedupe_topk (0901-...:98-121): for j = 1 .. topk-1 a repeat of an earlier
+ * expert id adds its weight (f32) to the first occurrence and is re-pointed
+ * at the first id in [0, min(2 topk, E)) no column of the token holds (0
+ * when all are held), with weight 0.  w: f32 [T, topk]; ids: int32
+ * [T, topk].  Requires topk <= 64. */
+int dwm_dedupe_topk(const float *w_in, const int32_t *ids_in, int64_t T, int topk, int64_t E, float *w_out,
+                    int32_t *ids_out, void *stream);
 
 #ifdef __cplusplus
 }

@@ -5,6 +5,7 @@ Test infrastructure only (see oracle/__init__.py).
 Reference files restated here:
 * patches/tpu-inference-experimental/fused-moe-fp4/0901-...:656-687
   (_fused_moe_fp4_routing: top-k routing "exactly as fused_moe_func")
+* 0901-...:98-121 (dedupe_topk)
 * patches/tpu-inference-ext/0101-...:131 (top-k weights cast to the hidden dtype)
 * patches/tpu-inference-ext/0405-moe-fast-dispatch.patch:70-98 (argsort,
   token_indices_sorted, group_sizes via one_hot(...).sum(0), row gather)
@@ -30,24 +31,83 @@ def top_k(x: np.ndarray, k: int):
     return np.take_along_axis(x, order, axis=-1), order.astype(np.int32)
 
 
-def route_topk(logits, topk: int, renormalize: bool = False, num_valid_tokens=None,
-               weight_dtype: str = "float32"):
-    """softmax -> top_k -> optional renormalize -> invalid-token mask -> cast.
+def scoring(logits: np.ndarray, scoring_fn: str) -> np.ndarray:
+    """Router scores in f32 along the last axis (apply_scoring_fn, called at
+    0901-...:667; its body is not vendored, so these are the functions'
+    definitions): "softmax" exp(x - max) / sum; "sigmoid" 1 / (1 + exp(-x));
+    "sqrtsoftplus" sqrt(log(1 + exp(x))), the DeepSeek V4 router score
+    (0901-...:176, :517 name it), with softplus in its overflow-free form
+    max(x, 0) + log1p(exp(-|x|))."""
+    x = np.asarray(logits, np.float32)
+    if scoring_fn == "softmax":
+        return softmax_f32(x)
+    if scoring_fn == "sigmoid":
+        return (np.float32(1) / (np.float32(1) + np.exp(-x))).astype(np.float32)
+    if scoring_fn == "sqrtsoftplus":
+        sp = (np.maximum(x, np.float32(0)) + np.log1p(np.exp(-np.abs(x)))).astype(np.float32)
+        return np.sqrt(sp).astype(np.float32)
+    raise ValueError(f"unknown scoring_fn {scoring_fn!r}")
 
-    0901-...:656-687 with scoring_fn softmax, no hash routing and no bias.
-    Invalid tokens get expert 0 and weight 0 (0901-...:682-686).
+
+def route_topk(logits, topk: int, renormalize: bool = False, num_valid_tokens=None,
+               weight_dtype: str = "float32", scoring_fn: str = "softmax", bias=None, hash_ids=None):
+    """scoring -> (hash ids | top_k of score + bias | top_k) -> optional
+    renormalize -> invalid-token mask -> cast (0901-...:656-687).
+
+    With ``bias`` (e_score_correction_bias) the experts are chosen on
+    score + bias and weighted by the unbiased score; with ``hash_ids``
+    (hash_based_topk_indices) the experts are given and weighted by their
+    scores.  Invalid tokens get expert 0 and weight 0 (0901-...:682-686).
+    The renormalizing sum runs over k in order.
     """
-    p = softmax_f32(logits)
-    w, ids = top_k(p, topk)
+    p = scoring(logits, scoring_fn)
+    if hash_ids is not None:
+        ids = np.asarray(hash_ids, np.int32)
+        w = np.take_along_axis(p, ids, axis=-1)
+    elif bias is not None:
+        _, ids = top_k((p + np.asarray(bias, np.float32)[None, :]).astype(np.float32), topk)
+        w = np.take_along_axis(p, ids, axis=-1)
+    else:
+        w, ids = top_k(p, topk)
+    w = w.astype(np.float32)
     if renormalize:
-        w = (w / w.sum(axis=-1, keepdims=True)).astype(np.float32)
+        tot = np.zeros(w.shape[:-1] + (1,), np.float32)
+        for j in range(w.shape[-1]):
+            tot = (tot + w[..., j:j + 1]).astype(np.float32)
+        w = (w / tot).astype(np.float32)
     if num_valid_tokens is not None:
         valid = (np.arange(w.shape[0]) < num_valid_tokens)[:, None]
         ids = np.where(valid, ids, 0).astype(np.int32)
         w = np.where(valid, w, 0.0).astype(np.float32)
     if weight_dtype == "bfloat16":
         w = round_bf16(w)
-    return w.astype(np.float32), ids
+    return w.astype(np.float32), ids.astype(np.int32)
+
+
+def dedupe_topk(topk_weights, topk_ids, num_experts: int):
+    """Makes each token's expert ids distinct (0901-...:98-121): for
+    j = 1 .. topk-1, a repeat of an earlier id adds its weight (f32) to the
+    first occurrence and is re-pointed at the first candidate in
+    arange(min(2 topk, E)) that no column of the token currently holds
+    (candidate 0 when all are held), with weight 0.  The add runs for every
+    token (adding +0.0 when there is no repeat), as the reference's
+    scatter-add does."""
+    w = np.asarray(topk_weights, np.float32).copy()
+    ids = np.asarray(topk_ids, np.int32).copy()
+    topk = ids.shape[-1]
+    cand = np.arange(min(2 * topk, num_experts), dtype=np.int32)
+    rows = np.arange(w.shape[0])
+    for j in range(1, topk):
+        same = ids[:, :j] == ids[:, j:j + 1]
+        dup = same.any(axis=-1)
+        first = np.argmax(same, axis=-1)
+        add = np.where(dup, w[:, j], np.float32(0)).astype(np.float32)
+        w[rows, first] = (w[rows, first] + add).astype(np.float32)
+        used = (ids[:, :, None] == cand[None, None, :]).any(axis=1)
+        free = cand[np.argmin(used, axis=-1)]
+        ids[:, j] = np.where(dup, free, ids[:, j])
+        w[:, j] = np.where(dup, np.float32(0), w[:, j])
+    return w, ids
 
 
 def dispatch(topk_ids: np.ndarray, num_experts: int):

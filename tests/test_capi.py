@@ -113,6 +113,23 @@ def test_checkpoint_format_argument_checks():
     assert rc == _lib.ERR_INVALID and "status" in msg
 
 
+def test_router_argument_checks():
+    null = None
+    p = ctypes.c_void_p(8)  # never dereferenced: the checks fail before any launch
+    rc, msg = _rc("dwm_route_topk", p, _lib.F32, 4, 8, 9, 0, null, null, 0, null, p, _lib.F32, p, null)
+    assert rc == _lib.ERR_INVALID and "topk" in msg
+    rc, msg = _rc("dwm_route_topk", p, _lib.F32, 4, 2048, 8, 0, null, null, 0, null, p, _lib.F32, p, null)
+    assert rc == _lib.ERR_UNSUPPORTED and "E <= 1024" in msg
+    rc, msg = _rc("dwm_route_topk", p, _lib.F32, 4, 64, 8, 7, null, null, 0, null, p, _lib.F32, p, null)
+    assert rc == _lib.ERR_INVALID and "score_fn" in msg
+    rc, msg = _rc("dwm_route_topk", null, _lib.F32, 4, 64, 8, 0, null, null, 0, null, p, _lib.F32, p, null)
+    assert rc == _lib.ERR_INVALID and "null" in msg
+    rc, _ = _rc("dwm_route_topk", null, _lib.F32, 0, 64, 8, 0, null, null, 0, null, null, _lib.F32, null, null)
+    assert rc == _lib.OK  # no tokens: nothing to do
+    rc, msg = _rc("dwm_dedupe_topk", p, p, 4, 65, 256, p, p, null)
+    assert rc == _lib.ERR_UNSUPPORTED and "topk" in msg
+
+
 def test_python_layer_rejects_host_tensors():
     import torch
     from dw_tpu_amd import e2m1_to_codes
