@@ -72,6 +72,18 @@ __device__ __forceinline__ float e8m0_to_f32(uint32_t code) {
   return __builtin_bit_cast(float, (code & 0xFFu) << 23);
 }
 
+// LDS pointer type of the direct global -> LDS loads (global_load_lds).
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// s_waitcnt immediate (gfx9 encoding): vmcnt <= vm, lgkmcnt == 0, expcnt untouched.
+__host__ __device__ constexpr int waitcnt_vm_lgkm0(int vm) { return (vm & 15) | ((vm >> 4) << 14) | (7 << 4); }
+
+// A compile-time int carried by value (generic lambdas specialise on it).
+template <int V>
+struct IntC {
+  static constexpr int value = V;
+};
+
 // Inclusive prefix sum across a 64-lane wavefront.
 __device__ __forceinline__ int wave_inclusive_scan(int v) {
   const int lane = threadIdx.x & 63;

@@ -338,6 +338,280 @@ __global__ __launch_bounds__(64 * KS) void dense_fp8_skinny_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Large M: block tiles of BM x BN = (64 WM) x (64 WN), each wave a 64 x 64
+// output of 2 x 2 MFMA 32x32 tiles.  All waves stream 64-deep K steps of the
+// lhs tile, the prepacked weight chunks and the step's scales into a ring of
+// NS LDS stages with direct global -> LDS loads (the only vector-memory
+// operations in the loop, so the waits are exact counts), one barrier per
+// step.  W8A16 decodes the e4m3 weights to bf16 (exact) and runs bf16 MFMA
+// 32x32x16; W8A8 runs the fp8 MFMA 32x32x64 on the codes.  Each 128-deep K
+// block's partial sum is scaled once into the f32 accumulator
+// (acc = fma(part, scale, acc)).
+//
+// Stage layout: lhs rows of 128 bytes (bf16) or 64 bytes (e4m3), their
+// 16-byte chunks swizzled (chunk c of row r at c ^ ((r >> 1) & 7), or
+// c ^ ((r >> 2) & 3) for 64-byte rows) so that a fragment read by 16 lanes
+// of consecutive rows hits distinct bank groups; then BN/16 weight chunks of
+// 1 KiB (the half of a prepacked 2 KiB chunk that covers the step); then the
+// scales: W8A16 the block's column scales of the step's K block, W8A8 the
+// block's row scales sx[., kb] and sw[kb, n0/128].
+template <int WM, int WN, bool A8>
+struct DenseMfmaCfg {
+  static constexpr int WAVES = WM * WN, THREADS = 64 * WAVES, WCOLS = WN;
+  static constexpr int BM = 64 * WM, BN = 64 * WN;
+  static constexpr int A_ROW = A8 ? 64 : 128;
+  static constexpr int A = 0;
+  static constexpr int B = BM * A_ROW;
+  static constexpr int S = B + BN * 64;
+  static constexpr int S_BYTES = WAVES * 256;  // one 64-value scale load per wave
+  static constexpr int STAGE = (S + S_BYTES + 1023) / 1024 * 1024;
+  static constexpr int A_LOADS = BM * A_ROW / 1024 / WAVES;  // 1 KiB lhs loads per wave per step
+  static constexpr int B_LOADS = BN / 16 / WAVES;            // 1 KiB weight loads per wave per step
+  static constexpr int S_LOADS = 1;                          // 256-byte scale loads per wave per step
+  static constexpr int LOADS = A_LOADS + B_LOADS + S_LOADS;
+  static_assert(A_LOADS * WAVES * 1024 == BM * A_ROW && B_LOADS * WAVES * 16 == BN, "loads split over the waves");
+  static_assert(!A8 || WAVES * 64 >= BM / 64 * 64 + 64, "row and weight scales fit one load per wave");
+  static_assert(BN == 128, "one 128-column weight-scale block per tile");
+};
+
+typedef __attribute__((ext_vector_type(8))) int i32x8_t;
+
+template <class C, bool A8, int NS>
+__global__ __launch_bounds__(C::THREADS) void dense_fp8_mfma_kernel(
+    const void *__restrict__ xin, const float *__restrict__ sx, int64_t M, int K, int N,
+    const uint8_t *__restrict__ wpk, const float *__restrict__ sw, int sw_ld, int ksplit, uint16_t *__restrict__ out,
+    float *__restrict__ partial) {
+  __shared__ __attribute__((aligned(1024))) uint8_t s_lds[NS * C::STAGE];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c32 = lane & 31, h = lane >> 5;
+  const int KB = K >> 7, N16 = N >> 4;
+  // Split K: blocks z = 0 .. ksplit-1 take consecutive runs of K blocks.
+  const int kb_per = (KB + ksplit - 1) / ksplit;
+  const int kb0 = blockIdx.z * kb_per;
+  const int nkb = max(0, min(KB, kb0 + kb_per) - kb0);
+  const int T = 2 * nkb;  // 64-deep steps of this block
+  const int64_t row0 = (int64_t)blockIdx.y * C::BM;
+  const int n0 = blockIdx.x * C::BN;
+  const int wm = wave / C::WCOLS, wn = wave % C::WCOLS;
+  // ---- load addressing (per lane, per step t) ----
+  // lhs: load i of this wave covers rows 8 (or 16) * (wave + WAVES * i) ..;
+  // lane l fills physical chunk l % 8 (l % 4) of its row with the logical
+  // chunk of the swizzle.
+  constexpr int RPL = A8 ? 16 : 8;  // rows per 1 KiB load
+  uint32_t aoff[C::A_LOADS];
+#pragma unroll
+  for (int i = 0; i < C::A_LOADS; ++i) {
+    const int r = RPL * (wave + C::WAVES * i) + (A8 ? (lane >> 2) : (lane >> 3));
+    int64_t gr = row0 + r;
+    if (gr >= M) gr = M - 1;
+    const int pc = A8 ? (lane & 3) : (lane & 7);
+    const int lc = A8 ? (pc ^ ((r >> 2) & 3)) : (pc ^ ((r >> 1) & 7));
+    aoff[i] = (uint32_t)(gr * (int64_t)K * (A8 ? 1 : 2)) + (uint32_t)lc * 16u;
+  }
+  const uint8_t *const abase = (const uint8_t *)xin;
+  const uint8_t *wsrc[C::B_LOADS];
+#pragma unroll
+  for (int i = 0; i < C::B_LOADS; ++i) {
+    int nb = n0 / 16 + wave + C::WAVES * i;
+    if (nb >= N16) nb = N16 - 1;
+    wsrc[i] = wpk + (int64_t)nb * KB * 2048 + lane * 16;
+  }
+  // scales: W8A16 wave w loads columns n0 + 64 w + lane of sw[kb]; W8A8
+  // waves < BM/64 load rows row0 + 64 w + lane of sx[., kb], the others
+  // sw[kb, n0/128 + lane - ...] (only the first value is used).
+  const float *ssrc;
+  int sstride;
+  if (!A8) {
+    int col = n0 + 64 * wave + lane;
+    if (col >= N) col = N - 1;
+    ssrc = sw + col;
+    sstride = sw_ld;
+  } else if (wave < C::BM / 64) {
+    int64_t r = row0 + 64 * wave + lane;
+    if (r >= M) r = M - 1;
+    ssrc = sx + r * KB;
+    sstride = 1;
+  } else {
+    ssrc = sw + n0 / 128;
+    sstride = sw_ld;
+  }
+  auto issue = [&](int stage, int t) {
+    uint8_t *const st = s_lds + stage * C::STAGE;
+    const int kb = kb0 + (t >> 1), half = t & 1;
+#pragma unroll
+    for (int i = 0; i < C::A_LOADS; ++i)
+      __builtin_amdgcn_global_load_lds((const void *)(abase + aoff[i] + (uint32_t)(kb0 * 2 + t) * (A8 ? 64u : 128u)),
+                                       (lds_void_t *)(st + C::A + (wave + C::WAVES * i) * 1024), 16, 0, 0);
+#pragma unroll
+    for (int i = 0; i < C::B_LOADS; ++i)
+      __builtin_amdgcn_global_load_lds((const void *)(wsrc[i] + (int64_t)kb * 2048 + half * 1024),
+                                       (lds_void_t *)(st + C::B + (wave + C::WAVES * i) * 1024), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((const void *)(ssrc + (int64_t)kb * sstride),
+                                     (lds_void_t *)(st + C::S + wave * 256), 4, 0, 0);
+  };
+  // ---- compute addressing ----
+  const int rA[2] = {64 * wm + c32, 64 * wm + 32 + c32};    // block-local rows of the 2 row tiles
+  const int cB[2] = {64 * wn + c32, 64 * wn + 32 + c32};    // block-local columns of the 2 column tiles
+  f32x16_t acc[2][2], part[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+  constexpr int PENDING = C::LOADS * (NS - 2);
+  static_assert(PENDING < 64, "vmcnt range");
+  if (T > 0) {
+#pragma unroll
+    for (int t = 0; t < NS - 1; ++t) issue(t, min(t, T - 1));
+  }
+  int cur = 0;
+  // One K step: MFMAs of stage `st` into part (FIRST: from zero).
+  auto step = [&](const uint8_t *st, auto first_c) {
+    constexpr bool FIRST = decltype(first_c)::value;
+    if constexpr (!A8) {
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        u32x4_t a[2], b[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const int r = rA[i];
+          const int pc = (2 * ks + h) ^ ((r >> 1) & 7);
+          a[i] = *(const u32x4_t *)(st + C::A + r * 128 + pc * 16);
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int col = cB[j];
+          const int kl = 16 * ks + 8 * h;
+          const uint32_t *pw = (const uint32_t *)(st + C::B + (col >> 4) * 1024 + (16 * (kl >> 5) + (col & 15)) * 32 +
+                                                  (kl & 31));
+          const uint32_t w0 = pw[0], w1 = pw[1];
+          b[j][0] = cvt_fp8x2_bf16<false>(w0);
+          b[j][1] = cvt_fp8x2_bf16<true>(w0);
+          b[j][2] = cvt_fp8x2_bf16<false>(w1);
+          b[j][3] = cvt_fp8x2_bf16<true>(w1);
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            if (FIRST && ks == 0) {
+              const f32x16_t z = {};
+              part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a[i]),
+                                                                   __builtin_bit_cast(bf16x8_t, b[j]), z, 0, 0, 0);
+            } else {
+              part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a[i]),
+                                                                   __builtin_bit_cast(bf16x8_t, b[j]), part[i][j], 0,
+                                                                   0, 0);
+            }
+          }
+      }
+    } else {
+      i32x8_t a[2], b[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int r = rA[i];
+        const u32x4_t lo = *(const u32x4_t *)(st + C::A + r * 64 + ((h ^ ((r >> 2) & 3)) * 16));
+        const u32x4_t hi = *(const u32x4_t *)(st + C::A + r * 64 + (((2 + h) ^ ((r >> 2) & 3)) * 16));
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          a[i][q] = (int)lo[q];
+          a[i][4 + q] = (int)hi[q];
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int col = cB[j];
+        const uint8_t *pc = st + C::B + (col >> 4) * 1024 + (col & 15) * 32 + 16 * h;
+        const u32x4_t lo = *(const u32x4_t *)pc;
+        const u32x4_t hi = *(const u32x4_t *)(pc + 16 * 32);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          b[j][q] = (int)lo[q];
+          b[j][4 + q] = (int)hi[q];
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          if (FIRST) {
+            const f32x16_t z = {};
+            part[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[i], b[j], z, 0, 0, 0, 127, 0, 127);
+          } else {
+            part[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[i], b[j], part[i][j], 0, 0, 0, 127, 0,
+                                                                         127);
+          }
+        }
+    }
+  };
+  for (int t = 0; t < T; t += 2) {
+#pragma unroll
+    for (int hs = 0; hs < 2; ++hs) {
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(PENDING));
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      // Every wave is done with step t + hs - 1: refill its stage.
+      issue(cur == 0 ? NS - 1 : cur - 1, min(t + hs + NS - 1, T - 1));
+      const uint8_t *const st = s_lds + cur * C::STAGE;
+      if (hs == 0) {
+        step(st, IntC<1>{});
+      } else {
+        step(st, IntC<0>{});
+        // The K block is complete: acc += part * scale.
+        if constexpr (!A8) {
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            const float sc = *(const float *)(st + C::S + cB[j] * 4);
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+              for (int r = 0; r < 16; ++r) acc[i][j][r] = __builtin_fmaf(part[i][j][r], sc, acc[i][j][r]);
+          }
+        } else {
+          const float swv = *(const float *)(st + C::S + (C::BM / 64) * 256);
+#pragma unroll
+          for (int i = 0; i < 2; ++i) {
+            float f[16];
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+              const f32x4_t v = *(const f32x4_t *)(st + C::S + (rA[i] - c32 + 8 * g + 4 * h) * 4);
+#pragma unroll
+              for (int q = 0; q < 4; ++q) f[4 * g + q] = v[q] * swv;
+            }
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+              for (int r = 0; r < 16; ++r) acc[i][j][r] = __builtin_fmaf(part[i][j][r], f[r], acc[i][j][r]);
+          }
+        }
+      }
+      cur = cur == NS - 1 ? 0 : cur + 1;
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
+  // Epilogue: the 32x32 layout (register r of lane (c32, h) is row
+  // 8 (r / 4) + 4 h + r % 4, column c32).
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int64_t col = n0 + cB[j];
+      if (col >= N) continue;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row = row0 + rA[i] - c32 + 8 * (r >> 2) + 4 * h + (r & 3);
+        if (row < M) {
+          if (partial) partial[((int64_t)blockIdx.z * M + row) * N + col] = acc[i][j][r];
+          else out[row * N + col] = f32_to_bf16_bits(acc[i][j][r]);
+        }
+      }
+    }
+  }
+}
+
 // out = bf16(sum_{ks} partial[ks]) in split order.
 __global__ void dense_fp8_reduce_kernel(const float *partial, int ksplit, int64_t MN, uint16_t *out) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < MN; i += (int64_t)gridDim.x * blockDim.x) {
@@ -373,10 +647,64 @@ static void launch_dense(const void *x, const float *sx, int64_t M, int64_t K, i
                      w, sw, sw_ld, ksplit, out, partial);
 }
 
+// MFMA path (M > 16, N % 128 == 0): W8A16 128x128 tiles (4 waves, three
+// 25 KB stages: two blocks per CU); W8A8 256x128 tiles (8 waves, four 26 KB
+// stages) from M >= 256, 128x128 below.  K is split over blocks until the
+// grid covers the 256 CUs; the f32 partials go to the workspace and
+// dense_fp8_reduce_kernel adds them in split order (deterministic).
+static bool dense_mfma_ok(int64_t M, int64_t K, int64_t N) {
+  return M > 16 && N % 128 == 0 && M * K * 2 < (1ll << 32) && M / 128 < 65535;
+}
+
+static int dense_mfma_ksplit(int64_t M, int64_t K, int64_t N, bool a8) {
+  const int64_t bm = (a8 && M >= 256) ? 256 : 128;
+  const int64_t tiles = (N / 128) * ((M + bm - 1) / bm);
+  int ks = 1;
+  while (tiles * ks < 256 && ks * 2 <= K / 128 && ks < 16) ks *= 2;
+  return ks;
+}
+
+template <bool A8>
+static int launch_dense_mfma(const void *x, const float *sx, int64_t M, int64_t K, int64_t N, const uint8_t *w,
+                             const float *sw, int sw_ld, uint16_t *out, void *workspace, int64_t workspace_bytes,
+                             hipStream_t st) {
+  const int ks = dense_mfma_ksplit(M, K, N, A8);
+  float *partial = nullptr;
+  if (ks > 1) {
+    const int64_t need = (int64_t)ks * M * N * 4;
+    DWM_CHECK_ARG(workspace && workspace_bytes >= need, "dense_fp8: workspace of %lld bytes needed", (long long)need);
+    partial = (float *)workspace;
+  }
+  if (A8 && M >= 256) {
+    using C = DenseMfmaCfg<4, 2, true>;
+    const dim3 grid((unsigned)(N / C::BN), (unsigned)((M + C::BM - 1) / C::BM), (unsigned)ks);
+    hipLaunchKernelGGL((dense_fp8_mfma_kernel<C, true, 4>), grid, dim3(C::THREADS), 0, st, x, sx, M, (int)K, (int)N,
+                       w, sw, sw_ld, ks, out, partial);
+  } else if (A8) {
+    using C = DenseMfmaCfg<2, 2, true>;
+    const dim3 grid((unsigned)(N / C::BN), (unsigned)((M + C::BM - 1) / C::BM), (unsigned)ks);
+    hipLaunchKernelGGL((dense_fp8_mfma_kernel<C, true, 4>), grid, dim3(C::THREADS), 0, st, x, sx, M, (int)K, (int)N,
+                       w, sw, sw_ld, ks, out, partial);
+  } else {
+    using C = DenseMfmaCfg<2, 2, false>;
+    const dim3 grid((unsigned)(N / C::BN), (unsigned)((M + C::BM - 1) / C::BM), (unsigned)ks);
+    hipLaunchKernelGGL((dense_fp8_mfma_kernel<C, false, 3>), grid, dim3(C::THREADS), 0, st, x, sx, M, (int)K,
+                       (int)N, w, sw, sw_ld, ks, out, partial);
+  }
+  int rc = launch_status("dense_fp8");
+  if (rc != DWM_OK || ks == 1) return rc;
+  const int64_t MN = M * N;
+  const int64_t blocks = (MN + 255) / 256 < 4096 ? (MN + 255) / 256 : 4096;
+  hipLaunchKernelGGL(dense_fp8_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, st, partial, ks, MN, out);
+  return launch_status("dense_fp8 reduce");
+}
+
 template <bool A8>
 static int run_dense(const void *x, const float *sx, int64_t M, int64_t K, int64_t N, const uint8_t *w,
                      const float *sw, int sw_ld, uint16_t *out, void *workspace, int64_t workspace_bytes,
                      hipStream_t st) {
+  if (dense_mfma_ok(M, K, N))
+    return launch_dense_mfma<A8>(x, sx, M, K, N, w, sw, sw_ld, out, workspace, workspace_bytes, st);
   if (M <= 16) {
     // 16 waves split K, two weight steps in flight per wave (64 KB per
     // block); measured fastest of 4/8/16 waves x 2/4/8 steps at K=7168, N=4096.
@@ -432,6 +760,12 @@ extern "C" int dwm_dense_fp8_workspace_size(int64_t M, int64_t K, int64_t N, int
   int rc = check_dense(M, K, N);
   if (rc != DWM_OK) return rc;
   DWM_CHECK_ARG(bytes, "dense_fp8_workspace_size: null pointer");
+  if (dense_mfma_ok(M, K, N)) {
+    // the larger of the W8A16 and W8A8 splits
+    const int ks = max(dense_mfma_ksplit(M, K, N, false), dense_mfma_ksplit(M, K, N, true));
+    *bytes = ks > 1 ? (int64_t)ks * M * N * 4 : 0;
+    return DWM_OK;
+  }
   const DensePlan p = dense_plan(M, K, N);
   *bytes = (M > 16 && p.ksplit > 1) ? (int64_t)p.ksplit * M * N * 4 : 0;
   return DWM_OK;

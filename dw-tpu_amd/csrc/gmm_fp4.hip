@@ -73,12 +73,6 @@ __device__ __forceinline__ void tile_classes(const int32_t *group_sizes, int num
   }
 }
 
-// s_waitcnt immediate and LDS pointer type for the direct global -> LDS loads.
-typedef __attribute__((address_space(3))) void lds_void_t;
-
-// s_waitcnt immediate (gfx9 encoding): vmcnt <= vm, lgkmcnt == 0, expcnt untouched.
-__host__ __device__ constexpr int waitcnt_vm_lgkm0(int vm) { return (vm & 15) | ((vm >> 4) << 14) | (7 << 4); }
-
 // lhs tile rows hold 8 16-byte chunks; chunk c of row r sits at physical
 // chunk c ^ ((r >> 1) & 7), so that the 16 lanes of one LDS cycle (16
 // consecutive rows, one logical chunk) hit 16 distinct 16-byte bank groups.

@@ -24,7 +24,8 @@ def _check(out, y64, ap, K):
 
 
 @pytest.mark.parametrize("M,K,N", [(1, 1024, 512), (3, 256, 48), (16, 1024, 512), (17, 512, 256),
-                                   (100, 1024, 384), (128, 1024, 512), (300, 768, 256)])
+                                   (100, 1024, 384), (128, 1024, 512), (300, 768, 256), (256, 512, 128),
+                                   (513, 1024, 640)])
 def test_w8a16_small_shapes(dev, M, K, N):
     from dw_tpu_amd.dense_fp8 import matmul
     from dw_tpu_amd.workloads import make_dense_workload
@@ -39,7 +40,7 @@ def test_w8a16_small_shapes(dev, M, K, N):
 
 
 @pytest.mark.parametrize("M,K,N", [(1, 1024, 512), (16, 1024, 512), (33, 512, 256), (128, 1024, 512),
-                                   (257, 768, 384)])
+                                   (257, 768, 384), (256, 512, 128), (600, 1024, 640)])
 def test_w8a8_small_shapes(dev, M, K, N):
     from dw_tpu_amd.dense_fp8 import matmul_w8a8
     from dw_tpu_amd.workloads import make_dense_workload
