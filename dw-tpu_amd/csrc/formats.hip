@@ -95,6 +95,75 @@ __device__ __forceinline__ float inv_or_zero(float s) {
   return __builtin_isinf(inv) ? 0.0f : inv;
 }
 
+// One MXFP4 group (32 codes of one column, checkpoint scale code sc) ->
+// 32 requantized codes (nibble i of word i / 8), the e8m0 scale code, and
+// the lossy / finite flags.  For 4 <= sc <= 252 every f32 step is exact and
+// the result has a closed form: with v the group's largest e2m1 magnitude,
+// the codes move up k = 3, 2, 2, 1, 1, 0, 0 binades (v = .5, 1, 1.5, 2, 3,
+// 4, 6) and the scale code down by k; other codes take the f32 path.
+struct Mx4Group {
+  uint32_t q[4];
+  uint32_t scode;
+  bool lossy, finite;
+};
+
+__device__ __forceinline__ Mx4Group mxfp4_group(u32x4_t in, uint32_t sc) {
+  Mx4Group r;
+  if (sc >= 4u && sc <= 252u) {
+    uint32_t vmax = 0;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const uint32_t m = in[w] & 0x77777777u;
+#pragma unroll
+      for (int b = 0; b < 8; ++b) vmax = max(vmax, (m >> (4 * b)) & 7u);
+    }
+    // k by the largest magnitude index (0: all zero), and each magnitude
+    // index's image after the k-binade shift, as nibble tables.
+    const uint32_t k = (0x00112233u >> (4 * vmax)) & 3u;
+    const uint32_t lut = k == 0 ? 0x76543210u : k == 1 ? 0x00765420u : k == 2 ? 0x00007640u : 0x00000060u;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      uint32_t o = 0;
+#pragma unroll
+      for (int b = 0; b < 8; ++b) {
+        const uint32_t c = (in[w] >> (4 * b)) & 0xFu;
+        o |= (((lut >> (4 * (c & 7u))) & 7u) | (c & 8u)) << (4 * b);
+      }
+      r.q[w] = o;
+    }
+    r.scode = vmax == 0 ? 0u : sc - k;
+    r.lossy = false;
+    r.finite = true;
+    return r;
+  }
+  // Checkpoint scale 2^(sc - 127): code 0 is 2^-127 (subnormal), 255 is NaN.
+  const float s = sc == 255u ? __builtin_bit_cast(float, 0x7FC00000u)
+                             : __builtin_bit_cast(float, sc == 0u ? 0x00400000u : sc << 23);
+  float x[32];
+  float amax = 0.0f;
+  bool finite = true;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    x[i] = e2m1_f32((in[i >> 3] >> (4 * (i & 7))) & 0xFu) * s;
+    finite = finite && __builtin_isfinite(x[i]);
+    amax = fmaxf(amax, fabsf(x[i]));
+  }
+  const float scale = pow2_ceil_f32(finite ? amax / 6.0f : 0.0f);
+  const float inv = inv_or_zero(scale);
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    uint32_t o = 0;
+#pragma unroll
+    for (int b = 0; b < 8; ++b) o |= (finite ? rne_e2m1(x[8 * w + b] * inv) : 0u) << (4 * b);
+    r.q[w] = o;
+  }
+  const uint32_t sb = __builtin_bit_cast(uint32_t, scale);
+  r.scode = finite ? (sb >> 23) & 0xFFu : 255u;
+  r.lossy = finite && (((sb & 0x807FFFFFu) != 0) || ((sb >> 23) & 0xFFu) == 255u);
+  r.finite = finite;
+  return r;
+}
+
 __global__ void format_status_zero_kernel(int32_t *status) {
   if (threadIdx.x < 2) status[threadIdx.x] = 0;
 }
@@ -120,28 +189,12 @@ __global__ __launch_bounds__(256) void mxfp4_requant_kernel(const uint8_t *__res
   const int64_t n = nt * 64 + nl;
   const int64_t kb = kt * 4 + kbl;
   const u32x4_t in = *(const u32x4_t *)(blocks + (e * N + n) * (K / 2) + kb * 16);
-  const uint32_t sc = scales[(e * N + n) * (K / 32) + kb];
-  // Checkpoint scale 2^(sc - 127): code 0 is 2^-127 (subnormal), 255 is NaN.
-  const float s = sc == 255u ? __builtin_bit_cast(float, 0x7FC00000u)
-                             : __builtin_bit_cast(float, sc == 0u ? 0x00400000u : sc << 23);
-  float x[32];
-  float amax = 0.0f;
-  bool finite = true;
-#pragma unroll
-  for (int i = 0; i < 32; ++i) {
-    const uint32_t c = (in[i >> 3] >> (4 * (i & 7))) & 0xFu;
-    x[i] = e2m1_f32(c) * s;
-    finite = finite && __builtin_isfinite(x[i]);
-    amax = fmaxf(amax, fabsf(x[i]));
-  }
-  const float scale = pow2_ceil_f32(finite ? amax / 6.0f : 0.0f);
-  const float inv = inv_or_zero(scale);
+  const Mx4Group g = mxfp4_group(in, scales[(e * N + n) * (K / 32) + kb]);
   const int cn = interleave ? ((nl & 1) ? 32 + (nl >> 1) : (nl >> 1)) : nl;
 #pragma unroll
-  for (int i = 0; i < 32; ++i) s_code[kbl * 32 + i][cn] = finite ? (uint8_t)rne_e2m1(x[i] * inv) : 0;
-  const uint32_t sb = __builtin_bit_cast(uint32_t, scale);
-  const uint32_t scode = finite ? (sb >> 23) & 0xFFu : 255u;
-  const bool lossy = finite && (((sb & 0x807FFFFFu) != 0) || ((sb >> 23) & 0xFFu) == 255u);
+  for (int i = 0; i < 32; ++i) s_code[kbl * 32 + i][cn] = (uint8_t)((g.q[i >> 3] >> (4 * (i & 7))) & 0xFu);
+  const uint32_t scode = g.scode;
+  const bool lossy = g.lossy, finite = g.finite;
   const int64_t nout = interleave ? ((n & 1) ? N / 2 + (n >> 1) : (n >> 1)) : n;
   scale_out[(e * (K / 32) + kb) * N + nout] = (uint8_t)scode;
   count_flags(lossy, status);
@@ -233,6 +286,92 @@ __global__ __launch_bounds__(256) void fp8_block_requant_kernel(const uint8_t *_
   *(u32x4_t *)(dst + 16) = *(const u32x4_t *)&s_t[kl][h * 32 + 16];
 }
 
+// ---- Tiled MXFP4 (K % 256 == 0, N % 256 == 0): whole 128-byte input rows
+// per 8 lanes and whole 128-byte output rows per 8 lanes, the transpose
+// staged in LDS.
+
+// Wave-aggregated add of a per-lane count into *counter.
+__device__ __forceinline__ void count_add(int v, int32_t *counter) {
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
+  if ((threadIdx.x & 63) == 0 && v != 0) atomicAdd(counter, v);
+}
+
+// MXFP4, block (kt, nt, e): K rows kt*256 .. +255, columns nt*256 .. +255.
+// Thread t: column octet o = t / 8 (columns 8 o .. 8 o + 7), K-block t % 8.
+// Its 32 x 8 codes are packed per row into words of 8 nibbles and staged as
+// s_out[kb][i][o] (kb blocks padded by 8 words: conflict-free writes).
+__global__ __launch_bounds__(256) void mxfp4_requant_tile_kernel(const uint8_t *__restrict__ blocks,
+                                                                 const uint8_t *__restrict__ scales, int64_t N,
+                                                                 int64_t K, int interleave,
+                                                                 uint8_t *__restrict__ codes_out,
+                                                                 uint8_t *__restrict__ scale_out,
+                                                                 int32_t *__restrict__ status) {
+  constexpr int KBW = 32 * 32 + 8;  // words per K-block of s_out
+  __shared__ __attribute__((aligned(16))) uint32_t s_out[8 * KBW];
+  __shared__ __attribute__((aligned(16))) uint8_t s_sc[8][256];
+  const int t = threadIdx.x, o = t >> 3, kb = t & 7;
+  const int64_t e = blockIdx.z, k0 = (int64_t)blockIdx.x * 256, n0 = (int64_t)blockIdx.y * 256;
+  uint32_t ow[32];
+#pragma unroll
+  for (int i = 0; i < 32; ++i) ow[i] = 0;
+  uint32_t sc_lo = 0, sc_hi = 0;
+  int nlossy = 0, nnonfinite = 0;
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    const int64_t n = n0 + 8 * o + c;
+    const u32x4_t in = *(const u32x4_t *)(blocks + (e * N + n) * (K / 2) + k0 / 2 + kb * 16);
+    const Mx4Group g = mxfp4_group(in, scales[(e * N + n) * (K / 32) + k0 / 32 + kb]);
+#pragma unroll
+    for (int i = 0; i < 32; ++i) ow[i] |= ((g.q[i >> 3] >> (4 * (i & 7))) & 0xFu) << (4 * c);
+    const uint32_t scode = g.scode;
+    nlossy += g.lossy ? 1 : 0;
+    nnonfinite += g.finite ? 0 : 1;
+    if (c < 4) sc_lo |= scode << (8 * c);
+    else sc_hi |= scode << (8 * (c - 4));
+  }
+  if (!interleave) {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) s_out[kb * KBW + i * 32 + o] = ow[i];
+    *(uint32_t *)&s_sc[kb][8 * o] = sc_lo;
+    *(uint32_t *)&s_sc[kb][8 * o + 4] = sc_hi;
+  } else {
+    // Even columns (w1) go to the first half of the output, odd (w3) to the
+    // second: this octet's even / odd nibbles are positions 4 o .. 4 o + 3.
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      const uint32_t w = ow[i];
+      const uint32_t ev = (w & 0xFu) | ((w >> 4) & 0xF0u) | ((w >> 8) & 0xF00u) | ((w >> 12) & 0xF000u);
+      const uint32_t od = ((w >> 4) & 0xFu) | ((w >> 8) & 0xF0u) | ((w >> 12) & 0xF00u) | ((w >> 16) & 0xF000u);
+      uint16_t *row = (uint16_t *)&s_out[kb * KBW + i * 32];
+      row[o] = (uint16_t)ev;
+      row[32 + o] = (uint16_t)od;
+    }
+    const uint32_t sev = (sc_lo & 0xFFu) | ((sc_lo >> 8) & 0xFF00u) | ((sc_hi << 16) & 0xFF0000u) | ((sc_hi << 8) & 0xFF000000u);
+    const uint32_t sod = ((sc_lo >> 8) & 0xFFu) | ((sc_lo >> 16) & 0xFF00u) | ((sc_hi << 8) & 0xFF0000u) | (sc_hi & 0xFF000000u);
+    *(uint32_t *)&s_sc[kb][4 * o] = sev;
+    *(uint32_t *)&s_sc[kb][128 + 4 * o] = sod;
+  }
+  count_add(nlossy, status);
+  count_add(nnonfinite, status + 1);
+  __syncthreads();
+  // 256 output rows of 128 bytes, 8 lanes per row.
+#pragma unroll
+  for (int p = 0; p < 8; ++p) {
+    const int row = 32 * p + (t >> 3), ch = t & 7;
+    const u32x4_t v = *(const u32x4_t *)&s_out[(row >> 5) * KBW + (row & 31) * 32 + ch * 4];
+    const int64_t colbyte = interleave ? (ch < 4 ? 0 : N / 4) + (n0 / 2) / 2 + (ch & 3) * 16 : n0 / 2 + ch * 16;
+    *(u32x4_t *)(codes_out + (e * K + k0 + row) * (N / 2) + colbyte) = v;
+  }
+  // 8 rows of 256 scale codes, 16 lanes per row.
+  if (t < 128) {
+    const int row = t >> 4, ch = t & 15;
+    const u32x4_t v = *(const u32x4_t *)&s_sc[row][ch * 16];
+    const int64_t col = interleave ? (ch < 8 ? 0 : N / 2) + n0 / 2 + (ch & 7) * 16 : n0 + ch * 16;
+    *(u32x4_t *)(scale_out + (e * (K / 32) + k0 / 32 + row) * N + col) = v;
+  }
+}
+
 }  // namespace dwm
 
 using namespace dwm;
@@ -253,8 +392,13 @@ extern "C" int dwm_mxfp4_requant(const uint8_t *blocks, const uint8_t *scales, i
   DWM_CHECK_ARG(blocks && scales && codes_out && scale_codes_out, "mxfp4_requant: null pointer");
   DWM_CHECK_ARG((uintptr_t)blocks % 16 == 0 && (uintptr_t)codes_out % 16 == 0,
                 "mxfp4_requant: blocks and codes_out must be 16-byte aligned");
-  hipLaunchKernelGGL(mxfp4_requant_kernel, dim3((unsigned)(K / 128), (unsigned)(N / 64), (unsigned)E), dim3(256), 0,
-                     st, blocks, scales, N, K, w13_interleave ? 1 : 0, codes_out, scale_codes_out, status);
+  if (K % 256 == 0 && N % 256 == 0)
+    hipLaunchKernelGGL(mxfp4_requant_tile_kernel, dim3((unsigned)(K / 256), (unsigned)(N / 256), (unsigned)E),
+                       dim3(256), 0, st, blocks, scales, N, K, w13_interleave ? 1 : 0, codes_out, scale_codes_out,
+                       status);
+  else
+    hipLaunchKernelGGL(mxfp4_requant_kernel, dim3((unsigned)(K / 128), (unsigned)(N / 64), (unsigned)E), dim3(256),
+                       0, st, blocks, scales, N, K, w13_interleave ? 1 : 0, codes_out, scale_codes_out, status);
   return launch_status("mxfp4_requant");
 }
 
@@ -272,6 +416,6 @@ extern "C" int dwm_fp8_block_requant(const uint8_t *w, const float *scale, int64
   DWM_CHECK_ARG((uintptr_t)w % 16 == 0 && (uintptr_t)w_out % 16 == 0 && (uintptr_t)scale % 4 == 0,
                 "fp8_block_requant: w and w_out must be 16-byte aligned");
   hipLaunchKernelGGL(fp8_block_requant_kernel, dim3((unsigned)(K / 128), (unsigned)(N / 64)), dim3(256), 0, st, w,
-                     scale, K, N, input_nk ? 1 : 0, w_out, scale_out, status);
+                       scale, K, N, input_nk ? 1 : 0, w_out, scale_out, status);
   return launch_status("fp8_block_requant");
 }

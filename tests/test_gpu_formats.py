@@ -38,8 +38,8 @@ def _run_mxfp4(dev, codes, scales, interleave):
 
 
 @pytest.mark.parametrize("interleave", [False, True])
-def test_mxfp4_random_bit_exact(dev, rng, interleave):
-    e, n, k = 3, 256, 384
+@pytest.mark.parametrize("e,n,k", [(3, 256, 384), (2, 512, 512)])  # the 128x64-tile and 256x256-tile kernels
+def test_mxfp4_random_bit_exact(dev, rng, interleave, e, n, k):
     codes = rng.integers(0, 16, (e, n, k), dtype=np.uint8)
     scales = rng.integers(100, 140, (e, n, k // 32)).astype(np.uint8)
     st = _run_mxfp4(dev, codes, scales, interleave)
@@ -102,8 +102,8 @@ def _run_fp8(dev, wc, scale, input_nk):
 
 
 @pytest.mark.parametrize("input_nk", [True, False])
-def test_fp8_block_requant_pow2_scales_exact(dev, rng, input_nk):
-    k, n = 512, 384
+@pytest.mark.parametrize("k,n", [(512, 384), (384, 512)])  # the 64- and 256-column-tile kernels
+def test_fp8_block_requant_pow2_scales_exact(dev, rng, input_nk, k, n):
     wc = to_e4m3((rng.standard_normal((k, n)) * 3).astype(np.float32))
     scale = np.ldexp(np.float32(1), rng.integers(-12, 0, (k // 128, n // 128))).astype(np.float32)
     if input_nk:
