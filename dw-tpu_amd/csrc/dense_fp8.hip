@@ -688,7 +688,7 @@ static int launch_dense_mfma(const void *x, const float *sx, int64_t M, int64_t 
   } else {
     using C = DenseMfmaCfg<2, 2, false>;
     const dim3 grid((unsigned)(N / C::BN), (unsigned)((M + C::BM - 1) / C::BM), (unsigned)ks);
-    hipLaunchKernelGGL((dense_fp8_mfma_kernel<C, false, 3>), grid, dim3(C::THREADS), 0, st, x, sx, M, (int)K,
+    hipLaunchKernelGGL((dense_fp8_mfma_kernel<C, false, 2>), grid, dim3(C::THREADS), 0, st, x, sx, M, (int)K,
                        (int)N, w, sw, sw_ld, ks, out, partial);
   }
   int rc = launch_status("dense_fp8");
