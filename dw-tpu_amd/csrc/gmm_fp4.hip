@@ -356,32 +356,28 @@ __device__ __forceinline__ void ws_consumer(int T, uint8_t *s_lds, int cw, int64
   }
 }
 
-template <class C, int MB, bool ACT>
-__global__ __launch_bounds__(C::THREADS) void gmm_fp4_ws_kernel(
-    const uint16_t *__restrict__ lhs, int64_t M, int K, const uint8_t *__restrict__ wpk,
-    const uint8_t *__restrict__ spk, const int32_t *__restrict__ group_sizes, int num_groups,
-    const int32_t *__restrict__ group_offset, int64_t e_local, int N, void *__restrict__ out,
-    int out_f32) {
-  constexpr int MT = 32 * MB;
-  constexpr int NT = C::NT;
-  constexpr int CW = C::CONS;
-  static_assert(C::STAGES * C::STAGE >= (kMaxGroups + MB * kClsStride) * 4, "tile classes alias the stages");
-  __shared__ __attribute__((aligned(1024))) uint8_t s_lds[C::STAGES * C::STAGE];
-  __shared__ int s_info[3];
-  int *s_rowstart = (int *)s_lds;
-  int *s_cls = s_rowstart + kMaxGroups;
+// The block's tile: (local group g, rows row0 .. row0 + rows - 1) x column
+// tile nt.
+struct TileRef {
+  int g, rows, nt;
+  int64_t row0;
+};
 
-  const int tid = threadIdx.x, wave = tid >> 6;
-  const int go = group_offset ? group_offset[0] : 0;
+// Every thread of the block calls this (it holds two block barriers).  Work
+// list: the (row tile, column tile) pairs of class 0 (MB blocks), then class
+// 1, ... (longest first, so the dispatcher's in-order refill of free CUs
+// balances them).  Each class is cut into 8 contiguous runs, one per XCD
+// (blocks equal mod 8 run on one XCD), so a row tile's column tiles share
+// that XCD's L2.  Returns false when the block has no tile.
+template <int MB, int THREADS>
+__device__ __forceinline__ bool find_tile(const int32_t *__restrict__ group_sizes, int num_groups, int go,
+                                          int64_t e_local, int64_t M, int n_tiles, int *s_rowstart, int *s_cls,
+                                          int *s_info, TileRef &ref) {
+  constexpr int MT = 32 * MB;
+  const int tid = threadIdx.x;
   tile_classes<MB>(group_sizes, num_groups, go, e_local, s_rowstart, s_cls);
   if (tid == 0) s_info[0] = -1;
   __syncthreads();
-  // Work list: the (row tile, column tile) pairs of class 0 (MB blocks), then
-  // class 1, ... (longest first, so the dispatcher's in-order refill of free
-  // CUs balances them).  Each class is cut into 8 contiguous runs, one per
-  // XCD (blocks equal mod 8 run on one XCD), so a row tile's column tiles
-  // share that XCD's L2.
-  const int n_tiles = (N + NT - 1) / NT;
   const int xcd = blockIdx.x & 7;
   int64_t j = blockIdx.x >> 3;
   int cls = -1;
@@ -404,7 +400,7 @@ __global__ __launch_bounds__(C::THREADS) void gmm_fp4_ws_kernel(
   const int trow = cls >= 0 ? (int)(entry / n_tiles) : -1;
   if (cls >= 0) {
     const int *const cs = s_cls + cls * kClsStride;
-    for (int g = tid; g < num_groups; g += C::THREADS) {
+    for (int g = tid; g < num_groups; g += THREADS) {
       if (cs[g] <= trow && trow < cs[g + 1]) {
         const int sz = group_sizes[g];
         // Class 0 holds the full tiles (then a partial one of MB blocks);
@@ -417,12 +413,37 @@ __global__ __launch_bounds__(C::THREADS) void gmm_fp4_ws_kernel(
     }
   }
   __syncthreads();  // also retires the class reads before the stages overwrite them
-  const int g = s_info[0];
-  if (cls < 0 || g < 0) return;
-  const int nt = (int)(entry % n_tiles);
-  const int64_t row0 = s_info[1];
-  if (row0 >= M) return;
-  const int rows = (int)min((int64_t)s_info[2], M - row0);
+  ref.g = s_info[0];
+  if (cls < 0 || ref.g < 0) return false;
+  ref.nt = (int)(entry % n_tiles);
+  ref.row0 = s_info[1];
+  if (ref.row0 >= M) return false;
+  ref.rows = (int)min((int64_t)s_info[2], M - ref.row0);
+  return true;
+}
+
+template <class C, int MB, bool ACT>
+__global__ __launch_bounds__(C::THREADS) void gmm_fp4_ws_kernel(
+    const uint16_t *__restrict__ lhs, int64_t M, int K, const uint8_t *__restrict__ wpk,
+    const uint8_t *__restrict__ spk, const int32_t *__restrict__ group_sizes, int num_groups,
+    const int32_t *__restrict__ group_offset, int64_t e_local, int N, void *__restrict__ out,
+    int out_f32) {
+  constexpr int NT = C::NT;
+  constexpr int CW = C::CONS;
+  static_assert(C::STAGES * C::STAGE >= (kMaxGroups + MB * kClsStride) * 4, "tile classes alias the stages");
+  __shared__ __attribute__((aligned(1024))) uint8_t s_lds[C::STAGES * C::STAGE];
+  __shared__ int s_info[3];
+  int *s_rowstart = (int *)s_lds;
+  int *s_cls = s_rowstart + kMaxGroups;
+
+  const int tid = threadIdx.x, wave = tid >> 6;
+  const int go = group_offset ? group_offset[0] : 0;
+  TileRef ref;
+  if (!find_tile<MB, C::THREADS>(group_sizes, num_groups, go, e_local, M, (N + NT - 1) / NT, s_rowstart, s_cls,
+                                 s_info, ref))
+    return;
+  const int g = ref.g, nt = ref.nt, rows = ref.rows;
+  const int64_t row0 = ref.row0;
   const int64_t e = g - go;
   const int T = K >> 6, KB = K >> 7, G = (N + 63) >> 6;
   const int g0 = nt * C::GT;  // first 64-column group of the tile
