@@ -75,6 +75,26 @@ __device__ __forceinline__ float e8m0_to_f32(uint32_t code) {
 // LDS pointer type of the direct global -> LDS loads (global_load_lds).
 typedef __attribute__((address_space(3))) void lds_void_t;
 
+// Raw buffer resource over [base, base + bytes) (gfx9 descriptor word 3:
+// 32-bit data format, no swizzle) for buffer_load ... lds: the address is a
+// scalar base plus a per-lane 32-bit offset plus a scalar offset, so a load
+// stream that advances by a uniform stride needs no vector arithmetic.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// SIZE bytes per lane from rsrc at voffset + soffset into LDS at lds + SIZE * lane
+// (SIZE must be a literal: the builtin takes it as an immediate).  The host
+// pass of a HIP compile also instantiates kernel templates, to emit their
+// launch stubs; it rejects this target builtin inside them without a
+// diagnostic and drops the stub, so there the call is a no-op.
+#if defined(__HIP_DEVICE_COMPILE__)
+#define buffer_load_lds(SIZE, rsrc, lds, voffset, soffset) \
+  __builtin_amdgcn_raw_ptr_buffer_load_lds((rsrc), (lds_void_t *)(lds), SIZE, (voffset), (soffset), 0, 0)
+#else
+#define buffer_load_lds(SIZE, rsrc, lds, voffset, soffset) ((void)(rsrc), (void)(lds), (void)(voffset), (void)(soffset))
+#endif
+
 // s_waitcnt immediate (gfx9 encoding): vmcnt <= vm, lgkmcnt == 0, expcnt untouched.
 __host__ __device__ constexpr int waitcnt_vm_lgkm0(int vm) { return (vm & 15) | ((vm >> 4) << 14) | (7 << 4); }
 

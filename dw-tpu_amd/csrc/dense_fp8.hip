@@ -353,9 +353,12 @@ __global__ __launch_bounds__(64 * KS) void dense_fp8_skinny_kernel(
 // 16-byte chunks swizzled (chunk c of row r at c ^ ((r >> 1) & 7), or
 // c ^ ((r >> 2) & 3) for 64-byte rows) so that a fragment read by 16 lanes
 // of consecutive rows hits distinct bank groups; then BN/16 weight chunks of
-// 1 KiB (the half of a prepacked 2 KiB chunk that covers the step); then the
-// scales: W8A16 the block's column scales of the step's K block, W8A8 the
-// block's row scales sx[., kb] and sw[kb, n0/128].
+// 1 KiB (the half of a prepacked 2 KiB chunk that covers the step: 16-byte
+// slot 32 q + 2 c + p holds k = 32 q + 16 p .. + 15 of column c), stored
+// with p flipped for c >= 8 (lane l loads slot l ^ ((l >> 4) & 1)), so that
+// 16 lanes reading one slot of 16 consecutive columns hit distinct bank
+// groups; then the scales: W8A16 the block's column scales of the step's K
+// block, W8A8 the block's row scales sx[., kb] and sw[kb, n0/128].
 template <int WM, int WN, bool A8>
 struct DenseMfmaCfg {
   static constexpr int WAVES = WM * WN, THREADS = 64 * WAVES, WCOLS = WN;
@@ -377,13 +380,16 @@ struct DenseMfmaCfg {
 
 typedef __attribute__((ext_vector_type(8))) int i32x8_t;
 
-template <class C, bool A8, int NS>
+template <class C, bool A8, int NS, bool PF = false>
 __global__ __launch_bounds__(C::THREADS) void dense_fp8_mfma_kernel(
     const void *__restrict__ xin, const float *__restrict__ sx, int64_t M, int K, int N,
     const uint8_t *__restrict__ wpk, const float *__restrict__ sw, int sw_ld, int ksplit, uint16_t *__restrict__ out,
     float *__restrict__ partial) {
   __shared__ __attribute__((aligned(1024))) uint8_t s_lds[NS * C::STAGE];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // The wave index is made wave-uniform, so that every load address below
+  // is a scalar base plus a per-lane 32-bit offset (no per-step vector
+  // address arithmetic) and the LDS destinations are scalar.
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c32 = lane & 31, h = lane >> 5;
   const int KB = K >> 7, N16 = N >> 4;
   // Split K: blocks z = 0 .. ksplit-1 take consecutive runs of K blocks.
@@ -409,46 +415,46 @@ __global__ __launch_bounds__(C::THREADS) void dense_fp8_mfma_kernel(
     const int lc = A8 ? (pc ^ ((r >> 2) & 3)) : (pc ^ ((r >> 1) & 7));
     aoff[i] = (uint32_t)(gr * (int64_t)K * (A8 ? 1 : 2)) + (uint32_t)lc * 16u;
   }
-  const uint8_t *const abase = (const uint8_t *)xin;
-  const uint8_t *wsrc[C::B_LOADS];
+  const __amdgpu_buffer_rsrc_t arsrc = make_rsrc(xin, (uint32_t)(M * K * (A8 ? 1 : 2)));
+  const __amdgpu_buffer_rsrc_t wrsrc = make_rsrc(wpk, (uint32_t)((int64_t)K * N));
+  uint32_t woff[C::B_LOADS];
 #pragma unroll
   for (int i = 0; i < C::B_LOADS; ++i) {
     int nb = n0 / 16 + wave + C::WAVES * i;
     if (nb >= N16) nb = N16 - 1;
-    wsrc[i] = wpk + (int64_t)nb * KB * 2048 + lane * 16;
+    woff[i] = (uint32_t)nb * (uint32_t)KB * 2048u + (uint32_t)(lane ^ ((lane >> 4) & 1)) * 16u;
   }
   // scales: W8A16 wave w loads columns n0 + 64 w + lane of sw[kb]; W8A8
   // waves < BM/64 load rows row0 + 64 w + lane of sx[., kb], the others
   // sw[kb, n0/128 + lane - ...] (only the first value is used).
-  const float *ssrc;
-  int sstride;
+  __amdgpu_buffer_rsrc_t srsrc;
+  uint32_t slane, sstride;  // bytes: per-lane offset, per K block
   if (!A8) {
-    int col = n0 + 64 * wave + lane;
-    if (col >= N) col = N - 1;
-    ssrc = sw + col;
-    sstride = sw_ld;
+    srsrc = make_rsrc(sw, (uint32_t)KB * (uint32_t)sw_ld * 4u);
+    slane = (uint32_t)min(n0 + 64 * wave + lane, N - 1) * 4u;
+    sstride = (uint32_t)sw_ld * 4u;
   } else if (wave < C::BM / 64) {
     int64_t r = row0 + 64 * wave + lane;
     if (r >= M) r = M - 1;
-    ssrc = sx + r * KB;
-    sstride = 1;
+    srsrc = make_rsrc(sx, (uint32_t)(M * KB * 4));
+    slane = (uint32_t)(r * KB) * 4u;
+    sstride = 4;
   } else {
-    ssrc = sw + n0 / 128;
-    sstride = sw_ld;
+    srsrc = make_rsrc(sw, (uint32_t)KB * (uint32_t)sw_ld * 4u);
+    slane = (uint32_t)(n0 / 128) * 4u;
+    sstride = (uint32_t)sw_ld * 4u;
   }
   auto issue = [&](int stage, int t) {
     uint8_t *const st = s_lds + stage * C::STAGE;
-    const int kb = kb0 + (t >> 1), half = t & 1;
+    const uint32_t kb = (uint32_t)(kb0 + (t >> 1)), half = (uint32_t)(t & 1);
+    const uint32_t astep = (uint32_t)(kb0 * 2 + t) * (A8 ? 64u : 128u);
 #pragma unroll
     for (int i = 0; i < C::A_LOADS; ++i)
-      __builtin_amdgcn_global_load_lds((const void *)(abase + aoff[i] + (uint32_t)(kb0 * 2 + t) * (A8 ? 64u : 128u)),
-                                       (lds_void_t *)(st + C::A + (wave + C::WAVES * i) * 1024), 16, 0, 0);
+      buffer_load_lds(16, arsrc, st + C::A + (wave + C::WAVES * i) * 1024, aoff[i], astep);
 #pragma unroll
     for (int i = 0; i < C::B_LOADS; ++i)
-      __builtin_amdgcn_global_load_lds((const void *)(wsrc[i] + (int64_t)kb * 2048 + half * 1024),
-                                       (lds_void_t *)(st + C::B + (wave + C::WAVES * i) * 1024), 16, 0, 0);
-    __builtin_amdgcn_global_load_lds((const void *)(ssrc + (int64_t)kb * sstride),
-                                     (lds_void_t *)(st + C::S + wave * 256), 4, 0, 0);
+      buffer_load_lds(16, wrsrc, st + C::B + (wave + C::WAVES * i) * 1024, woff[i], kb * 2048u + half * 1024u);
+    buffer_load_lds(4, srsrc, st + C::S + wave * 256, slane, kb * sstride);
   };
   // ---- compute addressing ----
   const int rA[2] = {64 * wm + c32, 64 * wm + 32 + c32};    // block-local rows of the 2 row tiles
@@ -460,92 +466,105 @@ __global__ __launch_bounds__(C::THREADS) void dense_fp8_mfma_kernel(
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-  constexpr int PENDING = C::LOADS * (NS - 2);
-  static_assert(PENDING < 64, "vmcnt range");
+  // PF: a wave reads the fragments of MFMA substep s + 1 (of step t + 1
+  // after the last substep of step t) while substep s's MFMAs run, so the
+  // barrier of step t also waits for step t + 1 to land.
+  constexpr int PENDING = C::LOADS * (NS - (PF ? 3 : 2));
+  static_assert(PENDING >= 0 && PENDING < 64, "vmcnt range");
   if (T > 0) {
 #pragma unroll
     for (int t = 0; t < NS - 1; ++t) issue(t, min(t, T - 1));
   }
   int cur = 0;
-  // One K step: MFMAs of stage `st` into part (FIRST: from zero).
-  auto step = [&](const uint8_t *st, auto first_c) {
-    constexpr bool FIRST = decltype(first_c)::value;
-    if constexpr (!A8) {
+  // W8A16: lane (c32, h) takes k = 32 h + 8 ks .. + 7 of the step in MFMA
+  // substep ks (the same k for the lhs chunk and the weight codes, so every
+  // product is formed once): per step 32 codes of each of its 2 columns, per
+  // substep one lhs chunk of each of its 2 rows.
+  struct Frag16 {
+    u32x4_t a[2];
+  };
+  u32x4_t w16[2][2];  // [column tile][k 32 h .. + 15, + 16 .. + 31]
+  auto read16w = [&](const uint8_t *st, u32x4_t (*w)[2]) {
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        u32x4_t a[2], b[2];
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          const int r = rA[i];
-          const int pc = (2 * ks + h) ^ ((r >> 1) & 7);
-          a[i] = *(const u32x4_t *)(st + C::A + r * 128 + pc * 16);
-        }
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const int col = cB[j];
-          const int kl = 16 * ks + 8 * h;
-          const uint32_t *pw = (const uint32_t *)(st + C::B + (col >> 4) * 1024 + (16 * (kl >> 5) + (col & 15)) * 32 +
-                                                  (kl & 31));
-          const uint32_t w0 = pw[0], w1 = pw[1];
-          b[j][0] = cvt_fp8x2_bf16<false>(w0);
-          b[j][1] = cvt_fp8x2_bf16<true>(w0);
-          b[j][2] = cvt_fp8x2_bf16<false>(w1);
-          b[j][3] = cvt_fp8x2_bf16<true>(w1);
-        }
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-          for (int j = 0; j < 2; ++j) {
-            if (FIRST && ks == 0) {
-              const f32x16_t z = {};
-              part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a[i]),
-                                                                   __builtin_bit_cast(bf16x8_t, b[j]), z, 0, 0, 0);
-            } else {
-              part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a[i]),
-                                                                   __builtin_bit_cast(bf16x8_t, b[j]), part[i][j], 0,
-                                                                   0, 0);
-            }
-          }
-      }
-    } else {
-      i32x8_t a[2], b[2];
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int r = rA[i];
-        const u32x4_t lo = *(const u32x4_t *)(st + C::A + r * 64 + ((h ^ ((r >> 2) & 3)) * 16));
-        const u32x4_t hi = *(const u32x4_t *)(st + C::A + r * 64 + (((2 + h) ^ ((r >> 2) & 3)) * 16));
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          a[i][q] = (int)lo[q];
-          a[i][4 + q] = (int)hi[q];
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int col = cB[j];
-        const uint8_t *pc = st + C::B + (col >> 4) * 1024 + (col & 15) * 32 + 16 * h;
-        const u32x4_t lo = *(const u32x4_t *)pc;
-        const u32x4_t hi = *(const u32x4_t *)(pc + 16 * 32);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          b[j][q] = (int)lo[q];
-          b[j][4 + q] = (int)hi[q];
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          if (FIRST) {
-            const f32x16_t z = {};
-            part[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[i], b[j], z, 0, 0, 0, 127, 0, 127);
-          } else {
-            part[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[i], b[j], part[i][j], 0, 0, 0, 127, 0,
-                                                                         127);
-          }
-        }
+    for (int j = 0; j < 2; ++j) {
+      const int c = cB[j] & 15;
+      const uint8_t *pw = st + C::B + (cB[j] >> 4) * 1024 + (32 * h + 2 * c) * 16;
+      w[j][0] = *(const u32x4_t *)(pw + 16 * (c >> 3));
+      w[j][1] = *(const u32x4_t *)(pw + 16 * ((c >> 3) ^ 1));
     }
   };
+  auto read16 = [&](const uint8_t *st, int ks, Frag16 &f) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int r = rA[i];
+      const int pc = (4 * h + ks) ^ ((r >> 1) & 7);
+      f.a[i] = *(const u32x4_t *)(st + C::A + r * 128 + pc * 16);
+    }
+  };
+  auto mma16 = [&](const Frag16 &f, const u32x4_t (*w)[2], int ks, bool first) {
+    u32x4_t b[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const uint32_t w0 = w[j][ks >> 1][2 * (ks & 1)], w1 = w[j][ks >> 1][2 * (ks & 1) + 1];
+      b[j][0] = cvt_fp8x2_bf16<false>(w0);
+      b[j][1] = cvt_fp8x2_bf16<true>(w0);
+      b[j][2] = cvt_fp8x2_bf16<false>(w1);
+      b[j][3] = cvt_fp8x2_bf16<true>(w1);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const f32x16_t z = {};
+        part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, f.a[i]),
+                                                             __builtin_bit_cast(bf16x8_t, b[j]),
+                                                             first ? z : part[i][j], 0, 0, 0);
+      }
+  };
+  // W8A8 step (64 deep): 32 lhs codes per row tile and 32 weight codes per
+  // column tile.
+  struct Frag8 {
+    i32x8_t a[2], b[2];
+  };
+  auto read8 = [&](const uint8_t *st, Frag8 &f) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int r = rA[i];
+      const u32x4_t lo = *(const u32x4_t *)(st + C::A + r * 64 + ((h ^ ((r >> 2) & 3)) * 16));
+      const u32x4_t hi = *(const u32x4_t *)(st + C::A + r * 64 + (((2 + h) ^ ((r >> 2) & 3)) * 16));
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        f.a[i][q] = (int)lo[q];
+        f.a[i][4 + q] = (int)hi[q];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int col = cB[j];
+      const int c = col & 15;
+      const uint8_t *pc = st + C::B + (col >> 4) * 1024 + c * 32 + 16 * (h ^ (c >> 3));
+      const u32x4_t lo = *(const u32x4_t *)pc;
+      const u32x4_t hi = *(const u32x4_t *)(pc + 16 * 32);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        f.b[j][q] = (int)lo[q];
+        f.b[j][4 + q] = (int)hi[q];
+      }
+    }
+  };
+  auto mma8 = [&](const Frag8 &f, bool first) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const f32x16_t z = {};
+        part[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.a[i], f.b[j], first ? z : part[i][j], 0, 0, 0,
+                                                                     127, 0, 127);
+      }
+  };
+  Frag16 f16;
+  u32x4_t w16n[2][2];  // PF: the next step's weight codes
+  Frag8 f8;
   for (int t = 0; t < T; t += 2) {
 #pragma unroll
     for (int hs = 0; hs < 2; ++hs) {
@@ -556,10 +575,54 @@ __global__ __launch_bounds__(C::THREADS) void dense_fp8_mfma_kernel(
       // Every wave is done with step t + hs - 1: refill its stage.
       issue(cur == 0 ? NS - 1 : cur - 1, min(t + hs + NS - 1, T - 1));
       const uint8_t *const st = s_lds + cur * C::STAGE;
-      if (hs == 0) {
-        step(st, IntC<1>{});
+      const int nxt = cur == NS - 1 ? 0 : cur + 1;
+      // PF: step t + hs + 1 has landed and its stage is not refilled before
+      // the next barrier (in the last step the prefetch reads stale stage
+      // contents that are never used).
+      const uint8_t *const sx = s_lds + nxt * C::STAGE;
+      if constexpr (!A8) {
+        if constexpr (PF) {
+          if (t + hs == 0) {
+            read16w(st, w16n);
+            read16(st, 0, f16);
+          }
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            w16[j][0] = w16n[j][0];
+            w16[j][1] = w16n[j][1];
+          }
+        } else {
+          read16w(st, w16);
+        }
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          if constexpr (PF) {
+            const Frag16 c = f16;
+            __builtin_amdgcn_sched_barrier(0);
+            if (ks < 3) read16(st, ks + 1, f16);
+            else read16(sx, 0, f16);
+            if (ks == 0) read16w(sx, w16n);
+            mma16(c, w16, ks, hs == 0 && ks == 0);
+            __builtin_amdgcn_sched_barrier(0);
+          } else {
+            read16(st, ks, f16);
+            mma16(f16, w16, ks, hs == 0 && ks == 0);
+          }
+        }
       } else {
-        step(st, IntC<0>{});
+        if constexpr (PF) {
+          if (t + hs == 0) read8(st, f8);
+          const Frag8 c = f8;
+          __builtin_amdgcn_sched_barrier(0);
+          read8(sx, f8);
+          mma8(c, hs == 0);
+          __builtin_amdgcn_sched_barrier(0);
+        } else {
+          read8(st, f8);
+          mma8(f8, hs == 0);
+        }
+      }
+      if (hs == 1) {
         // The K block is complete: acc += part * scale.
         if constexpr (!A8) {
 #pragma unroll
@@ -588,7 +651,7 @@ __global__ __launch_bounds__(C::THREADS) void dense_fp8_mfma_kernel(
           }
         }
       }
-      cur = cur == NS - 1 ? 0 : cur + 1;
+      cur = nxt;
     }
   }
   __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
@@ -647,13 +710,13 @@ static void launch_dense(const void *x, const float *sx, int64_t M, int64_t K, i
                      w, sw, sw_ld, ksplit, out, partial);
 }
 
-// MFMA path (M > 16, N % 128 == 0): W8A16 128x128 tiles (4 waves, three
-// 25 KB stages: two blocks per CU); W8A8 256x128 tiles (8 waves, four 26 KB
-// stages) from M >= 256, 128x128 below.  K is split over blocks until the
+// MFMA path (M > 16, N % 128 == 0): W8A16 128x128 tiles (4 waves, two or
+// three 25 KB stages: two blocks per CU); W8A8 256x128 tiles (8 waves, four
+// 26 KB stages, fragments read one step ahead) from M >= 256, 128x128 below.  K is split over blocks until the
 // grid covers the 256 CUs; the f32 partials go to the workspace and
 // dense_fp8_reduce_kernel adds them in split order (deterministic).
 static bool dense_mfma_ok(int64_t M, int64_t K, int64_t N) {
-  return M > 16 && N % 128 == 0 && M * K * 2 < (1ll << 32) && M / 128 < 65535;
+  return M > 16 && N % 128 == 0 && M * K * 2 < (1ll << 32) && K * N < (1ll << 32) && M / 128 < 65535;
 }
 
 static int dense_mfma_ksplit(int64_t M, int64_t K, int64_t N, bool a8) {
@@ -678,18 +741,24 @@ static int launch_dense_mfma(const void *x, const float *sx, int64_t M, int64_t 
   if (A8 && M >= 256) {
     using C = DenseMfmaCfg<4, 2, true>;
     const dim3 grid((unsigned)(N / C::BN), (unsigned)((M + C::BM - 1) / C::BM), (unsigned)ks);
-    hipLaunchKernelGGL((dense_fp8_mfma_kernel<C, true, 4>), grid, dim3(C::THREADS), 0, st, x, sx, M, (int)K, (int)N,
-                       w, sw, sw_ld, ks, out, partial);
+    hipLaunchKernelGGL((dense_fp8_mfma_kernel<C, true, 4, true>), grid, dim3(C::THREADS), 0, st, x, sx, M, (int)K,
+                       (int)N, w, sw, sw_ld, ks, out, partial);
   } else if (A8) {
     using C = DenseMfmaCfg<2, 2, true>;
     const dim3 grid((unsigned)(N / C::BN), (unsigned)((M + C::BM - 1) / C::BM), (unsigned)ks);
-    hipLaunchKernelGGL((dense_fp8_mfma_kernel<C, true, 4>), grid, dim3(C::THREADS), 0, st, x, sx, M, (int)K, (int)N,
-                       w, sw, sw_ld, ks, out, partial);
+    hipLaunchKernelGGL((dense_fp8_mfma_kernel<C, true, 4, true>), grid, dim3(C::THREADS), 0, st, x, sx, M, (int)K,
+                       (int)N, w, sw, sw_ld, ks, out, partial);
   } else {
     using C = DenseMfmaCfg<2, 2, false>;
     const dim3 grid((unsigned)(N / C::BN), (unsigned)((M + C::BM - 1) / C::BM), (unsigned)ks);
-    hipLaunchKernelGGL((dense_fp8_mfma_kernel<C, false, 2>), grid, dim3(C::THREADS), 0, st, x, sx, M, (int)K,
-                       (int)N, w, sw, sw_ld, ks, out, partial);
+    // Two blocks per CU either way; a grid that fits one round takes the
+    // deeper ring.
+    if ((int64_t)grid.x * grid.y * grid.z <= 512)
+      hipLaunchKernelGGL((dense_fp8_mfma_kernel<C, false, 3>), grid, dim3(C::THREADS), 0, st, x, sx, M, (int)K,
+                         (int)N, w, sw, sw_ld, ks, out, partial);
+    else
+      hipLaunchKernelGGL((dense_fp8_mfma_kernel<C, false, 2>), grid, dim3(C::THREADS), 0, st, x, sx, M, (int)K,
+                         (int)N, w, sw, sw_ld, ks, out, partial);
   }
   int rc = launch_status("dense_fp8");
   if (rc != DWM_OK || ks == 1) return rc;
