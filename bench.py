@@ -13,7 +13,9 @@ lhs once, output once) divided by the average step time measured with HIP
 events on the stream the kernels run on.  `extra` reports the other workloads
 (decode down-projection with dispatch / combine, prefill) the same way, and
 `cpu_baseline` times the numpy oracle of the same math on a bounded sample of
-experts on this host.
+experts on this host (and one expert on one thread), and reports the max abs
+and relative Frobenius error of one expert's GPU output rows against the
+oracle's float64 product.
 
 The default warmup (200 launches, ~30 ms of decode work) brings the GPU to
 its sustained clock before the timed region: the power manager ramps the
@@ -354,35 +356,66 @@ def profiled_traffic(name="gmm_fp4_decode_gate_up.md"):
     return int(m.group(1)) if m else None
 
 
-def cpu_baseline(wl, budget_s):
+def cpu_baseline(wl, budget_s, gpu_check=None):
     """numpy oracle of the same math (exact dequant to f32, per-expert f32
-    matmul, bf16 round) over as many non-empty experts as fit the budget."""
+    matmul, bf16 round) over as many non-empty experts as fit the budget, on
+    the BLAS threads numpy has, plus one expert on one thread.
+
+    gpu_check = (expert, rows as f32) of the GPU output: the oracle also
+    checks those rows against its float64 product (max abs error and
+    relative Frobenius error, the bf16 output rounding included)."""
     import numpy as np
-    from oracle import fp4, gmm
+    from oracle import fp4
     from oracle.numerics import bf16_to_f32, round_bf16
     try:
-        from threadpoolctl import threadpool_info
+        from threadpoolctl import threadpool_info, threadpool_limits
         threads = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
     except Exception:
+        threadpool_limits = None
         threads = 1
     starts = np.concatenate([[0], np.cumsum(wl.group_sizes)])
     lhs = bf16_to_f32(wl.lhs_bits)
+
+    def expert_bytes(sz):
+        return wl.K * wl.N // 2 + (wl.K // 32) * wl.N + sz * wl.K * 2 + sz * wl.N * 2
+
+    def dequant(e):
+        codes = fp4.e2m1_to_codes(fp4.unpack_nibbles(wl.rhs_e2m1[e]))
+        return fp4.dequant_fp4_block(codes, fp4.e8m0_decode(wl.scale_codes[e]))
+
     done, bts, t0 = 0, 0, time.perf_counter()
     for e in range(wl.E):
         sz = int(wl.group_sizes[e])
         if sz == 0:
             continue
-        codes = fp4.e2m1_to_codes(fp4.unpack_nibbles(wl.rhs_e2m1[e]))
-        w = fp4.dequant_fp4_block(codes, fp4.e8m0_decode(wl.scale_codes[e]))
-        round_bf16(lhs[starts[e]:starts[e + 1]] @ w)
+        round_bf16(lhs[starts[e]:starts[e + 1]] @ dequant(e))
         done += 1
-        bts += wl.K * wl.N // 2 + (wl.K // 32) * wl.N + sz * wl.K * 2 + sz * wl.N * 2
+        bts += expert_bytes(sz)
         if time.perf_counter() - t0 > budget_s:
             break
     dt = time.perf_counter() - t0
-    return {"value": round(bts / dt / 1e9, 4), "unit": "GB/s", "cores": int(threads), "kind": "port",
-            "sample": f"{done} of {int((wl.group_sizes > 0).sum())} non-empty experts of {wl.name} "
-                      f"(numpy oracle: dequant single-threaded, f32 matmul on {threads} BLAS threads), {dt:.1f} s"}
+    res = {"value": round(bts / dt / 1e9, 4), "unit": "GB/s", "cores": int(threads), "kind": "port",
+           "sample": f"{done} of {int((wl.group_sizes > 0).sum())} non-empty experts of {wl.name} "
+                     f"(numpy oracle: dequant single-threaded, f32 matmul on {threads} BLAS threads), {dt:.1f} s"}
+    e1 = int(np.flatnonzero(wl.group_sizes > 0)[0])
+    if threadpool_limits is not None:
+        with threadpool_limits(limits=1):
+            t1 = time.perf_counter()
+            round_bf16(lhs[starts[e1]:starts[e1 + 1]] @ dequant(e1))
+            dt1 = time.perf_counter() - t1
+        res["value_1thread"] = round(expert_bytes(int(wl.group_sizes[e1])) / dt1 / 1e9, 4)
+    if gpu_check is not None:
+        e, y = gpu_check
+        ref = lhs[starts[e]:starts[e + 1]].astype(np.float64) @ dequant(e).astype(np.float64)
+        err = y.astype(np.float64) - ref
+        # one bf16 ulp of the reference value (8 significant bits)
+        ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(ref), 2.0 ** -126))) - 7)
+        res["parity"] = {"expert": int(e), "rows": int(ref.shape[0]),
+                         "max_abs_err": float(np.abs(err).max()),
+                         "rel_frobenius": float(np.linalg.norm(err) / np.linalg.norm(ref)),
+                         "max_err_bf16_ulps": float((np.abs(err) / ulp).max()),
+                         "vs": "float64 oracle product of the same bf16 lhs and exact fp4 weights"}
+    return res
 
 
 def main():
@@ -402,6 +435,7 @@ def main():
               "the experts; runs on more than one GPU are not part of this build.", file=sys.stderr)
         sys.exit(2)
 
+    import numpy as np
     import torch
     dev = torch.device("cuda:0")
     if args.calib_copy:
@@ -416,6 +450,9 @@ def main():
     log("bench: decode_gate_up gmm")
     wl, b, ms = bench_gmm("decode_gate_up", dev, args.steps, args.warmup)
     main_res = gmm_result(wl, ms)
+    e_chk = int(np.flatnonzero(wl.group_sizes > 0)[0])
+    r0 = int(wl.group_sizes[:e_chk].sum())
+    gpu_check = (e_chk, b.out[0][r0:r0 + int(wl.group_sizes[e_chk])].float().cpu().numpy())
     extra = {}
     if args.extra == "all":
         for name in ("decode_down", "prefill"):
@@ -441,7 +478,7 @@ def main():
     cpu = None
     if args.cpu_budget > 0:
         log("bench: cpu baseline")
-        cpu = cpu_baseline(wl, args.cpu_budget)
+        cpu = cpu_baseline(wl, args.cpu_budget, gpu_check)
     line = {
         "metric": METRIC,
         "value": main_res["GB_s"],
