@@ -21,7 +21,10 @@ Parity pins (what checks each function against something other than itself):
 * ``gmm.gmm``: brute force on tiny shapes, float64 closed form, per-group
   independence, empty groups.  The reference's f32 accumulation order inside
   gmm_v2 is not vendored, so bit-exact gmm OUTPUT parity is unpinned by
-  construction; outputs are checked against a stated bf16 error bound.
+  construction; outputs are checked against a stated bf16 error bound and the
+  reference's acceptance rule (``gmm.acceptance_policy``).  The ``seq32``
+  accumulation it compares with: a pure-Python per-element loop on tiny
+  shapes (the same order, bit for bit) and the sequential-summation bound.
 * ``moe.dispatch``: brute force and the identities of
   moe_fast_dispatch.py:14-20.
 * ``moe.combine``: an explicit per-element Python loop (tiny shapes).

@@ -46,6 +46,8 @@ def gmm(lhs, codes, scale, group_sizes, group_offset: int = 0, out_dtype: str = 
     ``w`` may pass a precomputed ``dequant_rhs`` result.
     With out_dtype 'bfloat16' the result is rounded to bf16 (RNE); with
     'float32' to f32; with 'float64' it is returned unrounded.
+    accumulate: 'f64' (exact up to float64 rounding), 'f32' (BLAS) or
+    'seq32' (f32 running sum over k in order).
     """
     lhs = np.asarray(lhs, np.float32)
     m, k = lhs.shape
@@ -65,6 +67,15 @@ def gmm(lhs, codes, scale, group_sizes, group_offset: int = 0, out_dtype: str = 
         a = lhs[r0:r1]
         if accumulate == "f64":
             y = a.astype(np.float64) @ w[g - group_offset].astype(np.float64)
+        elif accumulate == "seq32":
+            # f32 running sum over k in order of the exact bf16 x bf16
+            # products (each fits f32): the plain sequential-accumulation
+            # kernel, the baseline of the acceptance policy below.
+            wg = w[g - group_offset].astype(np.float32)
+            acc = np.zeros((r1 - r0, n), np.float32)
+            for kk in range(k):
+                acc += a[:, kk:kk + 1] * wg[kk:kk + 1, :]
+            y = acc.astype(np.float64)
         else:
             y = (a @ w[g - group_offset].astype(np.float32)).astype(np.float64)
         out[r0:r1] = y
@@ -114,3 +125,19 @@ def error_stats(y, y64, mask=None):
     den = np.linalg.norm(y64)
     return {"max_abs": float(np.abs(d).max()) if d.size else 0.0,
             "rel_fro": float(np.linalg.norm(d) / den) if den > 0 else float(np.linalg.norm(d))}
+
+
+def acceptance_policy(y, y_base, y64, mask=None):
+    """The reference's kernel-acceptance rule
+    (results/dsv4-dense-gemm-kernel-1/NOTES.md:26-27): against the float64
+    result, a new kernel's RMS error is at most 1.10x, and its max abs error
+    at most 2x, those of the current kernel (here ``y_base``, the
+    sequential-f32 accumulation).  Returns (passed, stats)."""
+    y, y_base, y64 = (np.asarray(v, np.float64) for v in (y, y_base, y64))
+    if mask is not None:
+        y, y_base, y64 = y[mask], y_base[mask], y64[mask]
+    d, db = y - y64, y_base - y64
+    rms, rms_b = float(np.sqrt(np.mean(d * d))), float(np.sqrt(np.mean(db * db)))
+    mx, mx_b = float(np.abs(d).max()), float(np.abs(db).max())
+    st = {"rms": rms, "rms_base": rms_b, "max_abs": mx, "max_abs_base": mx_b}
+    return rms <= 1.10 * rms_b and mx <= 2.0 * mx_b, st

@@ -51,6 +51,32 @@ def test_w8a8_small_shapes(dev, M, K, N):
     print(M, K, N, _check(out, y64, odf.abs_product_w8a8(wl.xq, wl.sx, wl.wq, wl.sw), K))
 
 
+@pytest.mark.parametrize("M", [16, 300])
+def test_dense_reference_acceptance_policy(dev, M):
+    """The reference's kernel-acceptance rule
+    (results/dsv4-dense-gemm-kernel-1/NOTES.md:26-27), with the oracle's f32
+    per-K-block accumulation (the reference kernel's structure) as the
+    current kernel: RMS error <= 1.10x and max abs error <= 2x of its error
+    against float64, for both variants."""
+    from dw_tpu_amd.dense_fp8 import matmul, matmul_w8a8
+    from dw_tpu_amd.workloads import make_dense_workload
+    K, N = 2048, 512
+    wl = make_dense_workload(M, K, N, seed=79)
+    x = bf16_tensor(wl.x_bits, dev)
+    out16 = matmul(x, torch.from_numpy(wl.wq).to(dev).view(torch.float8_e4m3fn), torch.from_numpy(wl.s_w8a16).to(dev))
+    out8 = matmul_w8a8(torch.from_numpy(wl.xq).to(dev), torch.from_numpy(wl.sx).to(dev),
+                       torch.from_numpy(wl.wq).to(dev), torch.from_numpy(wl.sw).to(dev))
+    xf = bf16_to_f32(wl.x_bits)
+    cases = [(out16, odf.matmul_w8a16(xf, wl.wq, wl.s_w8a16, out_dtype="float64"),
+              odf.matmul_w8a16(xf, wl.wq, wl.s_w8a16, accumulate="f32")),
+             (out8, odf.matmul_w8a8(wl.xq, wl.sx, wl.wq, wl.sw, out_dtype="float64"),
+              odf.matmul_w8a8(wl.xq, wl.sx, wl.wq, wl.sw, accumulate="f32"))]
+    for out, y64, ybase in cases:
+        ok, st = ogmm.acceptance_policy(bf16_to_f32(bf16_bits(out)), ybase, y64)
+        print(M, st, flush=True)
+        assert ok, st
+
+
 @pytest.mark.parametrize("M", [1, 16, 128, 1024, 4096])
 def test_dense_fp8_workload_sampled(dev, M):
     """The dense_fp8 workload (K=7168, N=4096) at every M: sampled rows x

@@ -164,6 +164,26 @@ def test_gmm_cpu_plumbing_workload_full(dev):
     assert stats["rel_fro"] < 4e-3
 
 
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+def test_gmm_reference_acceptance_policy(dev, rng, out_dtype):
+    """The reference's kernel-acceptance rule
+    (results/dsv4-dense-gemm-kernel-1/NOTES.md:26-27) with the sequential-f32
+    kernel as the current one: RMS error <= 1.10x and max abs error <= 2x of
+    its error against float64."""
+    K, N = 2048, 256
+    lhs_bits, rhs, sc, gs = _random_case(rng, [300, 0, 64, 257], K, N)
+    out = _run(dev, lhs_bits, rhs, sc, gs, out_dtype=out_dtype)
+    lhs_f32 = bf16_to_f32(lhs_bits)
+    w = gmm.dequant_rhs(fp4.e2m1_to_codes(_nibbles_at(rhs, np.arange(N))), fp4.e8m0_decode(sc))
+    kind = "float32" if out_dtype == torch.float32 else "bfloat16"
+    y64, _ = gmm.gmm(lhs_f32, None, None, gs, out_dtype="float64", w=w)
+    ys, _ = gmm.gmm(lhs_f32, None, None, gs, out_dtype=kind, accumulate="seq32", w=w)
+    y = out.float().cpu().numpy()
+    ok, st = gmm.acceptance_policy(y, ys, y64)
+    print(kind, st, flush=True)
+    assert ok, st
+
+
 def _sample_rows(gs, rng):
     starts = np.concatenate([[0], np.cumsum(gs)])
     rows = []

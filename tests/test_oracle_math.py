@@ -85,6 +85,47 @@ def test_gmm_error_bound_accepts_f32_and_rejects_planted_mistakes(rng):
     assert np.any(np.abs(y_neg - y64) > bound)
 
 
+def test_gmm_seq32_is_the_sequential_f32_sum(rng):
+    lhs, nib, codes, exps, scale, gs = _tiny_gmm_case(rng, [3, 0, 2], K=64, N=4)
+    w = gmm.dequant_rhs(codes, scale)
+    ys, _ = gmm.gmm(lhs, None, None, gs, out_dtype="float64", accumulate="seq32", w=w)
+    # per element, an explicit f32 running sum in k order (bit for bit)
+    starts = gmm.group_starts(gs)
+    for g, sz in enumerate(gs):
+        for r in range(starts[g], starts[g] + sz):
+            for n in range(4):
+                acc = np.float32(0)
+                for k in range(64):
+                    acc = np.float32(acc + np.float32(lhs[r, k] * w[g, k, n]))
+                assert ys[r, n] == float(acc)
+    # and within the sequential-summation bound (K - 1) u sum|a w| of float64
+    K = 1024
+    lhs, nib, codes, exps, scale, gs = _tiny_gmm_case(rng, [17, 9], K=K, N=16)
+    w = gmm.dequant_rhs(codes, scale)
+    ys, _ = gmm.gmm(lhs, None, None, gs, out_dtype="float64", accumulate="seq32", w=w)
+    y64, _ = gmm.gmm(lhs, None, None, gs, out_dtype="float64", w=w)
+    ap = gmm.abs_product(lhs, w, gs)
+    assert np.all(np.abs(ys - y64) <= (K - 1) * 2.0 ** -24 * ap)
+    assert np.any(ys != y64)  # it does round
+
+
+def test_gmm_acceptance_policy(rng):
+    K = 512
+    lhs, nib, codes, exps, scale, gs = _tiny_gmm_case(rng, [40, 24], K=K, N=32)
+    w = gmm.dequant_rhs(codes, scale)
+    y64, _ = gmm.gmm(lhs, None, None, gs, out_dtype="float64", w=w)
+    ys, _ = gmm.gmm(lhs, None, None, gs, out_dtype="float32", accumulate="seq32", w=w)
+    yb, _ = gmm.gmm(lhs, None, None, gs, out_dtype="float32", accumulate="f32", w=w)
+    ok, st = gmm.acceptance_policy(ys, ys, y64)
+    assert ok and st["rms"] == st["rms_base"]
+    ok, _ = gmm.acceptance_policy(yb, ys, y64)  # a blocked BLAS sum is at least as accurate
+    assert ok
+    # planted: a 4-ulp-scale perturbation of every element fails it
+    bad = (ys.astype(np.float64) + 4 * np.abs(ys - y64).max()).astype(np.float32)
+    ok, _ = gmm.acceptance_policy(bad, ys, y64)
+    assert not ok
+
+
 # ---------------------------------------------------------------------- dispatch
 
 @pytest.mark.parametrize("T,topk,E", [(1, 1, 1), (5, 2, 3), (64, 2, 8), (37, 8, 32), (300, 6, 256)])
