@@ -6,30 +6,80 @@
 // One wavefront per token: lane l holds experts l, l + 64, ... (coalesced
 // loads of the logits row), the scores are computed in registers, and the
 // top-k runs as k wave-wide arg-max rounds (larger key first, then the lower
-// expert id, as lax.top_k orders ties).  Lane j keeps result j, so the
-// outputs are written by lanes 0 .. k-1 without a staging buffer.
+// expert id, as lax.top_k orders ties) over one 64-bit word per candidate.
+// Lane j keeps result j, so the outputs are written by lanes 0 .. k-1
+// without a staging buffer.
 #include "common.h"
 
 namespace dwm {
 
+// Wave-wide reductions without LDS traffic: four DPP steps combine the 16
+// lanes of each row (pairs, quads, the two halves of 8, the two halves of
+// 16, every lane ending with its row's result), then the four rows are read
+// as scalars and combined in row order.  The result is wave-uniform.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140;
+
+__device__ __forceinline__ uint32_t lane_u32(uint32_t v, int lane) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, lane);
+}
+
+template <class F>
+__device__ __forceinline__ float wave_reduce_f32(float v, F op) {
+  v = op(v, __builtin_bit_cast(float, dpp_u32<kDppXor1>(__builtin_bit_cast(uint32_t, v))));
+  v = op(v, __builtin_bit_cast(float, dpp_u32<kDppXor2>(__builtin_bit_cast(uint32_t, v))));
+  v = op(v, __builtin_bit_cast(float, dpp_u32<kDppHalfMirror>(__builtin_bit_cast(uint32_t, v))));
+  v = op(v, __builtin_bit_cast(float, dpp_u32<kDppMirror>(__builtin_bit_cast(uint32_t, v))));
+  const uint32_t b = __builtin_bit_cast(uint32_t, v);
+  float r = __builtin_bit_cast(float, lane_u32(b, 0));
+  r = op(r, __builtin_bit_cast(float, lane_u32(b, 16)));
+  r = op(r, __builtin_bit_cast(float, lane_u32(b, 32)));
+  return op(r, __builtin_bit_cast(float, lane_u32(b, 48)));
+}
+
 __device__ __forceinline__ float wave_max_f32(float v) {
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) v = fmaxf(v, __shfl_xor(v, d, 64));
-  return v;
+  return wave_reduce_f32(v, [](float a, float b) { return fmaxf(a, b); });
 }
 
 __device__ __forceinline__ float wave_sum_f32(float v) {
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
-  return v;
+  return wave_reduce_f32(v, [](float a, float b) { return a + b; });
 }
 
-// Key order of the selection: a before b when a's key is larger, or equal
-// with a lower expert id.  Taken experts carry taken = true and lose to all.
-__device__ __forceinline__ bool key_before(float ka, int ea, bool ta, float kb, int eb, bool tb) {
-  if (ta != tb) return tb;
-  if (ka != kb) return ka > kb;
-  return ea < eb;
+// Selection order: a larger key first, then the lower expert id (lax.top_k's
+// tie order).  Each candidate is one 64-bit word that orders that way as an
+// unsigned integer: the key's bits made monotone (flip all bits of a
+// negative, set the sign bit of a non-negative) above the inverted expert id.
+// A taken expert is 0 and loses to every candidate; a NaN key ranks below
+// every number (ties by id).  -0 is folded into +0 first, as the float
+// comparison treats them as equal.
+__device__ __forceinline__ uint64_t select_word(float key, int e) {
+  uint32_t b = __builtin_bit_cast(uint32_t, key == 0.0f ? 0.0f : key);
+  b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  if (key != key) b = 0u;
+  return ((uint64_t)b << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)e);
+}
+
+template <int CTRL>
+__device__ __forceinline__ uint64_t max_dpp_u64(uint64_t v) {
+  const uint64_t o = ((uint64_t)dpp_u32<CTRL>((uint32_t)(v >> 32)) << 32) | dpp_u32<CTRL>((uint32_t)v);
+  return o > v ? o : v;
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+  v = max_dpp_u64<kDppXor1>(v);
+  v = max_dpp_u64<kDppXor2>(v);
+  v = max_dpp_u64<kDppHalfMirror>(v);
+  v = max_dpp_u64<kDppMirror>(v);
+  uint64_t r = 0;
+#pragma unroll
+  for (int row = 0; row < 4; ++row) {
+    const uint64_t o = ((uint64_t)lane_u32((uint32_t)(v >> 32), 16 * row) << 32) | lane_u32((uint32_t)v, 16 * row);
+    r = o > r ? o : r;
+  }
+  return r;
 }
 
 template <int VPL>
@@ -43,8 +93,7 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const void *__restrict_
   const int lane = threadIdx.x & 63;
   const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
-  float p[VPL], key[VPL];
-  bool taken[VPL];
+  float p[VPL];
   float x[VPL];
   float m = -__builtin_inff();
 #pragma unroll
@@ -76,11 +125,11 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const void *__restrict_
 #pragma unroll
     for (int i = 0; i < VPL; ++i) p[i] = sqrtf(fmaxf(x[i], 0.0f) + log1pf(expf(-fabsf(x[i]))));
   }
+  uint64_t cand[VPL];  // 0 once taken (or for lanes past E)
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
     const int e = lane + 64 * i;
-    key[i] = (bias != nullptr && e < E) ? p[i] + bias[e] : p[i];
-    taken[i] = e >= E;
+    cand[i] = e < E ? select_word(bias != nullptr ? p[i] + bias[e] : p[i], e) : 0ull;
   }
   float my_w = 0.0f;  // result j = lane
   int my_id = 0;
@@ -91,7 +140,7 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const void *__restrict_
       float v = 0.0f;
 #pragma unroll
       for (int i = 0; i < VPL; ++i) v = slot == i ? p[i] : v;
-      v = __shfl(v, id & 63, 64);
+      v = __builtin_bit_cast(float, lane_u32(__builtin_bit_cast(uint32_t, v), id & 63));
       if (lane == j) {
         my_w = v;
         my_id = id;
@@ -99,44 +148,31 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const void *__restrict_
     }
   } else {
     for (int j = 0; j < topk; ++j) {
-      float bk = 0.0f, bw = 0.0f;
-      int be = 0x7FFFFFFF;
-      bool bt = true;
+      uint64_t best = cand[0];
 #pragma unroll
-      for (int i = 0; i < VPL; ++i) {
-        const int e = lane + 64 * i;
-        if (key_before(key[i], e, taken[i], bk, be, bt)) {
-          bk = key[i];
-          be = e;
-          bt = taken[i];
-          bw = p[i];
-        }
+      for (int i = 1; i < VPL; ++i) best = cand[i] > best ? cand[i] : best;
+      best = wave_max_u64(best);
+      // Every lane now holds the winner; its owner (lane id % 64) marks it
+      // taken and hands over its unbiased weight.
+      const int id = (int)(0xFFFFFFFFu - (uint32_t)best);
+      const int slot = id >> 6;
+      float v = 0.0f;
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) v = slot == i ? p[i] : v;
+      v = __builtin_bit_cast(float, lane_u32(__builtin_bit_cast(uint32_t, v), id & 63));
+      if (lane == (id & 63)) {
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) cand[i] = slot == i ? 0ull : cand[i];
       }
-#pragma unroll
-      for (int d = 32; d >= 1; d >>= 1) {
-        const float ok = __shfl_xor(bk, d, 64), ow = __shfl_xor(bw, d, 64);
-        const int oe = __shfl_xor(be, d, 64);
-        const bool ot = __shfl_xor((int)bt, d, 64) != 0;
-        if (key_before(ok, oe, ot, bk, be, bt)) {
-          bk = ok;
-          be = oe;
-          bt = ot;
-          bw = ow;
-        }
-      }
-      // Every lane now holds the winner; its owner marks it taken.
-#pragma unroll
-      for (int i = 0; i < VPL; ++i)
-        if (lane + 64 * i == be) taken[i] = true;
       if (lane == j) {
-        my_w = bw;
-        my_id = be;
+        my_w = v;
+        my_id = id;
       }
     }
   }
   if (renorm) {
     float tot = 0.0f;  // the sum over k in order
-    for (int j = 0; j < topk; ++j) tot += __shfl(my_w, j, 64);
+    for (int j = 0; j < topk; ++j) tot += __builtin_bit_cast(float, lane_u32(__builtin_bit_cast(uint32_t, my_w), j));
     my_w = my_w / tot;
   }
   if (num_valid != nullptr && t >= (int64_t)num_valid[0]) {
