@@ -162,7 +162,7 @@ def bench_dispatch_combine(dev, steps, warmup):
 
     res = {}
     ms = time_steps(lambda i: run(lib.dwm_moe_dispatch, disp_args), steps, warmup)
-    res["dispatch"] = {"ms": round(ms, 5), "ids": n, "experts": wl.E, "kernels": 3}
+    res["dispatch"] = {"ms": round(ms, 5), "ids": n, "experts": wl.E, "kernels": 1 if n <= 8192 else 3}
     ms = time_steps(lambda i: run(lib.dwm_row_gather, gather_args), steps, warmup)
     gb = 2 * n * wl.K * 2 + n * 4
     res["row_gather"] = {"ms": round(ms, 5), "GB_s": round(gb / (ms * 1e-3) / 1e9, 1), "rows": n, "H": wl.K,

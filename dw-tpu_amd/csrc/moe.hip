@@ -3,7 +3,8 @@
 // Dispatch replaces jnp.argsort(topk_ids.flatten()) + argsort // topk +
 // one_hot(...).sum(0) (patches/tpu-inference-ext/0405-moe-fast-dispatch.patch:70-98,
 // kernels/tpu_inference/layers/common/moe_fast_dispatch.py:41-44) with a
-// three-launch counting sort that is bit-exact to a stable argsort:
+// counting sort that is bit-exact to a stable argsort, in three launches
+// (one block for batches of up to 8192 ids, dispatch_fused_kernel):
 //   1. per 1024-id chunk, an LDS histogram -> counts[chunk][expert]
 //   2. one block: group sizes, exclusive offsets, per-(chunk, expert) bases
 //   3. per chunk, in id order (256 ids per step, wave by wave): each lane's
@@ -131,6 +132,78 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_scatter_kernel(
   }
 }
 
+// Small batches (n <= kFusedMax ids): one block of 1024 threads runs all
+// three steps -- the LDS histogram, the scan (wave 0) and the stable scatter
+// in 1024-id steps -- in one launch, with no workspace round trip.
+constexpr int kFusedThreads = 1024, kFusedMax = 8192;
+
+__global__ __launch_bounds__(kFusedThreads) void dispatch_fused_kernel(const int32_t *ids, int64_t n, int topk,
+                                                                       int E, int32_t *perm, int32_t *tok_sorted,
+                                                                       int32_t *revert, int32_t *group_sizes,
+                                                                       int32_t *group_offsets, int32_t *flags) {
+  constexpr int W = kFusedThreads / 64;
+  __shared__ int s_run[kMaxExperts + 1];     // counts, then the next position of each key
+  __shared__ int s_wcnt[W][kMaxExperts + 1];  // this step's count of each key per wave
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int e = tid; e <= E; e += kFusedThreads) {
+    s_run[e] = 0;
+#pragma unroll
+    for (int w = 0; w < W; ++w) s_wcnt[w][e] = 0;
+  }
+  __syncthreads();
+  bool bad = false;
+  for (int64_t j = tid; j < n; j += kFusedThreads) atomicAdd(&s_run[dispatch_key(ids[j], E, &bad)], 1);
+  if (bad && flags) atomicOr(flags, 1);
+  __syncthreads();
+  if (wave == 0) {
+    int carry = 0;
+    for (int b = 0; b <= E; b += 64) {
+      const int e = b + lane;
+      const int v = e <= E ? s_run[e] : 0;
+      const int inc = wave_inclusive_scan(v);
+      if (e <= E) {
+        if (e < E) group_sizes[e] = v;
+        if (group_offsets) group_offsets[e] = carry + inc - v;  // entry E = number of valid ids
+        s_run[e] = carry + inc - v;
+      }
+      carry += __shfl(inc, 63, 64);
+    }
+  }
+  int nbits = 0;
+  while ((1 << nbits) <= E) ++nbits;  // keys 0..E
+  __syncthreads();
+  for (int64_t base = 0; base < n; base += kFusedThreads) {
+    const int64_t j = base + tid;
+    const bool active = j < n;
+    bool b2 = false;
+    const int key = active ? dispatch_key(ids[j], E, &b2) : 0;
+    uint64_t peers = __ballot(active);
+    for (int b = 0; b < nbits; ++b) {
+      const bool bit = (key >> b) & 1;
+      const uint64_t m = __ballot(bit);
+      peers &= bit ? m : ~m;
+    }
+    const int rank = __popcll(peers & ((1ull << lane) - 1ull));
+    const int cnt = __popcll(peers);
+    const bool leader = active && rank == 0;
+    if (leader) s_wcnt[wave][key] = cnt;
+    __syncthreads();
+    if (active) {
+      int pos = s_run[key] + rank;
+      for (int w = 0; w < wave; ++w) pos += s_wcnt[w][key];
+      perm[pos] = (int32_t)j;
+      tok_sorted[pos] = (int32_t)(j / topk);
+      revert[j] = pos;
+    }
+    __syncthreads();
+    if (leader) {
+      atomicAdd(&s_run[key], cnt);
+      s_wcnt[wave][key] = 0;
+    }
+    __syncthreads();
+  }
+}
+
 // JAX gather index semantics: wrap a negative index once, then clamp.
 __device__ __forceinline__ int64_t gather_index(int64_t i, int64_t n) {
   if (i < 0) i += n;
@@ -157,47 +230,79 @@ __device__ __forceinline__ float load_f32(const void *p, int dtype, int64_t i) {
                           : bf16_bits_to_f32(((const uint16_t *)p)[i]);
 }
 
-// One block per token; each thread owns 8 consecutive columns per step.
+// Block (column chunk, token): each thread owns 8 consecutive columns of one
+// token.  The token's top-k rows are read in groups of KG, all loads of a
+// group issued before the group is summed (in k order, so the result is the
+// same left-to-right f32 sum), and the 8 outputs leave in 16-byte stores.
+constexpr int kCombineKG = 8;
+
+template <int XF32>
+__device__ __forceinline__ void load8_f32(const void *x, int64_t o, bool full, int64_t H, int64_t c, float *v) {
+  if (full && !XF32) {
+    const u32x4_t q = *(const u32x4_t *)((const uint16_t *)x + o);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = __builtin_bit_cast(float, q[i] << 16);
+      v[2 * i + 1] = __builtin_bit_cast(float, q[i] & 0xFFFF0000u);
+    }
+  } else if (full) {
+    const f32x4_t q0 = *(const f32x4_t *)((const float *)x + o);
+    const f32x4_t q1 = *(const f32x4_t *)((const float *)x + o + 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[i] = q0[i];
+      v[4 + i] = q1[i];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = c + i < H ? load_f32(x, XF32 ? DWM_F32 : DWM_BF16, o + i) : 0.0f;
+  }
+}
+
 template <int XF32, int OF32>
 __global__ __launch_bounds__(256) void combine_kernel(const void *x, int64_t x_rows, int64_t H,
                                                       const int32_t *idx, const void *w, int w_dtype,
                                                       int64_t T, int topk, void *out, int vec) {
-  for (int64_t t = blockIdx.x; t < T; t += gridDim.x) {
-    for (int64_t c = (int64_t)threadIdx.x * 8; c < H; c += (int64_t)blockDim.x * 8) {
-      float acc[8];
+  const int64_t c = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
+  if (c >= H) return;
+  const bool full = vec && c + 8 <= H;
+  for (int64_t t = blockIdx.y; t < T; t += gridDim.y) {
+    float acc[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
-      const bool full = vec && c + 8 <= H;
-      for (int k = 0; k < topk; ++k) {
-        const int64_t r = gather_index(idx[t * topk + k], x_rows);
-        const float wk = load_f32(w, w_dtype, t * topk + k);
-        float v[8];
-        if (full && !XF32) {
-          const u32x4_t q = *(const u32x4_t *)((const uint16_t *)x + r * H + c);
+    for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+    for (int k0 = 0; k0 < topk; k0 += kCombineKG) {
+      float v[kCombineKG][8], wk[kCombineKG];
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            v[2 * i] = __builtin_bit_cast(float, q[i] << 16);
-            v[2 * i + 1] = __builtin_bit_cast(float, q[i] & 0xFFFF0000u);
-          }
-        } else if (full) {
-          const f32x4_t q0 = *(const f32x4_t *)((const float *)x + r * H + c);
-          const f32x4_t q1 = *(const f32x4_t *)((const float *)x + r * H + c + 4);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            v[i] = q0[i];
-            v[4 + i] = q1[i];
-          }
-        } else {
-#pragma unroll
-          for (int i = 0; i < 8; ++i)
-            v[i] = c + i < H ? load_f32(x, XF32 ? DWM_F32 : DWM_BF16, r * H + c + i) : 0.0f;
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const float p = v[i] * wk;  // separately rounded product
-          acc[i] = acc[i] + p;        // then sum, k ascending from +0.0
+      for (int g = 0; g < kCombineKG; ++g) {
+        if (k0 + g < topk) {
+          const int64_t r = gather_index(idx[t * topk + k0 + g], x_rows);
+          wk[g] = load_f32(w, w_dtype, t * topk + k0 + g);
+          load8_f32<XF32>(x, r * H + c, full, H, c, v[g]);
         }
       }
+#pragma unroll
+      for (int g = 0; g < kCombineKG; ++g) {
+        if (k0 + g < topk) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const float p = v[g][i] * wk[g];  // separately rounded product
+            acc[i] = acc[i] + p;              // then sum, k ascending from +0.0
+          }
+        }
+      }
+    }
+    if (full) {
+      if (OF32) {
+        *(f32x4_t *)((float *)out + t * H + c) = f32x4_t{acc[0], acc[1], acc[2], acc[3]};
+        *(f32x4_t *)((float *)out + t * H + c + 4) = f32x4_t{acc[4], acc[5], acc[6], acc[7]};
+      } else {
+        u32x4_t q;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          q[i] = (uint32_t)f32_to_bf16_bits(acc[2 * i]) | ((uint32_t)f32_to_bf16_bits(acc[2 * i + 1]) << 16);
+        *(u32x4_t *)((uint16_t *)out + t * H + c) = q;
+      }
+    } else {
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         if (c + i >= H) break;
@@ -243,6 +348,11 @@ extern "C" int dwm_moe_dispatch(const int32_t *topk_ids, int64_t T, int topk, in
     return launch_status("moe_dispatch");
   }
   DWM_CHECK_ARG(topk_ids && perm && tok_sorted && revert, "moe_dispatch: null pointer");
+  if (n <= kFusedMax) {
+    hipLaunchKernelGGL(dispatch_fused_kernel, dim3(1), dim3(kFusedThreads), 0, st, topk_ids, n, topk,
+                       num_experts, perm, tok_sorted, revert, group_sizes, group_offsets, flags);
+    return launch_status("moe_dispatch");
+  }
   hipLaunchKernelGGL(dispatch_count_kernel, dim3((unsigned)nchunks), dim3(kDispThreads), 0, st,
                      topk_ids, n, num_experts, counts, flags);
   hipLaunchKernelGGL(dispatch_scan_kernel, dim3(1), dim3(1024), 0, st, counts, (int)nchunks,
@@ -286,22 +396,22 @@ extern "C" int dwm_moe_combine(const void *x, int x_dtype, int64_t x_rows, int64
   DWM_CHECK_ARG(x_rows > 0, "moe_combine: empty x with tokens to combine");
   DWM_CHECK_ARG(x && idx && w && out, "moe_combine: null pointer");
   const int xf32 = x_dtype == DWM_F32;
-  // 16-byte row loads need 8-column multiples and an aligned base.
-  const int vec = (H % 8 == 0) && ((uintptr_t)x % 16 == 0);
-  const unsigned grid = (unsigned)(T < 65536 ? T : 65536);
+  // 16-byte row loads and stores need 8-column multiples and aligned bases.
+  const int vec = (H % 8 == 0) && ((uintptr_t)x % 16 == 0) && ((uintptr_t)out % 16 == 0);
+  const dim3 grid((unsigned)((H + 2047) / 2048), (unsigned)(T < 65535 ? T : 65535));
   hipStream_t st = as_stream(stream);
   const int of32 = out_dtype == DWM_F32;
   if (!xf32 && !of32)
-    hipLaunchKernelGGL((combine_kernel<0, 0>), dim3(grid), dim3(256), 0, st, x, x_rows, H, idx, w,
+    hipLaunchKernelGGL((combine_kernel<0, 0>), grid, dim3(256), 0, st, x, x_rows, H, idx, w,
                        w_dtype, T, topk, out, vec);
   else if (!xf32 && of32)
-    hipLaunchKernelGGL((combine_kernel<0, 1>), dim3(grid), dim3(256), 0, st, x, x_rows, H, idx, w,
+    hipLaunchKernelGGL((combine_kernel<0, 1>), grid, dim3(256), 0, st, x, x_rows, H, idx, w,
                        w_dtype, T, topk, out, vec);
   else if (xf32 && !of32)
-    hipLaunchKernelGGL((combine_kernel<1, 0>), dim3(grid), dim3(256), 0, st, x, x_rows, H, idx, w,
+    hipLaunchKernelGGL((combine_kernel<1, 0>), grid, dim3(256), 0, st, x, x_rows, H, idx, w,
                        w_dtype, T, topk, out, vec);
   else
-    hipLaunchKernelGGL((combine_kernel<1, 1>), dim3(grid), dim3(256), 0, st, x, x_rows, H, idx, w,
+    hipLaunchKernelGGL((combine_kernel<1, 1>), grid, dim3(256), 0, st, x, x_rows, H, idx, w,
                        w_dtype, T, topk, out, vec);
   return launch_status("moe_combine");
 }
