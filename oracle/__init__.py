@@ -5,7 +5,7 @@ tokamax gmm_v2 FP4 patch, MoE fast dispatch / combine, e8m0 scales and the
 dense FP8 GEMM).  Every function cites the reference file:line it follows.
 
 Who may use it: only ``tests/``, ``__graft_entry__.smoke()`` and the
-``cpu_baseline`` leg of ``bench.py``, and only as the checker.  The product
+``cpu_baseline`` leg of ``bench.py``, and only to check results against.  The product
 package (``dw_tpu_amd``) never imports it; the product path fails loudly when
 its HIP library is missing instead of falling back to anything here.
 

@@ -20,7 +20,7 @@ def dev():
     if not torch.cuda.is_available():
         pytest.skip("no HIP device")
     from dw_tpu_amd import _lib
-    _lib.load()  # a missing library on a GPU box is a failure, not a skip
+    _lib.load()  # a missing library where a GPU is present is a failure, not a skip
     return torch.device("cuda:0")
 
 
