@@ -17,8 +17,11 @@ def _dispatch(dev, ids, E, check=False):
     return [t.cpu().numpy() for t in d]
 
 
+# Batches of up to 8192 ids take the one-block kernel, larger ones the
+# three-launch path: both sides of that boundary are covered.
 @pytest.mark.parametrize("T,topk,E", [(1, 1, 1), (3, 2, 8), (64, 2, 8), (256, 8, 32), (512, 8, 32),
-                                      (1000, 6, 256), (8192, 8, 32), (130, 8, 1024), (4096, 1, 3)])
+                                      (1000, 6, 256), (8192, 8, 32), (130, 8, 1024), (4096, 1, 3),
+                                      (1024, 8, 1024), (8192, 1, 5), (8193, 1, 7), (2731, 3, 64)])
 def test_dispatch_bit_exact(dev, rng, T, topk, E):
     ids = rng.integers(0, E, (T, topk)).astype(np.int32)
     got = _dispatch(dev, ids, E)
@@ -54,6 +57,14 @@ def test_dispatch_skewed_and_invalid_ids(dev, rng):
     assert gs.sum() == valid.sum() and off[-1] == valid.sum()
     assert set(perm[off[-1]:]) == set(np.nonzero(~valid)[0])  # invalid ids last
     assert np.array_equal(perm[rev], np.arange(bad.size))
+    # the same on the three-launch path (more than 8192 ids): invalid ids sort
+    # as one extra key E after every valid one, stably
+    big = rng.integers(0, 8, (3000, 3)).astype(np.int32)
+    big[5, 2], big[2999, 0], big[1500, 1] = 8, -3, 100
+    got = _dispatch(dev, big, 8)
+    perm, tok, rev, gs, off = moe.dispatch(np.where((big >= 0) & (big < 8), big, 8), 9)
+    for g, w in zip(got, (perm, tok, rev, gs[:8], off[:9])):
+        assert np.array_equal(g, w)
 
 
 @pytest.mark.parametrize("T,H,dtype", [(64, 1024, torch.bfloat16), (513, 7168, torch.bfloat16),
