@@ -182,7 +182,7 @@ def bench_moe_block(dev, steps, warmup):
     [2048, 7168] + combine to [256, 7168].  Two weight copies are rotated."""
     import numpy as np
     import torch
-    from dw_tpu_amd import fp4_weight_to_codes, moe_block
+    from dw_tpu_amd import MoeBlockGraph, fp4_weight_to_codes, moe_block
     from dw_tpu_amd.workloads import make_gmm_workload
     wl = make_gmm_workload("decode_gate_up", with_data=False)
     H, I, E = wl.K, wl.N // 2, wl.E
@@ -201,6 +201,9 @@ def bench_moe_block(dev, steps, warmup):
     ids = torch.from_numpy(wl.topk_ids).to(dev)
     wts = torch.from_numpy(wl.topk_weights).to(dev)
     ms = time_steps(lambda i: moe_block(hidden, ids, wts, w13s[i % copies], w2s[i % copies], E), steps, warmup)
+    # the same block captured once per weight copy (MoeBlockGraph) and replayed
+    graphs = [MoeBlockGraph(hidden, ids, wts, w13s[c], w2s[c], E) for c in range(copies)]
+    ms_graph = time_steps(lambda i: graphs[i % copies](), steps, warmup)
     nonempty = int((wl.group_sizes > 0).sum())
     n = wl.M
     wbytes = nonempty * (H * 2 * I // 2 + H // 32 * 2 * I + I * H // 2 + I // 32 * H)
@@ -210,7 +213,11 @@ def bench_moe_block(dev, steps, warmup):
     return {"moe_block_decode": {"ms": round(ms, 5), "GB_s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
                                  "TFLOP_s": round(flops / (ms * 1e-3) / 1e12, 1), "bytes": wbytes + act_bytes,
                                  "flops": flops, "T": wl.T, "topk": wl.topk, "H": H, "I": I, "E": E,
-                                 "nonempty_groups": nonempty}}
+                                 "nonempty_groups": nonempty},
+            "moe_block_decode_graph": {"ms": round(ms_graph, 5),
+                                       "GB_s": round((wbytes + act_bytes) / (ms_graph * 1e-3) / 1e9, 1),
+                                       "TFLOP_s": round(flops / (ms_graph * 1e-3) / 1e12, 1),
+                                       "note": "the same block replayed from a captured HIP graph"}}
 
 
 def bench_routing(dev, steps, warmup):

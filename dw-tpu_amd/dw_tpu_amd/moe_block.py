@@ -56,3 +56,50 @@ def moe_block(hidden: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.
     if return_intermediates:
         return MoeBlockOutputs(out, d, x, h, y)
     return out
+
+
+class MoeBlockGraph:
+    """``moe_block`` captured once into a HIP graph and replayed.
+
+    The reference runs the block as one compiled XLA program; here the
+    dispatch, gather, two gmm and combine launches are recorded once (shapes,
+    weights and options fixed at construction) and each call replays them
+    with one graph launch, so no host work sits between the kernels.  Inputs
+    are copied into the graph's own buffers before a replay; the returned
+    tensor is the graph's output buffer, overwritten by the next replay.
+    Every kernel of the block reads its sizes from device memory (group sizes
+    from the dispatch), and none of them allocates or synchronises, so the
+    captured work is the eager work.
+    """
+
+    def __init__(self, hidden: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.Tensor, w13: Fp4Weight,
+                 w2: Fp4Weight, num_experts: int, group_offset=None, f32_reduce: bool = False):
+        self.hidden = hidden.clone()
+        self.topk_ids = topk_ids.to(torch.int32).clone()
+        self.topk_weights = topk_weights.clone()
+        if isinstance(group_offset, torch.Tensor):
+            group_offset = group_offset.clone()
+        args = (w13, w2, num_experts)
+        kw = dict(group_offset=group_offset, f32_reduce=f32_reduce)
+        self._keep = (w13, w2, group_offset)
+        # One eager run on a side stream first (as torch's capture recipe asks).
+        side = torch.cuda.Stream(device=hidden.device)
+        side.wait_stream(torch.cuda.current_stream(hidden.device))
+        with torch.cuda.stream(side):
+            moe_block(self.hidden, self.topk_ids, self.topk_weights, *args, **kw)
+        torch.cuda.current_stream(hidden.device).wait_stream(side)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.out = moe_block(self.hidden, self.topk_ids, self.topk_weights, *args, **kw)
+
+    def __call__(self, hidden: torch.Tensor = None, topk_ids: torch.Tensor = None,
+                 topk_weights: torch.Tensor = None) -> torch.Tensor:
+        """Copies the given inputs (same shapes and dtypes as at construction)
+        into the graph's buffers and replays it on the current stream."""
+        for src, dst in ((hidden, self.hidden), (topk_ids, self.topk_ids), (topk_weights, self.topk_weights)):
+            if src is not None:
+                if src.shape != dst.shape:
+                    raise ValueError(f"MoeBlockGraph: shape {tuple(src.shape)} != captured {tuple(dst.shape)}")
+                dst.copy_(src)
+        self.graph.replay()
+        return self.out

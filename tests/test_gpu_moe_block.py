@@ -168,3 +168,27 @@ def test_moe_block_decode_size_sampled(dev, rng):
     # combine: exact on the kernel's gmm2 output (all columns)
     want = moe.combine(bf16_to_f32(bf16_bits(r.y)), rev, wts, topk, out_dtype="bfloat16")
     assert np.array_equal(bf16_bits(r.out), np_bf16_bits(want))
+
+
+def test_moe_block_graph_replays_match_eager(dev, rng):
+    """The captured block, replayed several times with new inputs and eager
+    work (and synchronisations) in between, gives the eager block's bits
+    every time."""
+    from dw_tpu_amd import MoeBlockGraph, fp4_weight_to_codes, moe_block
+    T, E, topk, H, I = 64, 8, 2, 256, 128
+    ids, wts, hidden_bits, (r13, s13), (r2, s2) = _block_case(rng, T, E, topk, H, I, empty=(3,))
+    w13 = fp4_weight_to_codes(torch.from_numpy(r13).to(dev), torch.from_numpy(s13).to(dev), gate_up=True)
+    w2 = fp4_weight_to_codes(torch.from_numpy(r2).to(dev), torch.from_numpy(s2).to(dev))
+    g = MoeBlockGraph(bf16_tensor(hidden_bits, dev), torch.from_numpy(ids).to(dev), torch.from_numpy(wts).to(dev),
+                      w13, w2, E)
+    for rep in range(4):
+        ids_r, wts_r, hb_r, _, _ = _block_case(rng, T, E, topk, H, I, empty=(rep % E,))
+        hidden, tid, tw = bf16_tensor(hb_r, dev), torch.from_numpy(ids_r).to(dev), torch.from_numpy(wts_r).to(dev)
+        want = moe_block(hidden, tid, tw, w13, w2, E)
+        torch.cuda.synchronize()
+        got = g(hidden, tid, tw).clone()
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16)), rep
+        # eager work between replays
+        moe_block(hidden, tid, tw, w13, w2, E)
+        torch.cuda.synchronize()
