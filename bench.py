@@ -176,10 +176,11 @@ def bench_dispatch_combine(dev, steps, warmup):
 
 def bench_moe_block(dev, steps, warmup):
     """The decode-size expert block through ``moe_block``: 256 tokens x top-8
-    over 32 experts (decode_gate_up routing), dispatch + row gather of hidden
-    [256, 7168] + gmm1 [2048, 7168] x [7168, 2x2048] with the fused
-    silu_and_mul_with_clamp (out [2048, 2048]) + gmm2 [2048, 2048] x
-    [2048, 7168] + combine to [256, 7168].  Two weight copies are rotated."""
+    over 32 experts (decode_gate_up routing), dispatch + gmm1 over the
+    routed rows of hidden [256, 7168] (gathered inside the gmm) x
+    [7168, 2x2048] with the fused silu_and_mul_with_clamp (out [2048, 2048])
+    + gmm2 [2048, 2048] x [2048, 7168] + combine to [256, 7168].  Two weight
+    copies are rotated."""
     import numpy as np
     import torch
     from dw_tpu_amd import MoeBlockGraph, fp4_weight_to_codes, moe_block
@@ -207,7 +208,10 @@ def bench_moe_block(dev, steps, warmup):
     nonempty = int((wl.group_sizes > 0).sum())
     n = wl.M
     wbytes = nonempty * (H * 2 * I // 2 + H // 32 * 2 * I + I * H // 2 + I // 32 * H)
-    act_bytes = wl.T * H * 2 + n * H * 2 * 2 + n * I * 2 * 2 + n * H * 2 + wl.T * H * 2
+    # hidden read once, h written by gmm1 and read by gmm2, y written by gmm2
+    # and read by the combine, out written (gmm1 reads the routed rows of
+    # hidden itself: no gathered copy)
+    act_bytes = wl.T * H * 2 + 2 * n * I * 2 + 2 * n * H * 2 + wl.T * H * 2
     flops = 2 * n * H * 2 * I + 2 * n * I * H
     gbs = (wbytes + act_bytes) / (ms * 1e-3) / 1e9
     return {"moe_block_decode": {"ms": round(ms, 5), "GB_s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),

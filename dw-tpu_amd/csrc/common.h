@@ -98,6 +98,14 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, ui
 // s_waitcnt immediate (gfx9 encoding): vmcnt <= vm, lgkmcnt == 0, expcnt untouched.
 __host__ __device__ constexpr int waitcnt_vm_lgkm0(int vm) { return (vm & 15) | ((vm >> 4) << 14) | (7 << 4); }
 
+// JAX gather index semantics: wrap a negative index once, then clamp.
+__device__ __forceinline__ int64_t gather_index(int64_t i, int64_t n) {
+  if (i < 0) i += n;
+  if (i < 0) i = 0;
+  if (i >= n) i = n - 1;
+  return i;
+}
+
 // A compile-time int carried by value (generic lambdas specialise on it).
 template <int V>
 struct IntC {

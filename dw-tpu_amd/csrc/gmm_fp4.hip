@@ -127,7 +127,8 @@ struct WsCfg {
 // Producer wave pw: NA of its A_LOADS lhs row groups hold rows of the tile;
 // the others are zero in every stage and never loaded.
 template <class C, int NA>
-__device__ __forceinline__ void ws_producer(const uint16_t *__restrict__ lhs, int64_t row0, int rows, int K, int T,
+__device__ __forceinline__ void ws_producer(const uint16_t *__restrict__ lhs, const int32_t *__restrict__ row_idx,
+                                            int64_t lhs_rows, int64_t row0, int rows, int K, int T,
                                             int KB, const uint8_t *__restrict__ wexp,
                                             const uint8_t *__restrict__ sexp, int g0, int G, uint8_t *s_lds,
                                             int pw) {
@@ -144,14 +145,17 @@ __device__ __forceinline__ void ws_producer(const uint16_t *__restrict__ lhs, in
       *(u32x4_t *)(s_lds + st * C::STAGE + C::A + (pw + NP * i) * 1024 + lane * 16) = u32x4_t{0u, 0u, 0u, 0u};
   // lhs load i: rows 8 (pw + NP i) .. + 7 of the tile; lane l fills physical
   // chunk l % 8 of row + l / 8 with logical chunk (l % 8) ^ swizzle(row).
-  // Rows past the tile repeat its last row.
-  const uint8_t *const abase = (const uint8_t *)(lhs + row0 * K);
+  // Rows past the tile repeat its last row.  With row_idx (the fused row
+  // gather) tile row r is lhs row row_idx[row0 + r], under JAX gather index
+  // semantics; the indices are read once, before any direct-to-LDS load.
+  const uint8_t *const abase = (const uint8_t *)(row_idx ? lhs : lhs + row0 * K);
   uint32_t aoff[NA > 0 ? NA : 1];
 #pragma unroll
   for (int i = 0; i < NA; ++i) {
     const int r = 8 * (pw + NP * i) + (lane >> 3);
     const int rs = r < rows ? r : rows - 1;
-    aoff[i] = (uint32_t)rs * (uint32_t)K * 2u + ((((lane & 7) ^ lhs_swizzle(r))) << 4);
+    const int64_t src = row_idx ? gather_index(row_idx[row0 + rs], lhs_rows) : rs;
+    aoff[i] = (uint32_t)(src * K * 2) + ((((lane & 7) ^ lhs_swizzle(r))) << 4);
   }
   const uint8_t *wsrc[C::G_LOADS];
   const uint8_t *ssrc[C::G_LOADS];
@@ -424,7 +428,8 @@ __device__ __forceinline__ bool find_tile(const int32_t *__restrict__ group_size
 
 template <class C, int MB, bool ACT>
 __global__ __launch_bounds__(C::THREADS) void gmm_fp4_ws_kernel(
-    const uint16_t *__restrict__ lhs, int64_t M, int K, const uint8_t *__restrict__ wpk,
+    const uint16_t *__restrict__ lhs, const int32_t *__restrict__ row_idx, int64_t lhs_rows, int64_t M, int K,
+    const uint8_t *__restrict__ wpk,
     const uint8_t *__restrict__ spk, const int32_t *__restrict__ group_sizes, int num_groups,
     const int32_t *__restrict__ group_offset, int64_t e_local, int N, void *__restrict__ out,
     int out_f32) {
@@ -453,10 +458,10 @@ __global__ __launch_bounds__(C::THREADS) void gmm_fp4_ws_kernel(
     const uint8_t *const sexp = spk + e * G * KB * 256;
     // Row groups pw + NP i with 8 (pw + NP i) < rows are loaded.
     const int na = min(C::A_LOADS, (rows + 8 * C::NPROD - 1 - 8 * pw) / (8 * C::NPROD));
-    if (na >= C::A_LOADS) ws_producer<C, C::A_LOADS>(lhs, row0, rows, K, T, KB, wexp, sexp, g0, G, s_lds, pw);
-    else if (na == 2) ws_producer<C, (C::A_LOADS > 2 ? 2 : C::A_LOADS)>(lhs, row0, rows, K, T, KB, wexp, sexp, g0, G, s_lds, pw);
-    else if (na == 1) ws_producer<C, (C::A_LOADS > 1 ? 1 : C::A_LOADS)>(lhs, row0, rows, K, T, KB, wexp, sexp, g0, G, s_lds, pw);
-    else ws_producer<C, 0>(lhs, row0, rows, K, T, KB, wexp, sexp, g0, G, s_lds, pw);
+    if (na >= C::A_LOADS) ws_producer<C, C::A_LOADS>(lhs, row_idx, lhs_rows, row0, rows, K, T, KB, wexp, sexp, g0, G, s_lds, pw);
+    else if (na == 2) ws_producer<C, (C::A_LOADS > 2 ? 2 : C::A_LOADS)>(lhs, row_idx, lhs_rows, row0, rows, K, T, KB, wexp, sexp, g0, G, s_lds, pw);
+    else if (na == 1) ws_producer<C, (C::A_LOADS > 1 ? 1 : C::A_LOADS)>(lhs, row_idx, lhs_rows, row0, rows, K, T, KB, wexp, sexp, g0, G, s_lds, pw);
+    else ws_producer<C, 0>(lhs, row_idx, lhs_rows, row0, rows, K, T, KB, wexp, sexp, g0, G, s_lds, pw);
     return;
   }
   const int act_mb = (rows + 31) >> 5;
@@ -503,7 +508,8 @@ __global__ __launch_bounds__(256) void gmm_zero_rows_kernel(const int32_t *group
 }
 
 template <int MB, int CW, int JW, int NP, int NS, bool ACT = false>
-static int launch_gmm_ws(const uint16_t *lhs, int64_t M, int64_t K, const uint8_t *w, const uint8_t *s,
+static int launch_gmm_ws(const uint16_t *lhs, const int32_t *row_idx, int64_t lhs_rows, int64_t M, int64_t K,
+                         const uint8_t *w, const uint8_t *s,
                          const int32_t *gs, int ng, const int32_t *go, int64_t e_local, int64_t N, void *out,
                          int out_f32, hipStream_t st) {
   using C = WsCfg<MB, CW, JW, NP, NS>;
@@ -514,7 +520,8 @@ static int launch_gmm_ws(const uint16_t *lhs, int64_t M, int64_t K, const uint8_
   const int64_t grid = ((max_tiles + 7) / 8 + MB) * 8;
   DWM_UNSUPPORTED_IF(grid > (1ll << 31) - 1, "gmm_fp4: too many tiles (%lld)", (long long)grid);
   DWM_UNSUPPORTED_IF(K > (1 << 24), "gmm_fp4: K <= 2^24 required");
-  hipLaunchKernelGGL((gmm_fp4_ws_kernel<C, MB, ACT>), dim3((unsigned)grid), dim3(C::THREADS), 0, st, lhs, M, (int)K, w,
+  hipLaunchKernelGGL((gmm_fp4_ws_kernel<C, MB, ACT>), dim3((unsigned)grid), dim3(C::THREADS), 0, st, lhs, row_idx,
+                     lhs_rows, M, (int)K, w,
                      s, gs, ng, go, e_local, (int)N, out, out_f32);
   return launch_status("gmm_fp4");
 }
@@ -523,7 +530,8 @@ static int launch_gmm_ws(const uint16_t *lhs, int64_t M, int64_t K, const uint8_
 
 using namespace dwm;
 
-extern "C" int dwm_gmm_fp4(const uint16_t *lhs, int64_t M, int64_t K, const uint8_t *weight,
+static int gmm_fp4_impl(const uint16_t *lhs, const int32_t *row_idx, int64_t lhs_rows, int64_t M, int64_t K,
+                        const uint8_t *weight,
                            const uint8_t *scale, const int32_t *group_sizes, int num_groups,
                            const int32_t *group_offset, int64_t E_local, int64_t N, void *out,
                            int out_dtype, int zero_init, int fuse_act, void *stream) {
@@ -540,6 +548,9 @@ extern "C" int dwm_gmm_fp4(const uint16_t *lhs, int64_t M, int64_t K, const uint
   DWM_UNSUPPORTED_IF(K > (1 << 30) || N > (1 << 30), "gmm_fp4: K, N must be < 2^30");
   if (M == 0) return DWM_OK;
   DWM_CHECK_ARG(lhs && out && (num_groups == 0 || group_sizes), "gmm_fp4: null pointer");
+  // The fused gather addresses lhs rows with 32-bit byte offsets.
+  DWM_UNSUPPORTED_IF(row_idx && lhs_rows * K * 2 >= (1ll << 32), "gmm_fp4_gather: lhs of %lld rows is too large",
+                     (long long)lhs_rows);
   DWM_CHECK_ARG(E_local == 0 || (weight && scale), "gmm_fp4: null weight pointer");
   DWM_CHECK_ARG((uintptr_t)lhs % 16 == 0 && (uintptr_t)weight % 16 == 0 && (uintptr_t)out % 16 == 0 &&
                     (uintptr_t)scale % 4 == 0,
@@ -560,8 +571,29 @@ extern "C" int dwm_gmm_fp4(const uint16_t *lhs, int64_t M, int64_t K, const uint
   // Measured fastest on the decode and prefill workloads among the tile,
   // wave-split and pipeline-depth variants tried.
   if (fuse_act == DWM_ACT_SILU_MUL_CLAMP)
-    return launch_gmm_ws<3, 8, 2, 4, 4, true>(lhs, M, K, weight, scale, group_sizes, num_groups, group_offset,
+    return launch_gmm_ws<3, 8, 2, 4, 4, true>(lhs, row_idx, lhs_rows, M, K, weight, scale, group_sizes, num_groups, group_offset,
                                               E_local, N, out, out_f32, st);
-  return launch_gmm_ws<3, 8, 2, 4, 4>(lhs, M, K, weight, scale, group_sizes, num_groups, group_offset, E_local, N,
+  return launch_gmm_ws<3, 8, 2, 4, 4>(lhs, row_idx, lhs_rows, M, K, weight, scale, group_sizes, num_groups, group_offset, E_local, N,
                                       out, out_f32, st);
+}
+
+extern "C" int dwm_gmm_fp4(const uint16_t *lhs, int64_t M, int64_t K, const uint8_t *weight,
+                           const uint8_t *scale, const int32_t *group_sizes, int num_groups,
+                           const int32_t *group_offset, int64_t E_local, int64_t N, void *out,
+                           int out_dtype, int zero_init, int fuse_act, void *stream) {
+  return gmm_fp4_impl(lhs, nullptr, M, M, K, weight, scale, group_sizes, num_groups, group_offset, E_local, N, out,
+                      out_dtype, zero_init, fuse_act, stream);
+}
+
+extern "C" int dwm_gmm_fp4_gather(const uint16_t *lhs, int64_t lhs_rows, const int32_t *row_idx, int64_t M,
+                                  int64_t K, const uint8_t *weight, const uint8_t *scale,
+                                  const int32_t *group_sizes, int num_groups, const int32_t *group_offset,
+                                  int64_t E_local, int64_t N, void *out, int out_dtype, int zero_init, int fuse_act,
+                                  void *stream) {
+  clear_error();
+  DWM_CHECK_ARG(lhs_rows >= 0 && M >= 0, "gmm_fp4_gather: bad sizes lhs_rows=%lld M=%lld", (long long)lhs_rows,
+                (long long)M);
+  DWM_CHECK_ARG(M == 0 || (row_idx && lhs_rows > 0), "gmm_fp4_gather: null row_idx or empty lhs with rows to gather");
+  return gmm_fp4_impl(lhs, row_idx, lhs_rows, M, K, weight, scale, group_sizes, num_groups, group_offset, E_local, N,
+                      out, out_dtype, zero_init, fuse_act, stream);
 }

@@ -204,13 +204,6 @@ __global__ __launch_bounds__(kFusedThreads) void dispatch_fused_kernel(const int
   }
 }
 
-// JAX gather index semantics: wrap a negative index once, then clamp.
-__device__ __forceinline__ int64_t gather_index(int64_t i, int64_t n) {
-  if (i < 0) i += n;
-  if (i < 0) i = 0;
-  if (i >= n) i = n - 1;
-  return i;
-}
 
 template <typename V>
 __global__ __launch_bounds__(256) void row_gather_kernel(const char *src, int64_t src_rows,

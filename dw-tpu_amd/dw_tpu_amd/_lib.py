@@ -34,6 +34,7 @@ SIGNATURES = {
     "dwm_gmm_fp4_prepack": [_p, _i32, _p, _i32, _i64, _i64, _i64, _p, _p, _p, _p],
     "dwm_gmm_fp4_prepack_gate_up": [_p, _i32, _p, _i32, _i64, _i64, _i64, _p, _p, _p, _p],
     "dwm_gmm_fp4": [_p, _i64, _i64, _p, _p, _p, _i32, _p, _i64, _i64, _p, _i32, _i32, _i32, _p],
+    "dwm_gmm_fp4_gather": [_p, _i64, _p, _i64, _i64, _p, _p, _p, _i32, _p, _i64, _i64, _p, _i32, _i32, _i32, _p],
     "dwm_moe_dispatch_workspace_size": [_i64, _i32, _p],
     "dwm_moe_dispatch": [_p, _i64, _i32, _i32, _p, _p, _p, _p, _p, _p, _p, _p],
     "dwm_row_gather": [_p, _i64, _i64, _p, _i64, _p, _p],

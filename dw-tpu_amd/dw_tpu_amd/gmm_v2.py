@@ -173,7 +173,8 @@ def gmm_v2(lhs: torch.Tensor,
            zero_initialize: bool = True,
            fuse_act=None,
            transpose_rhs: bool = False,
-           rhs_fp4_codes: bool = False) -> torch.Tensor:
+           rhs_fp4_codes: bool = False,
+           lhs_row_indices: torch.Tensor = None) -> torch.Tensor:
     """Ragged grouped matmul: out[rows of g] = lhs[rows of g] @ dequant(rhs[g - group_offset]).
 
     lhs: [M, K] bf16, rows sorted by group.  rhs: ``Fp4Weight`` (prepacked)
@@ -187,6 +188,12 @@ def gmm_v2(lhs: torch.Tensor,
     prepacked so per call) and the result is [M, N/2] =
     silu(min(gate, 10)) * clip(up, -10, 10) of the f32 accumulators, rounded
     once.  Tiling / VMEM arguments of the TPU kernel are accepted and ignored.
+
+    ``lhs_row_indices`` (an addition; int32 [M] device tensor): row r of the
+    grouped operand is ``lhs[lhs_row_indices[r]]`` (JAX gather index
+    semantics), read by the kernel directly -- the dispatch row gather fused
+    into the matmul.  ``lhs`` is then the source [rows, K] and the result has
+    M = len(lhs_row_indices) rows.
     """
     if rhs_bias is not None:
         raise NotImplementedError("gmm_v2: rhs_bias is not supported by the fp4 kernel")
@@ -226,10 +233,22 @@ def gmm_v2(lhs: torch.Tensor,
         go = torch.tensor([group_offset], dtype=torch.int32, device=dev)
     else:
         go = group_offset.reshape(-1)[:1].to(device=dev, dtype=torch.int32).contiguous()
-    m = lhs.shape[0]
+    act = _lib.ACT_SILU_MUL_CLAMP if fused else _lib.ACT_NONE
+    if lhs_row_indices is None:
+        m = lhs.shape[0]
+        out = torch.empty((m, w.n // 2 if fused else w.n), dtype=out_dtype, device=dev)
+        _lib.call("dwm_gmm_fp4", _lib.ptr(lhs), m, w.k, _lib.ptr(w.weight), _lib.ptr(w.scale), _lib.ptr(gs),
+                  gs.numel(), _lib.ptr(go), w.num_experts, w.n, _lib.ptr(out), _lib.dtype_code(out_dtype),
+                  1 if zero_initialize else 0, act, _lib.stream_handle(dev))
+        return out
+    idx = lhs_row_indices
+    if idx.dtype != torch.int32 or idx.dim() != 1:
+        raise ValueError("gmm_v2: lhs_row_indices must be a 1-D int32 tensor")
+    _lib.require_cuda(idx)
+    idx = idx.contiguous()
+    m = idx.numel()
     out = torch.empty((m, w.n // 2 if fused else w.n), dtype=out_dtype, device=dev)
-    _lib.call("dwm_gmm_fp4", _lib.ptr(lhs), m, w.k, _lib.ptr(w.weight), _lib.ptr(w.scale), _lib.ptr(gs),
-              gs.numel(), _lib.ptr(go), w.num_experts, w.n, _lib.ptr(out), _lib.dtype_code(out_dtype),
-              1 if zero_initialize else 0, _lib.ACT_SILU_MUL_CLAMP if fused else _lib.ACT_NONE,
-              _lib.stream_handle(dev))
+    _lib.call("dwm_gmm_fp4_gather", _lib.ptr(lhs), lhs.shape[0], _lib.ptr(idx), m, w.k, _lib.ptr(w.weight),
+              _lib.ptr(w.scale), _lib.ptr(gs), gs.numel(), _lib.ptr(go), w.num_experts, w.n, _lib.ptr(out),
+              _lib.dtype_code(out_dtype), 1 if zero_initialize else 0, act, _lib.stream_handle(dev))
     return out

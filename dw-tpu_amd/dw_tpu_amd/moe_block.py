@@ -1,4 +1,5 @@
-"""The routed-expert block around the FP4 gmm: dispatch, row gather, gmm1
+"""The routed-expert block around the FP4 gmm: dispatch, gmm1 (reading the
+dispatched rows of ``hidden`` itself: the row gather fused into its loads)
 with the fused ``silu_and_mul_with_clamp`` activation, gmm2 and the
 routing-weighted combine -- the local (one-GPU) body of the reference's
 ``moe_gmm_local`` (patches/tpu-inference-ext/0103-...:77-78 for gmm1 with the
@@ -16,7 +17,6 @@ from dataclasses import dataclass
 
 import torch
 
-from .fused_moe_gmm import gmm_wrapper
 from .gmm_v2 import Fp4Weight, gmm_v2
 from .moe_fast_combine import fast_combine
 from .moe_fast_dispatch import moe_dispatch, row_gather
@@ -27,7 +27,7 @@ class MoeBlockOutputs:
     """The block's result and its intermediates (device tensors)."""
     out: torch.Tensor       # [T, H] combined
     dispatch: object        # moe_fast_dispatch.Dispatch
-    x: torch.Tensor         # [T * topk, H] gathered rows (expert order)
+    x: torch.Tensor         # [T * topk, H] the rows gmm1 reads (expert order), gathered for inspection
     h: torch.Tensor         # [T * topk, I] activation of gmm1 (bf16)
     y: torch.Tensor         # [T * topk, H] gmm2 output (bf16 or f32)
 
@@ -45,8 +45,10 @@ def moe_block(hidden: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.
         raise ValueError(f"moe_block: shapes do not chain: hidden {tuple(hidden.shape)}, w13 {w13.shape}, w2 {w2.shape}")
     topk = topk_ids.shape[1]
     d = moe_dispatch(topk_ids, num_experts)
-    x = row_gather(hidden, d.token_indices_sorted)
-    h = gmm_wrapper(x, w13, None, None, d.group_sizes, group_offset, fuse_act="silu_and_mul_with_clamp")
+    # gmm1 reads hidden[token_indices_sorted] itself (the row gather fused
+    # into its loads), the same rows the separate gather would write.
+    h = gmm_v2(hidden, w13, d.group_sizes, group_offset=group_offset, zero_initialize=False,
+               fuse_act="silu_and_mul_with_clamp", lhs_row_indices=d.token_indices_sorted)
     # With a group_offset (an expert-parallel shard) rows of other shards'
     # experts are zeroed before the combine, as the reference does
     # (patches/tpu-inference-ext/0103-...:94-97: 0 * NaN would poison it).
@@ -54,7 +56,7 @@ def moe_block(hidden: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.
                preferred_element_type=torch.float32 if f32_reduce else None)
     out = fast_combine(y, d.topk_argsort_revert_indices, topk_weights, topk, out_dtype=hidden.dtype)
     if return_intermediates:
-        return MoeBlockOutputs(out, d, x, h, y)
+        return MoeBlockOutputs(out, d, row_gather(hidden, d.token_indices_sorted), h, y)
     return out
 
 

@@ -154,6 +154,20 @@ int dwm_gmm_fp4(const uint16_t *lhs, int64_t M, int64_t K, const uint8_t *weight
                 const int32_t *group_offset, int64_t E_local, int64_t N, void *out,
                 int out_dtype, int zero_init, int fuse_act, void *stream);
 
+/* dwm_gmm_fp4 with the dispatch row gather fused into its lhs loads: row r
+ * of the grouped operand is lhs[row_idx[r]] (lhs: [lhs_rows, K] bf16, the
+ * tokens' hidden states; row_idx: device int32[M], JAX gather index
+ * semantics as dwm_row_gather), so
+ *   dwm_gmm_fp4_gather(hidden, T, tok_sorted, M, ...)
+ * gives the bits of dwm_row_gather(hidden -> x) then dwm_gmm_fp4(x, M, ...)
+ * without writing x.  Replaces the gather + gmm1 pair of moe_gmm_local
+ * (moe_fast_dispatch.py:188-194 feeding patches/tpu-inference-ext/0103-...:77-78).
+ * Requires lhs_rows * K * 2 < 2^32; otherwise as dwm_gmm_fp4. */
+int dwm_gmm_fp4_gather(const uint16_t *lhs, int64_t lhs_rows, const int32_t *row_idx, int64_t M, int64_t K,
+                       const uint8_t *weight, const uint8_t *scale, const int32_t *group_sizes, int num_groups,
+                       const int32_t *group_offset, int64_t E_local, int64_t N, void *out, int out_dtype,
+                       int zero_init, int fuse_act, void *stream);
+
 /* ---------------------------------------------------------------------- */
 /* MoE dispatch and combine.                                               */
 /* ---------------------------------------------------------------------- */

@@ -215,3 +215,31 @@ def test_gmm_full_size_workloads_sampled(dev, rng, name):
     print(name, stats, flush=True)
     # size-independent checks on the full output: finite, every row written
     assert torch.isfinite(out.float()).all()
+
+
+@pytest.mark.parametrize("fused_act", [False, True])
+@pytest.mark.parametrize("group_offset", [None, 1])
+def test_gmm_fused_row_gather_equals_gather_then_gmm(dev, rng, fused_act, group_offset):
+    """gmm_v2(hidden, ..., lhs_row_indices=idx) gives the bits of
+    gmm_v2(hidden[idx], ...): the row gather fused into the gmm's loads,
+    including JAX gather index semantics (a negative index wraps once, an
+    out-of-range one clamps)."""
+    from dw_tpu_amd import fp4_weight_to_codes, gmm_v2, row_gather
+    T, K, N = 150, 256, 192
+    sizes = [37, 0, 120, 64, 9]
+    M = sum(sizes)
+    hidden = bf16_tensor(bf16_bits_np(rng.standard_normal((T, K)).astype(np.float32)), dev)
+    idx_np = rng.integers(0, T, M).astype(np.int32)
+    idx_np[3], idx_np[50], idx_np[M - 1] = -1, T + 7, -T - 5
+    idx = torch.from_numpy(idx_np).to(dev)
+    rhs = torch.from_numpy(rng.integers(0, 256, (len(sizes), K, N // 2), dtype=np.uint8)).to(dev)
+    sc = torch.from_numpy(rng.integers(123, 130, (len(sizes), K // 32, 1, N), dtype=np.uint8)).to(dev)
+    w = fp4_weight_to_codes(rhs[1:] if group_offset else rhs, sc[1:] if group_offset else sc, gate_up=fused_act)
+    gs = torch.from_numpy(np.array(sizes, np.int32)).to(dev)
+    act = "silu_and_mul_with_clamp" if fused_act else None
+    x = row_gather(hidden, idx)
+    want = gmm_v2(x, w, gs, group_offset=group_offset, fuse_act=act)
+    got = gmm_v2(hidden, w, gs, group_offset=group_offset, fuse_act=act, lhs_row_indices=idx)
+    torch.cuda.synchronize()
+    assert got.shape == want.shape
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
