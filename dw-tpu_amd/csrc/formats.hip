@@ -20,6 +20,9 @@
 // tile through LDS so both the reads and the writes are whole 16-byte runs.
 #include "common.h"
 
+typedef __attribute__((ext_vector_type(2))) float f32x2_t;
+typedef __attribute__((ext_vector_type(2))) short i16x2_t;
+
 namespace dwm {
 
 // e2m1 nibble -> f32 (sign bit 3; magnitudes 0, .5, 1, 1.5, 2, 3, 4, 6).
@@ -29,44 +32,12 @@ __device__ __forceinline__ float e2m1_f32(uint32_t c) {
   return __builtin_bit_cast(float, mag | ((c & 8u) << 28));
 }
 
-// e4m3fn code -> f32 (bias 7, subnormals m * 2^-9, 0x7F / 0xFF NaN).
-__device__ __forceinline__ float e4m3_f32(uint32_t c) {
-  const uint32_t e = (c >> 3) & 15u, m = c & 7u;
-  const uint32_t sign = (c & 0x80u) << 24;
-  if (e == 15 && m == 7) return __builtin_bit_cast(float, 0x7FC00000u | sign);
-  if (e == 0) return __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, (float)m * 0.001953125f) | sign);
-  return __builtin_bit_cast(float, sign | ((e + 120u) << 23) | (m << 20));
-}
-
 // f32 -> e2m1 nibble, round to nearest even, saturating at 6; the sign of q
 // (also of -0 and of values rounding to 0) sets bit 3.
 __device__ __forceinline__ uint32_t rne_e2m1(float q) {
   const float a = fabsf(q);
   const uint32_t c = (a > 0.25f) + (a >= 0.75f) + (a > 1.25f) + (a >= 1.75f) + (a > 2.5f) + (a >= 3.5f) + (a > 5.0f);
   return c | ((__builtin_bit_cast(uint32_t, q) >> 28) & 8u);
-}
-
-// f32 -> e4m3fn code, round to nearest even; magnitudes >= 464 (and NaN) give
-// 0x7F (NaN) with the sign of q.
-__device__ __forceinline__ uint32_t rne_e4m3(float q) {
-  const uint32_t bits = __builtin_bit_cast(uint32_t, q);
-  const uint32_t sign = (bits >> 24) & 0x80u;
-  const float a = fabsf(q);
-  if (!(a < 464.0f)) return sign | 0x7Fu;
-  if (a < 0.015625f) {  // below 2^-6: multiples of 2^-9 (the step to 2^-6 lands on code 8)
-    return sign | (uint32_t)rintf(a * 512.0f);
-  }
-  const uint32_t ab = bits & 0x7FFFFFFFu;
-  int32_t ex = (int32_t)(ab >> 23) - 127;
-  uint32_t keep = (ab >> 20) & 7u;
-  const uint32_t rem = ab & 0xFFFFFu;
-  if (rem > 0x80000u || (rem == 0x80000u && (keep & 1u))) {
-    if (++keep == 8u) {
-      keep = 0;
-      ++ex;
-    }
-  }
-  return sign | ((uint32_t)(ex + 7) << 3) | keep;
 }
 
 // 2^ceil(log2(s)) for finite s > 0, exactly as frexp gives it (mantissa in
@@ -217,6 +188,31 @@ __global__ __launch_bounds__(256) void mxfp4_requant_kernel(const uint8_t *__res
 // ---- FP8 128 x 128 -> 1 x 128 ---------------------------------------------
 // Block (kb, nt): K rows kb*128 .. +127, columns nt*64 .. +63.  The tile is
 // staged [k][n] in LDS; thread t then owns column t/4, rows 32*(t%4) .. +31.
+// Four e4m3 codes (one dword) -> f32, exactly (the gfx950 converter with
+// unit scale decodes OCP e4m3 exactly, NaN codes included).
+__device__ __forceinline__ void e4m3x4_f32(uint32_t w, float *v) {
+  const f32x2_t lo = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(w, 1.0f, false);
+  const f32x2_t hi = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(w, 1.0f, true);
+  v[0] = lo[0];
+  v[1] = lo[1];
+  v[2] = hi[0];
+  v[3] = hi[1];
+}
+
+// Four f32 of magnitude <= 448 -> e4m3 codes, round to nearest even (the
+// converter with unit scale; larger magnitudes never reach it here).
+__device__ __forceinline__ uint32_t f32x4_e4m3(const float *v) {
+  i16x2_t r = {0, 0};
+  r = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(r, v[0], v[1], 1.0f, false);
+  r = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(r, v[2], v[3], 1.0f, true);
+  return __builtin_bit_cast(uint32_t, r);
+}
+
+// FP8 block requant, block (kb, nt): K rows kb*128 .. +127, columns nt*64 ..
+// +63.  Thread t: column nl = t / 4, K part t % 4 (32 values).  With the
+// checkpoint's [N, K] layout the thread loads exactly its own 32 codes; the
+// [K, N] layout is transposed through LDS first.  The new codes leave
+// through the LDS tile as whole 32-byte runs of output rows.
 __global__ __launch_bounds__(256) void fp8_block_requant_kernel(const uint8_t *__restrict__ w,
                                                                 const float *__restrict__ scale, int64_t K, int64_t N,
                                                                 int input_nk, uint8_t *__restrict__ w_out,
@@ -225,33 +221,44 @@ __global__ __launch_bounds__(256) void fp8_block_requant_kernel(const uint8_t *_
   __shared__ __attribute__((aligned(16))) uint8_t s_t[128][64];
   const int t = threadIdx.x;
   const int64_t kb = blockIdx.x, nt = blockIdx.y;
+  const int nl = t >> 2, part = t & 3;
+  uint32_t cw[8];  // the thread's 32 input codes, k = part * 32 + 4 j .. + 3 in word j
   if (input_nk) {
-    const int nl = t >> 2, part = t & 3;
     const uint8_t *src = w + (nt * 64 + nl) * K + kb * 128 + part * 32;
     const u32x4_t a = *(const u32x4_t *)src, b = *(const u32x4_t *)(src + 16);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      s_t[part * 32 + i][nl] = (uint8_t)(a[i >> 2] >> (8 * (i & 3)));
-      s_t[part * 32 + 16 + i][nl] = (uint8_t)(b[i >> 2] >> (8 * (i & 3)));
+    for (int j = 0; j < 4; ++j) {
+      cw[j] = a[j];
+      cw[4 + j] = b[j];
     }
   } else {
     const int kl = t >> 1, h = t & 1;
     const uint8_t *src = w + (kb * 128 + kl) * N + nt * 64 + h * 32;
     *(u32x4_t *)&s_t[kl][h * 32] = *(const u32x4_t *)src;
     *(u32x4_t *)&s_t[kl][h * 32 + 16] = *(const u32x4_t *)(src + 16);
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      uint32_t v = 0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) v |= (uint32_t)s_t[part * 32 + 4 * j + q][nl] << (8 * q);
+      cw[j] = v;
+    }
   }
-  __syncthreads();
-  const int nl = t >> 2, part = t & 3;
   const int64_t n = nt * 64 + nl;
   const float bs = input_nk ? scale[(n / 128) * (K / 128) + kb] : scale[kb * (N / 128) + n / 128];
   float x[32];
   float amax = 0.0f;
   bool finite = true;
 #pragma unroll
-  for (int i = 0; i < 32; ++i) {
-    x[i] = e4m3_f32(s_t[part * 32 + i][nl]) * bs;
-    finite = finite && __builtin_isfinite(x[i]);
-    amax = fmaxf(amax, fabsf(x[i]));
+  for (int j = 0; j < 8; ++j) {
+    e4m3x4_f32(cw[j], x + 4 * j);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      x[4 * j + q] *= bs;
+      finite = finite && __builtin_isfinite(x[4 * j + q]);
+      amax = fmaxf(amax, fabsf(x[4 * j + q]));
+    }
   }
   // The four threads of a column are adjacent lanes.
   amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
@@ -263,19 +270,25 @@ __global__ __launch_bounds__(256) void fp8_block_requant_kernel(const uint8_t *_
   const float s2 = pow2_ceil_f32(all_finite ? amax / 448.0f : 0.0f);
   const float inv = inv_or_zero(s2);
   bool exact = true;
-  uint8_t q[32];
+  uint32_t qw[8];
 #pragma unroll
-  for (int i = 0; i < 32; ++i) {
-    const uint32_t c = all_finite ? rne_e4m3(x[i] * inv) : 0u;
-    q[i] = (uint8_t)c;
-    exact = exact && (e4m3_f32(c) * s2 == x[i]);
+  for (int j = 0; j < 8; ++j) {
+    float y[4], back[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) y[q] = x[4 * j + q] * inv;
+    qw[j] = all_finite ? f32x4_e4m3(y) : 0u;
+    e4m3x4_f32(qw[j], back);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) exact = exact && (back[q] * s2 == x[4 * j + q]);
   }
   int ex = exact ? 1 : 0;
   ex &= __shfl_xor(ex, 1, 64);
   ex &= __shfl_xor(ex, 2, 64);
   __syncthreads();  // every thread has read its inputs before codes overwrite the tile
 #pragma unroll
-  for (int i = 0; i < 32; ++i) s_t[part * 32 + i][nl] = q[i];
+  for (int j = 0; j < 8; ++j)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) s_t[part * 32 + 4 * j + q][nl] = (uint8_t)(qw[j] >> (8 * q));
   if (part == 0) scale_out[kb * N + n] = all_finite ? s2 : __builtin_bit_cast(float, 0x7FC00000u);
   count_flags(part == 0 && all_finite && !ex, status);
   count_flags(part == 0 && !all_finite, status + 1);

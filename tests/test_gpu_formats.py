@@ -102,7 +102,7 @@ def _run_fp8(dev, wc, scale, input_nk):
 
 
 @pytest.mark.parametrize("input_nk", [True, False])
-@pytest.mark.parametrize("k,n", [(512, 384), (384, 512)])  # the 64- and 256-column-tile kernels
+@pytest.mark.parametrize("k,n", [(512, 384), (384, 512)])
 def test_fp8_block_requant_pow2_scales_exact(dev, rng, input_nk, k, n):
     wc = to_e4m3((rng.standard_normal((k, n)) * 3).astype(np.float32))
     scale = np.ldexp(np.float32(1), rng.integers(-12, 0, (k // 128, n // 128))).astype(np.float32)
