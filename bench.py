@@ -377,6 +377,7 @@ def cpu_baseline(wl, budget_s, gpu_check=None):
     relative Frobenius error, the bf16 output rounding included)."""
     import numpy as np
     from oracle import fp4
+    from oracle import gmm as ogmm
     from oracle.numerics import bf16_to_f32, round_bf16
     try:
         from threadpoolctl import threadpool_info, threadpool_limits
@@ -417,14 +418,17 @@ def cpu_baseline(wl, budget_s, gpu_check=None):
         res["value_1thread"] = round(expert_bytes(int(wl.group_sizes[e1])) / dt1 / 1e9, 4)
     if gpu_check is not None:
         e, y = gpu_check
-        ref = lhs[starts[e]:starts[e + 1]].astype(np.float64) @ dequant(e).astype(np.float64)
+        a = lhs[starts[e]:starts[e + 1]].astype(np.float64)
+        w = dequant(e).astype(np.float64)
+        ref = a @ w
         err = y.astype(np.float64) - ref
-        # one bf16 ulp of the reference value (8 significant bits)
-        ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(ref), 2.0 ** -126))) - 7)
+        # the stated per-element tolerance (bf16 output rounding plus K * 2^-24
+        # times sum_k |a_k w_k|, any order of f32 accumulation)
+        bound = ogmm.error_bound(ref, np.abs(a) @ np.abs(w), wl.K, "bfloat16")
         res["parity"] = {"expert": int(e), "rows": int(ref.shape[0]),
                          "max_abs_err": float(np.abs(err).max()),
                          "rel_frobenius": float(np.linalg.norm(err) / np.linalg.norm(ref)),
-                         "max_err_bf16_ulps": float((np.abs(err) / ulp).max()),
+                         "max_err_over_tolerance": float((np.abs(err) / bound).max()),
                          "vs": "float64 oracle product of the same bf16 lhs and exact fp4 weights"}
     return res
 
