@@ -711,8 +711,9 @@ static void launch_dense(const void *x, const float *sx, int64_t M, int64_t K, i
 }
 
 // MFMA path (M > 16, N % 128 == 0): W8A16 128x128 tiles (4 waves, two or
-// three 25 KB stages: two blocks per CU); W8A8 256x128 tiles (8 waves, four
-// 26 KB stages, fragments read one step ahead) from M >= 256, 128x128 below.  K is split over blocks until the
+// three 25 KB stages: two blocks per CU), 256x128 tiles (8 waves) when those
+// alone fill the grid; W8A8 256x128 tiles (8 waves, four 26 KB stages,
+// fragments read one step ahead) from M >= 256, 128x128 below.  K is split over blocks until the
 // grid covers the 256 CUs; the f32 partials go to the workspace and
 // dense_fp8_reduce_kernel adds them in split order (deterministic).
 static bool dense_mfma_ok(int64_t M, int64_t K, int64_t N) {
@@ -747,6 +748,13 @@ static int launch_dense_mfma(const void *x, const float *sx, int64_t M, int64_t 
     using C = DenseMfmaCfg<2, 2, true>;
     const dim3 grid((unsigned)(N / C::BN), (unsigned)((M + C::BM - 1) / C::BM), (unsigned)ks);
     hipLaunchKernelGGL((dense_fp8_mfma_kernel<C, true, 4, true>), grid, dim3(C::THREADS), 0, st, x, sx, M, (int)K,
+                       (int)N, w, sw, sw_ld, ks, out, partial);
+  } else if (ks == 1 && (N / 128) * ((M + 255) / 256) >= 256) {
+    // Enough rows for 256 x 128 tiles to fill the grid: half the weight
+    // re-reads of 128-row tiles (8 waves, one block per CU).
+    using C = DenseMfmaCfg<4, 2, false>;
+    const dim3 grid((unsigned)(N / C::BN), (unsigned)((M + C::BM - 1) / C::BM), 1);
+    hipLaunchKernelGGL((dense_fp8_mfma_kernel<C, false, 2>), grid, dim3(C::THREADS), 0, st, x, sx, M, (int)K,
                        (int)N, w, sw, sw_ld, ks, out, partial);
   } else {
     using C = DenseMfmaCfg<2, 2, false>;

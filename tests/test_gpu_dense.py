@@ -25,7 +25,7 @@ def _check(out, y64, ap, K):
 
 @pytest.mark.parametrize("M,K,N", [(1, 1024, 512), (3, 256, 48), (16, 1024, 512), (17, 512, 256),
                                    (100, 1024, 384), (128, 1024, 512), (300, 768, 256), (256, 512, 128),
-                                   (513, 1024, 640)])
+                                   (513, 1024, 640), (1900, 256, 4096)])  # the last: 256-row tiles, ragged M
 def test_w8a16_small_shapes(dev, M, K, N):
     from dw_tpu_amd.dense_fp8 import matmul
     from dw_tpu_amd.workloads import make_dense_workload
