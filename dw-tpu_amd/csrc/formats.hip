@@ -314,6 +314,31 @@ __device__ __forceinline__ void count_add(int v, int32_t *counter) {
 // Thread t: column octet o = t / 8 (columns 8 o .. 8 o + 7), K-block t % 8.
 // Its 32 x 8 codes are packed per row into words of 8 nibbles and staged as
 // s_out[kb][i][o] (kb blocks padded by 8 words: conflict-free writes).
+// In-register transpose of an 8 x 8 matrix of nibbles, element (r, s) =
+// nibble s of x[r] -> nibble r of x[s]: three rounds of block swaps (2 x 2,
+// 4 x 4, 8 x 8 blocks), the bit-matrix transpose of Hacker's Delight
+// (section 7-3) on 4-bit elements.
+__device__ __forceinline__ void transpose8x8_nibbles(uint32_t *x) {
+#pragma unroll
+  for (int r = 0; r < 8; r += 2) {
+    const uint32_t t = ((x[r] >> 4) ^ x[r + 1]) & 0x0F0F0F0Fu;
+    x[r + 1] ^= t;
+    x[r] ^= t << 4;
+  }
+#pragma unroll
+  for (int r = 0; r < 8; r += (r & 1) ? 3 : 1) {  // r = 0, 1, 4, 5
+    const uint32_t t = ((x[r] >> 8) ^ x[r + 2]) & 0x00FF00FFu;
+    x[r + 2] ^= t;
+    x[r] ^= t << 8;
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const uint32_t t = ((x[r] >> 16) ^ x[r + 4]) & 0x0000FFFFu;
+    x[r + 4] ^= t;
+    x[r] ^= t << 16;
+  }
+}
+
 __global__ __launch_bounds__(256) void mxfp4_requant_tile_kernel(const uint8_t *__restrict__ blocks,
                                                                  const uint8_t *__restrict__ scales, int64_t N,
                                                                  int64_t K, int interleave,
@@ -325,9 +350,7 @@ __global__ __launch_bounds__(256) void mxfp4_requant_tile_kernel(const uint8_t *
   __shared__ __attribute__((aligned(16))) uint8_t s_sc[8][256];
   const int t = threadIdx.x, o = t >> 3, kb = t & 7;
   const int64_t e = blockIdx.z, k0 = (int64_t)blockIdx.x * 256, n0 = (int64_t)blockIdx.y * 256;
-  uint32_t ow[32];
-#pragma unroll
-  for (int i = 0; i < 32; ++i) ow[i] = 0;
+  uint32_t qc[4][8];  // qc[j][c]: codes k = 8 j .. 8 j + 7 (nibbles) of column c
   uint32_t sc_lo = 0, sc_hi = 0;
   int nlossy = 0, nnonfinite = 0;
 #pragma unroll
@@ -336,12 +359,25 @@ __global__ __launch_bounds__(256) void mxfp4_requant_tile_kernel(const uint8_t *
     const u32x4_t in = *(const u32x4_t *)(blocks + (e * N + n) * (K / 2) + k0 / 2 + kb * 16);
     const Mx4Group g = mxfp4_group(in, scales[(e * N + n) * (K / 32) + k0 / 32 + kb]);
 #pragma unroll
-    for (int i = 0; i < 32; ++i) ow[i] |= ((g.q[i >> 3] >> (4 * (i & 7))) & 0xFu) << (4 * c);
+    for (int j = 0; j < 4; ++j) qc[j][c] = g.q[j];
     const uint32_t scode = g.scode;
     nlossy += g.lossy ? 1 : 0;
     nnonfinite += g.finite ? 0 : 1;
     if (c < 4) sc_lo |= scode << (8 * c);
     else sc_hi |= scode << (8 * (c - 4));
+  }
+  // ow[i]: the 8 columns' codes of row k = i, column c in nibble c; with
+  // interleave the columns are taken in the order 0, 2, 4, 6, 1, 3, 5, 7, so
+  // the low half-word holds the even (w1) and the high one the odd (w3) codes.
+  uint32_t ow[32];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    uint32_t x[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) x[c] = interleave ? qc[j][(c < 4) ? 2 * c : 2 * (c - 4) + 1] : qc[j][c];
+    transpose8x8_nibbles(x);
+#pragma unroll
+    for (int r = 0; r < 8; ++r) ow[8 * j + r] = x[r];
   }
   if (!interleave) {
 #pragma unroll
@@ -350,15 +386,12 @@ __global__ __launch_bounds__(256) void mxfp4_requant_tile_kernel(const uint8_t *
     *(uint32_t *)&s_sc[kb][8 * o + 4] = sc_hi;
   } else {
     // Even columns (w1) go to the first half of the output, odd (w3) to the
-    // second: this octet's even / odd nibbles are positions 4 o .. 4 o + 3.
+    // second: this octet's even / odd codes are positions 4 o .. 4 o + 3.
 #pragma unroll
     for (int i = 0; i < 32; ++i) {
-      const uint32_t w = ow[i];
-      const uint32_t ev = (w & 0xFu) | ((w >> 4) & 0xF0u) | ((w >> 8) & 0xF00u) | ((w >> 12) & 0xF000u);
-      const uint32_t od = ((w >> 4) & 0xFu) | ((w >> 8) & 0xF0u) | ((w >> 12) & 0xF00u) | ((w >> 16) & 0xF000u);
       uint16_t *row = (uint16_t *)&s_out[kb * KBW + i * 32];
-      row[o] = (uint16_t)ev;
-      row[32 + o] = (uint16_t)od;
+      row[o] = (uint16_t)(ow[i] & 0xFFFFu);
+      row[32 + o] = (uint16_t)(ow[i] >> 16);
     }
     const uint32_t sev = (sc_lo & 0xFFu) | ((sc_lo >> 8) & 0xFF00u) | ((sc_hi << 16) & 0xFF0000u) | ((sc_hi << 8) & 0xFF000000u);
     const uint32_t sod = ((sc_lo >> 8) & 0xFFu) | ((sc_lo >> 16) & 0xFF00u) | ((sc_hi << 8) & 0xFF0000u) | (sc_hi & 0xFF000000u);
