@@ -60,6 +60,20 @@ def test_gmm_argument_checks_need_no_gpu():
     assert rc == _lib.ERR_UNSUPPORTED and "fuse_act" in msg
     rc, msg = _rc("dwm_gmm_fp4_prepack_gate_up", null, 0, null, _lib.U8, 1, 128, 80, null, null, null, null)
     assert rc == _lib.ERR_UNSUPPORTED and "64" in msg
+    # the fused-gather entry: its own checks, then the gmm's
+    g = "dwm_gmm_fp4_gather"
+    rc, msg = _rc(g, null, 10, null, 8, 128, null, null, null, 4, null, 4, 64, null, _lib.BF16, 0, 0, null)
+    assert rc == _lib.ERR_INVALID and "row_idx" in msg
+    rc, msg = _rc(g, null, -1, null, 8, 128, null, null, null, 4, null, 4, 64, null, _lib.BF16, 0, 0, null)
+    assert rc == _lib.ERR_INVALID and "lhs_rows" in msg
+    idx = (ctypes.c_int32 * 8)()
+    rc, msg = _rc(g, null, 10, idx, 8, 192, null, null, null, 4, null, 4, 64, null, _lib.BF16, 0, 0, null)
+    assert rc == _lib.ERR_UNSUPPORTED and "K" in msg
+    rc, msg = _rc(g, ctypes.c_void_p(16), 1 << 20, idx, 8, 4096, ctypes.c_void_p(16), ctypes.c_void_p(16),
+                  ctypes.c_void_p(16), 4, null, 4, 64, ctypes.c_void_p(16), _lib.BF16, 0, 0, null)
+    assert rc == _lib.ERR_UNSUPPORTED and "too large" in msg  # 32-bit lhs row offsets
+    rc, _ = _rc(g, null, 0, null, 0, 128, null, null, null, 4, null, 4, 64, null, _lib.BF16, 0, 0, null)
+    assert rc == _lib.OK  # M == 0: nothing to do
 
 
 def test_prepack_size_query():
