@@ -81,6 +81,9 @@ class MoeBlockGraph:
         self.topk_weights = topk_weights.clone()
         if isinstance(group_offset, torch.Tensor):
             group_offset = group_offset.clone()
+        elif group_offset is not None:
+            # an int would become a host-to-device copy inside the capture
+            group_offset = torch.tensor([int(group_offset)], dtype=torch.int32, device=hidden.device)
         args = (w13, w2, num_experts)
         kw = dict(group_offset=group_offset, f32_reduce=f32_reduce)
         self._keep = (w13, w2, group_offset)

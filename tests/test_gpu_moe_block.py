@@ -192,3 +192,21 @@ def test_moe_block_graph_replays_match_eager(dev, rng):
         # eager work between replays
         moe_block(hidden, tid, tw, w13, w2, E)
         torch.cuda.synchronize()
+
+
+def test_moe_block_graph_with_group_offset(dev, rng):
+    """An expert-parallel shard (group_offset as an int) captured and replayed."""
+    from dw_tpu_amd import MoeBlockGraph, fp4_weight_to_codes, moe_block
+    T, E, topk, H, I = 48, 8, 2, 256, 128
+    ids, wts, hidden_bits, (r13, s13), (r2, s2) = _block_case(rng, T, E, topk, H, I)
+    lo, hi = 2, 6  # this shard's experts
+    w13 = fp4_weight_to_codes(torch.from_numpy(r13[lo:hi]).to(dev), torch.from_numpy(s13[lo:hi]).to(dev),
+                              gate_up=True)
+    w2 = fp4_weight_to_codes(torch.from_numpy(r2[lo:hi]).to(dev), torch.from_numpy(s2[lo:hi]).to(dev))
+    hidden, tid, tw = bf16_tensor(hidden_bits, dev), torch.from_numpy(ids).to(dev), torch.from_numpy(wts).to(dev)
+    want = moe_block(hidden, tid, tw, w13, w2, E, group_offset=lo)
+    g = MoeBlockGraph(hidden, tid, tw, w13, w2, E, group_offset=lo)
+    for _ in range(3):
+        got = g().clone()
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16))
