@@ -243,9 +243,9 @@ __global__ __launch_bounds__(kDenseThreads) void dense_fp8_kernel(
 }
 
 // Skinny M (<= 16 rows, decode): one block owns 16 columns and KS waves split
-// its K steps.  Each wave streams its contiguous prepacked weight chunks
-// through a D-deep register ring and loads its lhs fragments straight from
-// L2 (only rows < M); there is no LDS staging and no barrier in the K loop.
+// its K steps.  Each wave streams its contiguous prepacked weight chunks and
+// its lhs fragments (straight from L2, only rows < M) through a D-deep
+// register ring; there is no LDS staging and no barrier in the K loop.
 // The waves' f32 partial sums are added in LDS in wave order (deterministic)
 // and rounded once, in the same launch.
 template <int KS, int D, bool A8>
@@ -265,15 +265,34 @@ __global__ __launch_bounds__(64 * KS) void dense_fp8_skinny_kernel(
   const uint8_t *const wp = wpk + (int64_t)nb * KB * 2048 + lane * 32;
   // lhs fragment of MFMA step s: row r, k = 128 kb + 32 q + 8 s .. + 7
   const uint8_t *const xrow = (const uint8_t *)xin + (int64_t)(rok ? r : 0) * K * (A8 ? 1 : 2) + 32 * q * (A8 ? 1 : 2);
-  u32x4_t wlo[D], whi[D];
-  auto load_w = [&](int slot, int kb) {
+  // Everything a K block reads -- its weight chunk, its lhs fragments and its
+  // scales -- travels in one D-deep register ring, loaded in K-block order:
+  // the wait for block kb then covers only loads issued before those of
+  // block kb + 1 (vector loads complete in order), so D blocks stay in flight.
+  constexpr int XW = A8 ? 2 : 4;  // 16-byte lhs loads per K block
+  u32x4_t wlo[D], whi[D], xa[D][XW];
+  float wsc[D], xsc[D][4];
+  auto load = [&](int slot, int kb) {
     const u32x4_t *p = (const u32x4_t *)(wp + (int64_t)kb * 2048);
     wlo[slot] = p[0];
     whi[slot] = p[1];
+    if (rok) {
+      const u32x4_t *xp = (const u32x4_t *)(xrow + (int64_t)kb * (A8 ? 128 : 256));
+#pragma unroll
+      for (int s = 0; s < XW; ++s) xa[slot][s] = xp[s];
+    } else {
+#pragma unroll
+      for (int s = 0; s < XW; ++s) xa[slot][s] = u32x4_t{0u, 0u, 0u, 0u};
+    }
+    wsc[slot] = A8 ? sw[(int64_t)kb * sw_ld + (col >> 7)] : sw[(int64_t)kb * sw_ld + col];
+    if (A8) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) xsc[slot][i] = sx[(int64_t)min(4 * q + i, M - 1) * KB + kb];
+    }
   };
 #pragma unroll
   for (int d = 0; d < D; ++d)
-    if (kb_begin + d < kb_end) load_w(d, kb_begin + d);
+    if (kb_begin + d < kb_end) load(d, kb_begin + d);
   f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
   for (int kb0 = kb_begin; kb0 < kb_end; kb0 += D) {
 #pragma unroll
@@ -281,28 +300,24 @@ __global__ __launch_bounds__(64 * KS) void dense_fp8_skinny_kernel(
       const int kb = kb0 + d;
       if (kb >= kb_end) break;
       u32x4_t a[4];
-      if (rok) {
-        if (A8) {
-          const u32x4_t *xp = (const u32x4_t *)(xrow + (int64_t)kb * 128);
-          const u32x4_t v0 = xp[0], v1 = xp[1];
+      if (A8) {
 #pragma unroll
-          for (int s = 0; s < 4; ++s) {
-            const uint32_t w0 = s < 2 ? v0[2 * s] : v1[2 * s - 4];
-            const uint32_t w1 = s < 2 ? v0[2 * s + 1] : v1[2 * s - 3];
-            a[s] = u32x4_t{cvt_fp8x2_bf16<false>(w0), cvt_fp8x2_bf16<true>(w0), cvt_fp8x2_bf16<false>(w1),
-                           cvt_fp8x2_bf16<true>(w1)};
-          }
-        } else {
-          const u32x4_t *xp = (const u32x4_t *)(xrow + (int64_t)kb * 256);
-#pragma unroll
-          for (int s = 0; s < 4; ++s) a[s] = xp[s];
+        for (int s = 0; s < 4; ++s) {
+          const uint32_t w0 = s < 2 ? xa[d][0][2 * s] : xa[d][1][2 * s - 4];
+          const uint32_t w1 = s < 2 ? xa[d][0][2 * s + 1] : xa[d][1][2 * s - 3];
+          a[s] = u32x4_t{cvt_fp8x2_bf16<false>(w0), cvt_fp8x2_bf16<true>(w0), cvt_fp8x2_bf16<false>(w1),
+                         cvt_fp8x2_bf16<true>(w1)};
         }
       } else {
 #pragma unroll
-        for (int s = 0; s < 4; ++s) a[s] = u32x4_t{0u, 0u, 0u, 0u};
+        for (int s = 0; s < 4; ++s) a[s] = xa[d][s];
       }
       const u32x4_t lo = wlo[d], hi = whi[d];
-      if (kb + D < kb_end) load_w(d, kb + D);
+      const float wscale = wsc[d];
+      float f[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) f[i] = A8 ? xsc[d][i] * wscale : wscale;
+      if (kb + D < kb_end) load(d, kb + D);
       f32x4_t part = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
@@ -314,16 +329,8 @@ __global__ __launch_bounds__(64 * KS) void dense_fp8_skinny_kernel(
                                                        __builtin_bit_cast(bf16x8_t, b), part, 0, 0, 0);
       }
       // acc += part * scale (f32 multiply, then f32 add)
-      const float wscale = A8 ? sw[(int64_t)kb * sw_ld + (col >> 7)] : sw[(int64_t)kb * sw_ld + col];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float f = wscale;
-        if (A8) {
-          const int m = min(4 * q + i, M - 1);
-          f = sx[(int64_t)m * KB + kb] * wscale;
-        }
-        acc[i] = acc[i] + part[i] * f;
-      }
+      for (int i = 0; i < 4; ++i) acc[i] = acc[i] + part[i] * f[i];
     }
   }
   if (wave > 0) s_red[wave - 1][lane] = acc;
@@ -783,8 +790,10 @@ static int run_dense(const void *x, const float *sx, int64_t M, int64_t K, int64
   if (dense_mfma_ok(M, K, N))
     return launch_dense_mfma<A8>(x, sx, M, K, N, w, sw, sw_ld, out, workspace, workspace_bytes, st);
   if (M <= 16) {
-    // 16 waves split K, two weight steps in flight per wave (64 KB per
-    // block); measured fastest of 4/8/16 waves x 2/4/8 steps at K=7168, N=4096.
+    // 16 waves split K, two K blocks (weights, lhs fragments and scales) in
+    // flight per wave; 4/8/16 waves x 2..7 blocks in flight all measured
+    // within 0.5 us at K=7168, N=4096: the 29 MB stream plus launch and start-up
+    // latency sets the time (8 us at M = 1).
     hipLaunchKernelGGL((dense_fp8_skinny_kernel<16, 2, A8>), dim3((unsigned)(N / 16)), dim3(1024), 0, st, x, sx,
                        (int)M, (int)K, (int)N, w, sw, sw_ld, out);
     return launch_status("dense_fp8");
