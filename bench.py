@@ -174,21 +174,10 @@ def bench_dispatch_combine(dev, steps, warmup):
     return res
 
 
-def bench_moe_block(dev, steps, warmup):
-    """The decode-size expert block through ``moe_block``: 256 tokens x top-8
-    over 32 experts (decode_gate_up routing), dispatch + gmm1 over the
-    routed rows of hidden [256, 7168] (gathered inside the gmm) x
-    [7168, 2x2048] with the fused silu_and_mul_with_clamp (out [2048, 2048])
-    + gmm2 [2048, 2048] x [2048, 7168] + combine to [256, 7168].  Two weight
-    copies are rotated."""
-    import numpy as np
+def _block_weights(dev, E, H, I, copies):
+    """Random gate/up and down expert weights (prepacked), ``copies`` sets."""
     import torch
-    from dw_tpu_amd import MoeBlockGraph, fp4_weight_to_codes, moe_block
-    from dw_tpu_amd.workloads import make_gmm_workload
-    wl = make_gmm_workload("decode_gate_up", with_data=False)
-    H, I, E = wl.K, wl.N // 2, wl.E
-    rng = np.random.Generator(np.random.PCG64(12))
-    copies = 2
+    from dw_tpu_amd import fp4_weight_to_codes
     w13s, w2s = [], []
     for _ in range(copies):
         r13 = torch.randint(0, 256, (E, H, I), dtype=torch.uint8, device=dev)   # [E, H, 2I] packed
@@ -198,13 +187,10 @@ def bench_moe_block(dev, steps, warmup):
         s2 = torch.randint(118, 124, (E, I // 32, 1, H), dtype=torch.uint8, device=dev)
         w2s.append(fp4_weight_to_codes(r2, s2))
         del r13, s13, r2, s2
-    hidden = torch.from_numpy(rng.standard_normal((wl.T, H), dtype=np.float32)).to(torch.bfloat16).to(dev)
-    ids = torch.from_numpy(wl.topk_ids).to(dev)
-    wts = torch.from_numpy(wl.topk_weights).to(dev)
-    ms = time_steps(lambda i: moe_block(hidden, ids, wts, w13s[i % copies], w2s[i % copies], E), steps, warmup)
-    # the same block captured once per weight copy (MoeBlockGraph) and replayed
-    graphs = [MoeBlockGraph(hidden, ids, wts, w13s[c], w2s[c], E) for c in range(copies)]
-    ms_graph = time_steps(lambda i: graphs[i % copies](), steps, warmup)
+    return w13s, w2s
+
+
+def _block_result(wl, ms, H, I):
     nonempty = int((wl.group_sizes > 0).sum())
     n = wl.M
     wbytes = nonempty * (H * 2 * I // 2 + H // 32 * 2 * I + I * H // 2 + I // 32 * H)
@@ -214,14 +200,50 @@ def bench_moe_block(dev, steps, warmup):
     act_bytes = wl.T * H * 2 + 2 * n * I * 2 + 2 * n * H * 2 + wl.T * H * 2
     flops = 2 * n * H * 2 * I + 2 * n * I * H
     gbs = (wbytes + act_bytes) / (ms * 1e-3) / 1e9
-    return {"moe_block_decode": {"ms": round(ms, 5), "GB_s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
-                                 "TFLOP_s": round(flops / (ms * 1e-3) / 1e12, 1), "bytes": wbytes + act_bytes,
-                                 "flops": flops, "T": wl.T, "topk": wl.topk, "H": H, "I": I, "E": E,
-                                 "nonempty_groups": nonempty},
-            "moe_block_decode_graph": {"ms": round(ms_graph, 5),
-                                       "GB_s": round((wbytes + act_bytes) / (ms_graph * 1e-3) / 1e9, 1),
-                                       "TFLOP_s": round(flops / (ms_graph * 1e-3) / 1e12, 1),
-                                       "note": "the same block replayed from a captured HIP graph"}}
+    return {"ms": round(ms, 5), "GB_s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "TFLOP_s": round(flops / (ms * 1e-3) / 1e12, 1), "mfma_bf16_frac": round(flops / (ms * 1e-3) / 1e12
+                                                                                   / BF16_PEAK_TFLOPS, 4),
+            "bytes": wbytes + act_bytes, "flops": flops, "T": wl.T, "topk": wl.topk, "H": H, "I": I, "E": wl.E,
+            "nonempty_groups": nonempty}
+
+
+def bench_moe_block(dev, steps, warmup):
+    """The expert block through ``moe_block``: dispatch + gmm1 over the routed
+    rows of hidden [T, 7168] (gathered inside the gmm) x [7168, 2x2048] with
+    the fused silu_and_mul_with_clamp + gmm2 [., 2048] x [2048, 7168] +
+    combine to [T, 7168], over 32 experts.  Decode: 256 tokens x top-8
+    (decode_gate_up routing), also replayed from a captured HIP graph;
+    prefill: 8192 tokens x top-8 (the prefill workload's skewed routing).
+    Two weight copies are rotated."""
+    import numpy as np
+    import torch
+    from dw_tpu_amd import MoeBlockGraph, moe_block
+    from dw_tpu_amd.workloads import make_gmm_workload
+    res = {}
+    copies = 2
+    for name, key in (("decode_gate_up", "moe_block_decode"), ("prefill", "moe_block_prefill")):
+        wl = make_gmm_workload(name, with_data=False)
+        H, I, E = wl.K, wl.N // 2, wl.E
+        w13s, w2s = _block_weights(dev, E, H, I, copies)
+        rng = np.random.Generator(np.random.PCG64(12))
+        hidden = torch.from_numpy(rng.standard_normal((wl.T, H), dtype=np.float32)).to(torch.bfloat16).to(dev)
+        ids = torch.from_numpy(wl.topk_ids).to(dev)
+        wts = torch.from_numpy(wl.topk_weights).to(dev)
+        big = name == "prefill"
+        n_steps, n_warm = (min(steps, 5), min(warmup, 3)) if big else (steps, warmup)
+        ms = time_steps(lambda i: moe_block(hidden, ids, wts, w13s[i % copies], w2s[i % copies], E), n_steps, n_warm)
+        res[key] = _block_result(wl, ms, H, I)
+        if not big:
+            # the same block captured once per weight copy (MoeBlockGraph) and replayed
+            graphs = [MoeBlockGraph(hidden, ids, wts, w13s[c], w2s[c], E) for c in range(copies)]
+            ms_graph = time_steps(lambda i: graphs[i % copies](), steps, warmup)
+            g = _block_result(wl, ms_graph, H, I)
+            res["moe_block_decode_graph"] = {"ms": g["ms"], "GB_s": g["GB_s"], "TFLOP_s": g["TFLOP_s"],
+                                             "note": "the same block replayed from a captured HIP graph"}
+            del graphs
+        del w13s, w2s, hidden
+        torch.cuda.empty_cache()
+    return res
 
 
 def bench_routing(dev, steps, warmup):
