@@ -127,3 +127,23 @@ def test_dense_repeatable_and_prepack_equivalent(dev):
     c = matmul(x, w.view(torch.float8_e4m3fn), s)
     assert torch.equal(a.view(torch.int16), b.view(torch.int16))
     assert torch.equal(a.view(torch.int16), c.view(torch.int16))
+
+
+def test_dense_full_size_exact_scaling(dev):
+    """At M = 4096 (K=7168, N=4096): doubling the bf16 activations doubles the
+    W8A16 output exactly (every product, partial sum and scale product scales
+    by a power of two); doubling the W8A8 row scales does the same."""
+    from dw_tpu_amd.dense_fp8 import matmul, matmul_w8a8, prepack_fp8
+    from dw_tpu_amd.workloads import make_dense_workload
+    wl = make_dense_workload(4096)
+    pw = prepack_fp8(torch.from_numpy(wl.wq).to(dev))
+    x = bf16_tensor(wl.x_bits, dev)
+    s16 = torch.from_numpy(wl.s_w8a16).to(dev)
+    a = matmul(x, pw, s16).float()
+    b = matmul(x * 2, pw, s16).float()
+    assert torch.equal(b, a * 2)
+    xq, sx, sw = (torch.from_numpy(v).to(dev) for v in (wl.xq, wl.sx, wl.sw))
+    a8 = matmul_w8a8(xq, sx, pw, sw).float()
+    b8 = matmul_w8a8(xq, sx * 2, pw, sw).float()
+    torch.cuda.synchronize()
+    assert torch.equal(b8, a8 * 2)

@@ -243,3 +243,53 @@ def test_gmm_fused_row_gather_equals_gather_then_gmm(dev, rng, fused_act, group_
     torch.cuda.synchronize()
     assert got.shape == want.shape
     assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
+@pytest.mark.parametrize("name", ["decode_gate_up", "prefill"])
+def test_gmm_full_size_exact_scaling(dev, name):
+    """A size-independent property at the full workload: doubling the lhs is
+    exact in bf16, and so is every product and every f32 partial sum, so
+    gmm(2 lhs) == 2 gmm(lhs) bit for bit (an order- or index-dependent bug,
+    such as a row read from the wrong tile, breaks it only by chance)."""
+    from dw_tpu_amd import fp4_weight_to_codes, gmm_v2
+    from dw_tpu_amd.workloads import make_gmm_workload
+    wl = make_gmm_workload(name)
+    pw = fp4_weight_to_codes(torch.from_numpy(wl.rhs_e2m1).to(dev), torch.from_numpy(wl.scale_codes).to(dev))
+    lhs = bf16_tensor(wl.lhs_bits, dev)
+    gs = torch.from_numpy(wl.group_sizes).to(dev)
+    y1 = gmm_v2(lhs, pw, gs, preferred_element_type=torch.float32)
+    y2 = gmm_v2(lhs * 2, pw, gs, preferred_element_type=torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(y2, y1 * 2)
+    assert torch.isfinite(y1).all()
+
+
+def test_gmm_full_size_row_permutation_and_group_independence(dev, rng):
+    """decode_gate_up at full size: permuting rows inside each expert group
+    permutes the output rows bit for bit (each row's result depends on its
+    own lhs row only), and rewriting one expert's weights leaves every other
+    group's rows bit-identical."""
+    from dw_tpu_amd import fp4_weight_to_codes, gmm_v2
+    from dw_tpu_amd.workloads import make_gmm_workload
+    wl = make_gmm_workload("decode_gate_up")
+    rhs = torch.from_numpy(wl.rhs_e2m1).to(dev)
+    sc = torch.from_numpy(wl.scale_codes).to(dev)
+    pw = fp4_weight_to_codes(rhs, sc)
+    lhs = bf16_tensor(wl.lhs_bits, dev)
+    gs = torch.from_numpy(wl.group_sizes).to(dev)
+    y = gmm_v2(lhs, pw, gs)
+    starts = np.concatenate([[0], np.cumsum(wl.group_sizes)])
+    perm = np.concatenate([s + rng.permutation(n) for s, n in zip(starts[:-1], wl.group_sizes)]).astype(np.int64)
+    p = torch.from_numpy(perm).to(dev)
+    yp = gmm_v2(lhs[p].contiguous(), pw, gs)
+    assert torch.equal(yp.view(torch.int16), y[p].view(torch.int16))
+    g = int(np.flatnonzero(wl.group_sizes > 0)[1])
+    rhs2 = rhs.clone()
+    rhs2[g] = torch.randint(0, 256, rhs2[g].shape, dtype=torch.uint8, device=dev)
+    y2 = gmm_v2(lhs, fp4_weight_to_codes(rhs2, sc), gs)
+    torch.cuda.synchronize()
+    other = np.ones(wl.M, bool)
+    other[starts[g]:starts[g + 1]] = False
+    o = torch.from_numpy(np.flatnonzero(other)).to(dev)
+    assert torch.equal(y2[o].view(torch.int16), y[o].view(torch.int16))
+    assert not torch.equal(y2[starts[g]:starts[g + 1]].view(torch.int16), y[starts[g]:starts[g + 1]].view(torch.int16))
