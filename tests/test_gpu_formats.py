@@ -1,7 +1,7 @@
 """Checkpoint weight formats on the GPU (dwm_mxfp4_requant,
 dwm_fp8_block_requant): bit-exact against oracle/checkpoint.py, including
-every checkpoint scale code, -0, NaN / overflow groups and both layouts, and
-end to end into the gmm's prepacked weights."""
+every checkpoint scale code, -0, NaN / overflow groups and both layouts, end
+to end into the gmm's prepacked weights, and at full checkpoint size."""
 import numpy as np
 import pytest
 import torch
@@ -122,3 +122,42 @@ def test_fp8_block_requant_general_scales_and_edges(dev, rng):
     wc2 = wc.copy()
     wc2[(wc2 & 0x7F) == 0x7F] = 0x80                            # no NaN: -0 instead
     _run_fp8(dev, wc2, scale, False)
+
+
+def test_mxfp4_full_size_gate_up_checkpoint(dev):
+    # The whole 32-expert gate/up checkpoint (N = 2 x 2048 interleaved w1/w3
+    # columns, K = 7168) in one call: the first and the last expert bit-exact
+    # against the oracle, the status counters over every expert.
+    e, n, k = 32, 4096, 7168
+    g = torch.Generator(device=dev).manual_seed(7)
+    blocks = torch.randint(0, 256, (e, n, k // 2), dtype=torch.uint8, device=dev, generator=g)
+    scales = torch.randint(110, 135, (e, n, k // 32), dtype=torch.uint8, device=dev, generator=g)
+    planted = [(0, 5, 3), (0, 4095, 223), (13, 2048, 100), (31, 1, 0), (31, 3000, 77)]
+    for ex, col, grp in planted:
+        scales[ex, col, grp] = 255  # a NaN scale: the whole group is non-finite
+    from dw_tpu_amd import mxfp4_requant
+    q, sc, st = mxfp4_requant(blocks, scales, True)
+    torch.cuda.synchronize()
+    assert (st.inexact_groups, st.nonfinite_groups) == (0, len(planted))
+    for ex in (0, e - 1):
+        wq, wsc, lossy, nonfinite = C.mxfp4_requant(blocks[ex:ex + 1].cpu().numpy(),
+                                                    scales[ex:ex + 1].cpu().numpy(), True)
+        assert lossy == 0 and nonfinite == sum(p[0] == ex for p in planted)
+        got_q = _unpack_n(q[ex:ex + 1].cpu().numpy())
+        assert np.array_equal(got_q, wq), (ex, np.argwhere(got_q != wq)[:5])
+        got_sc = sc[ex:ex + 1].cpu().numpy()[:, :, 0, :]
+        assert np.array_equal(got_sc, wsc), (ex, np.argwhere(got_sc != wsc)[:5])
+
+
+@pytest.mark.parametrize("input_nk", [True, False])
+def test_fp8_block_requant_full_size(dev, rng, input_nk):
+    # A whole DeepSeek FP8 projection (N = 4096, K = 7168) with general block
+    # scales: bit-exact codes and scales, and the same inexact-block count.
+    n, k = 4096, 7168
+    wc = rng.integers(0, 256, (n, k), dtype=np.uint8)
+    wc[(wc & 0x7F) == 0x7F] = 0  # no NaN codes: every block finite
+    scale = (rng.random((n // 128, k // 128)) * 0.02 + 1e-4).astype(np.float32)
+    if not input_nk:
+        wc, scale = wc.T.copy(), scale.T.copy()
+    st = _run_fp8(dev, wc, scale, input_nk)
+    assert st.nonfinite_groups == 0 and st.inexact_groups > 0
