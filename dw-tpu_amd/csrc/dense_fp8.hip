@@ -365,7 +365,11 @@ __global__ __launch_bounds__(64 * KS) void dense_fp8_skinny_kernel(
 // with p flipped for c >= 8 (lane l loads slot l ^ ((l >> 4) & 1)), so that
 // 16 lanes reading one slot of 16 consecutive columns hit distinct bank
 // groups; then the scales: W8A16 the block's column scales of the step's K
-// block, W8A8 the block's row scales sx[., kb] and sw[kb, n0/128].
+// block, W8A8 sw[kb, n0/128] (every wave loads it, so each wave issues the
+// same loads per step).  W8A8's row scales sit outside the ring: every 8 K
+// blocks the waves load sx[row0 .. + BM - 1, the next 8 K blocks] into one
+// of two [BM][8] f32 buffers, 8 rows of 32 contiguous bytes per load (a
+// column of sx read per step would touch one line per row).
 template <int WM, int WN, bool A8>
 struct DenseMfmaCfg {
   static constexpr int WAVES = WM * WN, THREADS = 64 * WAVES, WCOLS = WN;
@@ -376,12 +380,15 @@ struct DenseMfmaCfg {
   static constexpr int S = B + BN * 64;
   static constexpr int S_BYTES = WAVES * 256;  // one 64-value scale load per wave
   static constexpr int STAGE = (S + S_BYTES + 1023) / 1024 * 1024;
+  static constexpr int SX_BUF = BM * 8 * 4;                        // W8A8: [BM rows][8 K blocks] f32
+  static constexpr int SX_BYTES = A8 ? 2 * SX_BUF : 0;
+  static constexpr int SX_LOADS = A8 ? BM / 8 / WAVES : 0;         // 8-row loads per wave per 8 K blocks
   static constexpr int A_LOADS = BM * A_ROW / 1024 / WAVES;  // 1 KiB lhs loads per wave per step
   static constexpr int B_LOADS = BN / 16 / WAVES;            // 1 KiB weight loads per wave per step
   static constexpr int S_LOADS = 1;                          // 256-byte scale loads per wave per step
   static constexpr int LOADS = A_LOADS + B_LOADS + S_LOADS;
   static_assert(A_LOADS * WAVES * 1024 == BM * A_ROW && B_LOADS * WAVES * 16 == BN, "loads split over the waves");
-  static_assert(!A8 || WAVES * 64 >= BM / 64 * 64 + 64, "row and weight scales fit one load per wave");
+  static_assert(!A8 || SX_LOADS * WAVES * 8 == BM, "row-scale loads split over the waves");
   static_assert(BN == 128, "one 128-column weight-scale block per tile");
 };
 
@@ -392,7 +399,7 @@ __global__ __launch_bounds__(C::THREADS) void dense_fp8_mfma_kernel(
     const void *__restrict__ xin, const float *__restrict__ sx, int64_t M, int K, int N,
     const uint8_t *__restrict__ wpk, const float *__restrict__ sw, int sw_ld, int ksplit, uint16_t *__restrict__ out,
     float *__restrict__ partial) {
-  __shared__ __attribute__((aligned(1024))) uint8_t s_lds[NS * C::STAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t s_lds[NS * C::STAGE + C::SX_BYTES];
   // The wave index is made wave-uniform, so that every load address below
   // is a scalar base plus a per-lane 32-bit offset (no per-step vector
   // address arithmetic) and the LDS destinations are scalar.
@@ -432,25 +439,31 @@ __global__ __launch_bounds__(C::THREADS) void dense_fp8_mfma_kernel(
     woff[i] = (uint32_t)nb * (uint32_t)KB * 2048u + (uint32_t)(lane ^ ((lane >> 4) & 1)) * 16u;
   }
   // scales: W8A16 wave w loads columns n0 + 64 w + lane of sw[kb]; W8A8
-  // waves < BM/64 load rows row0 + 64 w + lane of sx[., kb], the others
-  // sw[kb, n0/128 + lane - ...] (only the first value is used).
-  __amdgpu_buffer_rsrc_t srsrc;
-  uint32_t slane, sstride;  // bytes: per-lane offset, per K block
-  if (!A8) {
-    srsrc = make_rsrc(sw, (uint32_t)KB * (uint32_t)sw_ld * 4u);
-    slane = (uint32_t)min(n0 + 64 * wave + lane, N - 1) * 4u;
-    sstride = (uint32_t)sw_ld * 4u;
-  } else if (wave < C::BM / 64) {
-    int64_t r = row0 + 64 * wave + lane;
-    if (r >= M) r = M - 1;
-    srsrc = make_rsrc(sx, (uint32_t)(M * KB * 4));
-    slane = (uint32_t)(r * KB) * 4u;
-    sstride = 4;
-  } else {
-    srsrc = make_rsrc(sw, (uint32_t)KB * (uint32_t)sw_ld * 4u);
-    slane = (uint32_t)(n0 / 128) * 4u;
-    sstride = (uint32_t)sw_ld * 4u;
+  // every wave loads sw[kb, n0/128] (all lanes the one value).
+  const __amdgpu_buffer_rsrc_t srsrc = make_rsrc(sw, (uint32_t)KB * (uint32_t)sw_ld * 4u);
+  const uint32_t slane = A8 ? (uint32_t)(n0 / 128) * 4u : (uint32_t)min(n0 + 64 * wave + lane, N - 1) * 4u;
+  const uint32_t sstride = (uint32_t)sw_ld * 4u;  // bytes per K block
+  // W8A8 row scales: load i of this wave covers block rows 8 (wave + WAVES i)
+  // .. + 7, lane l row + l / 8, K block kb0 + 8 c + l % 8 of chunk c (rows
+  // past M repeat the last row; K blocks past the block's run are unused).
+  __amdgpu_buffer_rsrc_t xrsrc;
+  uint32_t xoff[C::SX_LOADS > 0 ? C::SX_LOADS : 1];
+  if constexpr (A8) {
+    xrsrc = make_rsrc(sx, (uint32_t)(M * KB * 4));
+#pragma unroll
+    for (int i = 0; i < C::SX_LOADS; ++i) {
+      int64_t r = row0 + 8 * (wave + C::WAVES * i) + (lane >> 3);
+      if (r >= M) r = M - 1;
+      xoff[i] = (uint32_t)(r * KB) * 4u + (uint32_t)(lane & 7) * 4u;
+    }
   }
+  uint8_t *const s_sx = s_lds + NS * C::STAGE;
+  auto issue_sx = [&](int c) {  // row scales of K blocks kb0 + 8 c .. + 7 into buffer c % 2
+#pragma unroll
+    for (int i = 0; i < C::SX_LOADS; ++i)
+      buffer_load_lds(4, xrsrc, s_sx + (c & 1) * C::SX_BUF + (wave + C::WAVES * i) * 256, xoff[i],
+                      (uint32_t)(kb0 + 8 * c) * 4u);
+  };
   auto issue = [&](int stage, int t) {
     uint8_t *const st = s_lds + stage * C::STAGE;
     const uint32_t kb = (uint32_t)(kb0 + (t >> 1)), half = (uint32_t)(t & 1);
@@ -478,7 +491,11 @@ __global__ __launch_bounds__(C::THREADS) void dense_fp8_mfma_kernel(
   // barrier of step t also waits for step t + 1 to land.
   constexpr int PENDING = C::LOADS * (NS - (PF ? 3 : 2));
   static_assert(PENDING >= 0 && PENDING < 64, "vmcnt range");
+  // W8A8: row-scale chunk c + 1 is issued with step 16 c's loads, so every
+  // wait for a later step (at least PENDING younger loads) covers it; the
+  // buffer it fills was last read in the fold of step 16 c - 1.
   if (T > 0) {
+    if constexpr (A8) issue_sx(0);
 #pragma unroll
     for (int t = 0; t < NS - 1; ++t) issue(t, min(t, T - 1));
   }
@@ -580,6 +597,9 @@ __global__ __launch_bounds__(C::THREADS) void dense_fp8_mfma_kernel(
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
       // Every wave is done with step t + hs - 1: refill its stage.
+      if constexpr (A8) {
+        if (hs == 0 && ((t >> 1) & 7) == 0 && t + 16 < T) issue_sx((t >> 4) + 1);
+      }
       issue(cur == 0 ? NS - 1 : cur - 1, min(t + hs + NS - 1, T - 1));
       const uint8_t *const st = s_lds + cur * C::STAGE;
       const int nxt = cur == NS - 1 ? 0 : cur + 1;
@@ -641,16 +661,16 @@ __global__ __launch_bounds__(C::THREADS) void dense_fp8_mfma_kernel(
               for (int r = 0; r < 16; ++r) acc[i][j][r] = __builtin_fmaf(part[i][j][r], sc, acc[i][j][r]);
           }
         } else {
-          const float swv = *(const float *)(st + C::S + (C::BM / 64) * 256);
+          const float swv = *(const float *)(st + C::S);
+          // sx[row, kb] of block row r at s_sx[(kb - kb0) / 8 % 2][r][(kb - kb0) % 8]
+          const float *const xs = (const float *)(s_sx + ((t >> 4) & 1) * C::SX_BUF) + ((t >> 1) & 7);
 #pragma unroll
           for (int i = 0; i < 2; ++i) {
             float f[16];
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-              const f32x4_t v = *(const f32x4_t *)(st + C::S + (rA[i] - c32 + 8 * g + 4 * h) * 4);
+            for (int g = 0; g < 4; ++g)
 #pragma unroll
-              for (int q = 0; q < 4; ++q) f[4 * g + q] = v[q] * swv;
-            }
+              for (int q = 0; q < 4; ++q) f[4 * g + q] = xs[(rA[i] - c32 + 8 * g + 4 * h + q) * 8] * swv;
 #pragma unroll
             for (int j = 0; j < 2; ++j)
 #pragma unroll
