@@ -352,43 +352,47 @@ __global__ __launch_bounds__(64 * KS) void dense_fp8_skinny_kernel(
 // NS LDS stages with direct global -> LDS loads (the only vector-memory
 // operations in the loop, so the waits are exact counts), one barrier per
 // step.  W8A16 decodes the e4m3 weights to bf16 (exact) and runs bf16 MFMA
-// 32x32x16; W8A8 runs the fp8 MFMA 32x32x64 on the codes.  Each 128-deep K
-// block's partial sum is scaled once into the f32 accumulator
-// (acc = fma(part, scale, acc)).
+// 32x32x16, 64 K per step; W8A8 runs the fp8 MFMA 32x32x64 on the codes, a
+// whole 128-deep K block per step.  Each K block's partial sum is scaled once
+// into the f32 accumulator (acc = fma(part, scale, acc)).
 //
-// Stage layout: lhs rows of 128 bytes (bf16) or 64 bytes (e4m3), their
-// 16-byte chunks swizzled (chunk c of row r at c ^ ((r >> 1) & 7), or
-// c ^ ((r >> 2) & 3) for 64-byte rows) so that a fragment read by 16 lanes
-// of consecutive rows hits distinct bank groups; then BN/16 weight chunks of
-// 1 KiB (the half of a prepacked 2 KiB chunk that covers the step: 16-byte
-// slot 32 q + 2 c + p holds k = 32 q + 16 p .. + 15 of column c), stored
-// with p flipped for c >= 8 (lane l loads slot l ^ ((l >> 4) & 1)), so that
-// 16 lanes reading one slot of 16 consecutive columns hit distinct bank
-// groups; then the scales: W8A16 the block's column scales of the step's K
-// block, W8A8 sw[kb, n0/128] (every wave loads it, so each wave issues the
-// same loads per step).  W8A8's row scales sit outside the ring: every 8 K
-// blocks the waves load sx[row0 .. + BM - 1, the next 8 K blocks] into one
-// of two [BM][8] f32 buffers, 8 rows of 32 contiguous bytes per load (a
-// column of sx read per step would touch one line per row).
+// Stage layout: lhs rows of 128 bytes (64 K of bf16, or 128 K of e4m3: every
+// lhs load takes whole 128-byte lines), their 16-byte chunks swizzled (chunk
+// c of row r at c ^ ((r >> 1) & 7)) so that a fragment read by 16 lanes of
+// consecutive rows hits distinct bank groups; then per 16 columns the 1 KiB
+// halves of the prepacked 2 KiB chunk that the step covers (W8A16 one, W8A8
+// both; in a half, 16-byte slot 32 q + 2 c + p holds k = 32 q + 16 p .. + 15
+// of column c), stored with p flipped for c >= 8 (lane l loads slot
+// l ^ ((l >> 4) & 1)), so that 16 lanes reading one slot of 16 consecutive
+// columns hit distinct bank groups; then the scales: W8A16 the block's
+// column scales of the step's K block, W8A8 sw[kb, n0/128] (every wave loads
+// it, so each wave issues the same loads per step).  W8A8's row scales sit
+// outside the ring: every SX_KB K blocks the waves load sx[row0 .. + BM - 1,
+// the next SX_KB K blocks] into one of two [BM][SX_KB] f32 buffers, rows of
+// 4 * SX_KB contiguous bytes (a column of sx read per step would touch one
+// line per row).
 template <int WM, int WN, bool A8>
 struct DenseMfmaCfg {
   static constexpr int WAVES = WM * WN, THREADS = 64 * WAVES, WCOLS = WN;
   static constexpr int BM = 64 * WM, BN = 64 * WN;
-  static constexpr int A_ROW = A8 ? 64 : 128;
+  static constexpr int A_ROW = 128;            // lhs bytes per row per step: 64 K of bf16 or 128 K of e4m3
+  static constexpr int W_STEP = A8 ? 2048 : 1024;  // weight bytes per 16 columns per step
   static constexpr int A = 0;
   static constexpr int B = BM * A_ROW;
-  static constexpr int S = B + BN * 64;
+  static constexpr int S = B + BN / 16 * W_STEP;
   static constexpr int S_BYTES = WAVES * 256;  // one 64-value scale load per wave
   static constexpr int STAGE = (S + S_BYTES + 1023) / 1024 * 1024;
-  static constexpr int SX_BUF = BM * 8 * 4;                        // W8A8: [BM rows][8 K blocks] f32
+  static constexpr int SX_KB = BM == 256 ? 4 : 8;                  // W8A8: K blocks per row-scale chunk
+  static constexpr int SX_BUF = BM * SX_KB * 4;                    // [BM rows][SX_KB] f32
   static constexpr int SX_BYTES = A8 ? 2 * SX_BUF : 0;
-  static constexpr int SX_LOADS = A8 ? BM / 8 / WAVES : 0;         // 8-row loads per wave per 8 K blocks
-  static constexpr int A_LOADS = BM * A_ROW / 1024 / WAVES;  // 1 KiB lhs loads per wave per step
-  static constexpr int B_LOADS = BN / 16 / WAVES;            // 1 KiB weight loads per wave per step
-  static constexpr int S_LOADS = 1;                          // 256-byte scale loads per wave per step
+  static constexpr int SX_LOADS = A8 ? SX_BUF / 256 / WAVES : 0;   // 256-byte loads per wave per chunk
+  static constexpr int A_LOADS = BM * A_ROW / 1024 / WAVES;        // 1 KiB lhs loads per wave per step
+  static constexpr int B_LOADS = BN / 16 * W_STEP / 1024 / WAVES;  // 1 KiB weight loads per wave per step
+  static constexpr int S_LOADS = 1;                                // 256-byte scale loads per wave per step
   static constexpr int LOADS = A_LOADS + B_LOADS + S_LOADS;
-  static_assert(A_LOADS * WAVES * 1024 == BM * A_ROW && B_LOADS * WAVES * 16 == BN, "loads split over the waves");
-  static_assert(!A8 || SX_LOADS * WAVES * 8 == BM, "row-scale loads split over the waves");
+  static_assert(A_LOADS * WAVES * 1024 == BM * A_ROW && B_LOADS * WAVES * 1024 == BN / 16 * W_STEP,
+                "loads split over the waves");
+  static_assert(!A8 || (SX_LOADS * WAVES * 256 == SX_BUF && WAVES % 2 == 0), "row-scale loads split over the waves");
   static_assert(BN == 128, "one 128-column weight-scale block per tile");
 };
 
@@ -410,70 +414,76 @@ __global__ __launch_bounds__(C::THREADS) void dense_fp8_mfma_kernel(
   const int kb_per = (KB + ksplit - 1) / ksplit;
   const int kb0 = blockIdx.z * kb_per;
   const int nkb = max(0, min(KB, kb0 + kb_per) - kb0);
-  const int T = 2 * nkb;  // 64-deep steps of this block
+  const int T = A8 ? nkb : 2 * nkb;  // steps of this block (W8A8 128 K deep, W8A16 64 K)
   const int64_t row0 = (int64_t)blockIdx.y * C::BM;
   const int n0 = blockIdx.x * C::BN;
   const int wm = wave / C::WCOLS, wn = wave % C::WCOLS;
   // ---- load addressing (per lane, per step t) ----
-  // lhs: load i of this wave covers rows 8 (or 16) * (wave + WAVES * i) ..;
-  // lane l fills physical chunk l % 8 (l % 4) of its row with the logical
-  // chunk of the swizzle.
-  constexpr int RPL = A8 ? 16 : 8;  // rows per 1 KiB load
+  // lhs: load i of this wave covers rows 8 (wave + WAVES i) .. + 7; lane l
+  // fills physical chunk l % 8 of row + l / 8 with the logical chunk of the
+  // swizzle.
   uint32_t aoff[C::A_LOADS];
 #pragma unroll
   for (int i = 0; i < C::A_LOADS; ++i) {
-    const int r = RPL * (wave + C::WAVES * i) + (A8 ? (lane >> 2) : (lane >> 3));
+    const int r = 8 * (wave + C::WAVES * i) + (lane >> 3);
     int64_t gr = row0 + r;
     if (gr >= M) gr = M - 1;
-    const int pc = A8 ? (lane & 3) : (lane & 7);
-    const int lc = A8 ? (pc ^ ((r >> 2) & 3)) : (pc ^ ((r >> 1) & 7));
+    const int lc = (lane & 7) ^ ((r >> 1) & 7);
     aoff[i] = (uint32_t)(gr * (int64_t)K * (A8 ? 1 : 2)) + (uint32_t)lc * 16u;
   }
   const __amdgpu_buffer_rsrc_t arsrc = make_rsrc(xin, (uint32_t)(M * K * (A8 ? 1 : 2)));
   const __amdgpu_buffer_rsrc_t wrsrc = make_rsrc(wpk, (uint32_t)((int64_t)K * N));
+  // weights: load i of this wave fills 1 KiB slot g = wave + WAVES i of the
+  // stage's weight region: W8A16 the step's half of 16-column group g, W8A8
+  // half g % 2 of group g / 2.
   uint32_t woff[C::B_LOADS];
 #pragma unroll
   for (int i = 0; i < C::B_LOADS; ++i) {
-    int nb = n0 / 16 + wave + C::WAVES * i;
+    const int g = wave + C::WAVES * i;
+    int nb = n0 / 16 + (A8 ? g >> 1 : g);
     if (nb >= N16) nb = N16 - 1;
-    woff[i] = (uint32_t)nb * (uint32_t)KB * 2048u + (uint32_t)(lane ^ ((lane >> 4) & 1)) * 16u;
+    woff[i] = (uint32_t)nb * (uint32_t)KB * 2048u + (A8 ? (uint32_t)(g & 1) * 1024u : 0u) +
+              (uint32_t)(lane ^ ((lane >> 4) & 1)) * 16u;
   }
   // scales: W8A16 wave w loads columns n0 + 64 w + lane of sw[kb]; W8A8
   // every wave loads sw[kb, n0/128] (all lanes the one value).
   const __amdgpu_buffer_rsrc_t srsrc = make_rsrc(sw, (uint32_t)KB * (uint32_t)sw_ld * 4u);
   const uint32_t slane = A8 ? (uint32_t)(n0 / 128) * 4u : (uint32_t)min(n0 + 64 * wave + lane, N - 1) * 4u;
   const uint32_t sstride = (uint32_t)sw_ld * 4u;  // bytes per K block
-  // W8A8 row scales: load i of this wave covers block rows 8 (wave + WAVES i)
-  // .. + 7, lane l row + l / 8, K block kb0 + 8 c + l % 8 of chunk c (rows
-  // past M repeat the last row; K blocks past the block's run are unused).
+  // W8A8 row scales: load i of this wave covers block rows XR (wave + WAVES i)
+  // .. + XR - 1 (XR = 64 / SX_KB), lane l row + l / SX_KB, K block
+  // kb0 + SX_KB c + l % SX_KB of chunk c (rows past M repeat the last row; K
+  // blocks past the block's run are never read).
+  constexpr int XR = 64 / C::SX_KB;
   __amdgpu_buffer_rsrc_t xrsrc;
   uint32_t xoff[C::SX_LOADS > 0 ? C::SX_LOADS : 1];
   if constexpr (A8) {
     xrsrc = make_rsrc(sx, (uint32_t)(M * KB * 4));
 #pragma unroll
     for (int i = 0; i < C::SX_LOADS; ++i) {
-      int64_t r = row0 + 8 * (wave + C::WAVES * i) + (lane >> 3);
+      int64_t r = row0 + XR * (wave + C::WAVES * i) + lane / C::SX_KB;
       if (r >= M) r = M - 1;
-      xoff[i] = (uint32_t)(r * KB) * 4u + (uint32_t)(lane & 7) * 4u;
+      xoff[i] = (uint32_t)(r * KB) * 4u + (uint32_t)(lane % C::SX_KB) * 4u;
     }
   }
   uint8_t *const s_sx = s_lds + NS * C::STAGE;
-  auto issue_sx = [&](int c) {  // row scales of K blocks kb0 + 8 c .. + 7 into buffer c % 2
+  auto issue_sx = [&](int c) {  // row scales of K blocks kb0 + SX_KB c .. into buffer c % 2
 #pragma unroll
     for (int i = 0; i < C::SX_LOADS; ++i)
       buffer_load_lds(4, xrsrc, s_sx + (c & 1) * C::SX_BUF + (wave + C::WAVES * i) * 256, xoff[i],
-                      (uint32_t)(kb0 + 8 * c) * 4u);
+                      (uint32_t)(kb0 + C::SX_KB * c) * 4u);
   };
   auto issue = [&](int stage, int t) {
     uint8_t *const st = s_lds + stage * C::STAGE;
-    const uint32_t kb = (uint32_t)(kb0 + (t >> 1)), half = (uint32_t)(t & 1);
-    const uint32_t astep = (uint32_t)(kb0 * 2 + t) * (A8 ? 64u : 128u);
+    const uint32_t kb = (uint32_t)(kb0 + (A8 ? t : t >> 1));
+    const uint32_t wstep = A8 ? kb * 2048u : kb * 2048u + (uint32_t)(t & 1) * 1024u;
+    const uint32_t astep = (uint32_t)((A8 ? kb0 : kb0 * 2) + t) * 128u;  // lhs bytes before the step
 #pragma unroll
     for (int i = 0; i < C::A_LOADS; ++i)
       buffer_load_lds(16, arsrc, st + C::A + (wave + C::WAVES * i) * 1024, aoff[i], astep);
 #pragma unroll
     for (int i = 0; i < C::B_LOADS; ++i)
-      buffer_load_lds(16, wrsrc, st + C::B + (wave + C::WAVES * i) * 1024, woff[i], kb * 2048u + half * 1024u);
+      buffer_load_lds(16, wrsrc, st + C::B + (wave + C::WAVES * i) * 1024, woff[i], wstep);
     buffer_load_lds(4, srsrc, st + C::S + wave * 256, slane, kb * sstride);
   };
   // ---- compute addressing ----
@@ -491,9 +501,12 @@ __global__ __launch_bounds__(C::THREADS) void dense_fp8_mfma_kernel(
   // barrier of step t also waits for step t + 1 to land.
   constexpr int PENDING = C::LOADS * (NS - (PF ? 3 : 2));
   static_assert(PENDING >= 0 && PENDING < 64, "vmcnt range");
-  // W8A8: row-scale chunk c + 1 is issued with step 16 c's loads, so every
-  // wait for a later step (at least PENDING younger loads) covers it; the
-  // buffer it fills was last read in the fold of step 16 c - 1.
+  static_assert(!A8 || (PF && NS - 1 <= C::SX_KB), "W8A8 prefetches its fragments; row-scale chunk timing");
+  // W8A8: row-scale chunk c + 1 is issued before step SX_KB c's refill, so
+  // it is older than the loads of every step from SX_KB (c + 1) on (issued
+  // at step SX_KB (c + 1) - NS + 1 or later) and the wait for such a step
+  // covers it; the buffer it fills was last read in the fold of step
+  // SX_KB c - 1.
   if (T > 0) {
     if constexpr (A8) issue_sx(0);
 #pragma unroll
@@ -550,12 +563,12 @@ __global__ __launch_bounds__(C::THREADS) void dense_fp8_mfma_kernel(
   struct Frag8 {
     i32x8_t a[2], b[2];
   };
-  auto read8 = [&](const uint8_t *st, Frag8 &f) {
+  auto read8 = [&](const uint8_t *st, int hs, Frag8 &f) {  // substep hs: k = 64 hs .. + 63 of the step
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int r = rA[i];
-      const u32x4_t lo = *(const u32x4_t *)(st + C::A + r * 64 + ((h ^ ((r >> 2) & 3)) * 16));
-      const u32x4_t hi = *(const u32x4_t *)(st + C::A + r * 64 + (((2 + h) ^ ((r >> 2) & 3)) * 16));
+      const u32x4_t lo = *(const u32x4_t *)(st + C::A + r * 128 + (((4 * hs + h) ^ ((r >> 1) & 7)) * 16));
+      const u32x4_t hi = *(const u32x4_t *)(st + C::A + r * 128 + (((4 * hs + 2 + h) ^ ((r >> 1) & 7)) * 16));
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         f.a[i][q] = (int)lo[q];
@@ -566,7 +579,7 @@ __global__ __launch_bounds__(C::THREADS) void dense_fp8_mfma_kernel(
     for (int j = 0; j < 2; ++j) {
       const int col = cB[j];
       const int c = col & 15;
-      const uint8_t *pc = st + C::B + (col >> 4) * 1024 + c * 32 + 16 * (h ^ (c >> 3));
+      const uint8_t *pc = st + C::B + (col >> 4) * 2048 + hs * 1024 + c * 32 + 16 * (h ^ (c >> 3));
       const u32x4_t lo = *(const u32x4_t *)pc;
       const u32x4_t hi = *(const u32x4_t *)(pc + 16 * 32);
 #pragma unroll
@@ -589,16 +602,19 @@ __global__ __launch_bounds__(C::THREADS) void dense_fp8_mfma_kernel(
   Frag16 f16;
   u32x4_t w16n[2][2];  // PF: the next step's weight codes
   Frag8 f8;
-  for (int t = 0; t < T; t += 2) {
+  // W8A16: pairs of 64-deep steps (t, t + 1), a K block per pair; W8A8: one
+  // step per K block.
+  constexpr int TS = A8 ? 1 : 2;
+  for (int t = 0; t < T; t += TS) {
 #pragma unroll
-    for (int hs = 0; hs < 2; ++hs) {
+    for (int hs = 0; hs < TS; ++hs) {
       __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(PENDING));
       asm volatile("" ::: "memory");
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
       // Every wave is done with step t + hs - 1: refill its stage.
       if constexpr (A8) {
-        if (hs == 0 && ((t >> 1) & 7) == 0 && t + 16 < T) issue_sx((t >> 4) + 1);
+        if (t % C::SX_KB == 0 && t + C::SX_KB < T) issue_sx(t / C::SX_KB + 1);
       }
       issue(cur == 0 ? NS - 1 : cur - 1, min(t + hs + NS - 1, T - 1));
       const uint8_t *const st = s_lds + cur * C::STAGE;
@@ -637,19 +653,25 @@ __global__ __launch_bounds__(C::THREADS) void dense_fp8_mfma_kernel(
           }
         }
       } else {
-        if constexpr (PF) {
-          if (t + hs == 0) read8(st, f8);
+        // Two 64-deep substeps; each reads the next one's fragments (after
+        // the second, the next step's first) during its MFMAs.
+        if (t == 0) read8(st, 0, f8);
+        {
           const Frag8 c = f8;
           __builtin_amdgcn_sched_barrier(0);
-          read8(sx, f8);
-          mma8(c, hs == 0);
+          read8(st, 1, f8);
+          mma8(c, true);
           __builtin_amdgcn_sched_barrier(0);
-        } else {
-          read8(st, f8);
-          mma8(f8, hs == 0);
+        }
+        {
+          const Frag8 c = f8;
+          __builtin_amdgcn_sched_barrier(0);
+          read8(sx, 0, f8);
+          mma8(c, false);
+          __builtin_amdgcn_sched_barrier(0);
         }
       }
-      if (hs == 1) {
+      if (A8 || hs == 1) {
         // The K block is complete: acc += part * scale.
         if constexpr (!A8) {
 #pragma unroll
@@ -662,15 +684,15 @@ __global__ __launch_bounds__(C::THREADS) void dense_fp8_mfma_kernel(
           }
         } else {
           const float swv = *(const float *)(st + C::S);
-          // sx[row, kb] of block row r at s_sx[(kb - kb0) / 8 % 2][r][(kb - kb0) % 8]
-          const float *const xs = (const float *)(s_sx + ((t >> 4) & 1) * C::SX_BUF) + ((t >> 1) & 7);
+          // sx[row, kb0 + t] of block row r at s_sx[t / SX_KB % 2][r][t % SX_KB]
+          const float *const xs = (const float *)(s_sx + ((t / C::SX_KB) & 1) * C::SX_BUF) + t % C::SX_KB;
 #pragma unroll
           for (int i = 0; i < 2; ++i) {
             float f[16];
 #pragma unroll
             for (int g = 0; g < 4; ++g)
 #pragma unroll
-              for (int q = 0; q < 4; ++q) f[4 * g + q] = xs[(rA[i] - c32 + 8 * g + 4 * h + q) * 8] * swv;
+              for (int q = 0; q < 4; ++q) f[4 * g + q] = xs[(rA[i] - c32 + 8 * g + 4 * h + q) * C::SX_KB] * swv;
 #pragma unroll
             for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -739,9 +761,10 @@ static void launch_dense(const void *x, const float *sx, int64_t M, int64_t K, i
 
 // MFMA path (M > 16, N % 128 == 0): W8A16 128x128 tiles (4 waves, two or
 // three 25 KB stages: two blocks per CU), 256x128 tiles (8 waves) when those
-// alone fill the grid; W8A8 256x128 tiles (8 waves, four 26 KB stages,
-// fragments read one step ahead) from M >= 256, 128x128 below.  K is split over blocks until the
-// grid covers the 256 CUs; the f32 partials go to the workspace and
+// alone fill the grid; W8A8 256x128 tiles (8 waves, three 50 KB stages of
+// one K block each, fragments read one substep ahead) from M >= 256, 128x128
+// below (four 33 KB stages).  K is split over blocks until the grid covers
+// the 256 CUs; the f32 partials go to the workspace and
 // dense_fp8_reduce_kernel adds them in split order (deterministic).
 static bool dense_mfma_ok(int64_t M, int64_t K, int64_t N) {
   return M > 16 && N % 128 == 0 && M * K * 2 < (1ll << 32) && K * N < (1ll << 32) && M / 128 < 65535;
@@ -767,9 +790,10 @@ static int launch_dense_mfma(const void *x, const float *sx, int64_t M, int64_t 
     partial = (float *)workspace;
   }
   if (A8 && M >= 256) {
+    // 50 KB stages: three fit beside the row-scale buffers.
     using C = DenseMfmaCfg<4, 2, true>;
     const dim3 grid((unsigned)(N / C::BN), (unsigned)((M + C::BM - 1) / C::BM), (unsigned)ks);
-    hipLaunchKernelGGL((dense_fp8_mfma_kernel<C, true, 4, true>), grid, dim3(C::THREADS), 0, st, x, sx, M, (int)K,
+    hipLaunchKernelGGL((dense_fp8_mfma_kernel<C, true, 3, true>), grid, dim3(C::THREADS), 0, st, x, sx, M, (int)K,
                        (int)N, w, sw, sw_ld, ks, out, partial);
   } else if (A8) {
     using C = DenseMfmaCfg<2, 2, true>;
