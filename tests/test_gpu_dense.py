@@ -40,7 +40,8 @@ def test_w8a16_small_shapes(dev, M, K, N):
 
 
 @pytest.mark.parametrize("M,K,N", [(1, 1024, 512), (16, 1024, 512), (33, 512, 256), (128, 1024, 512),
-                                   (257, 768, 384), (256, 512, 128), (600, 1024, 640)])
+                                   (257, 768, 384), (256, 512, 128), (600, 1024, 640),
+                                   (200, 5120, 4096)])  # the last: 10 K blocks per split, two row-scale chunks
 def test_w8a8_small_shapes(dev, M, K, N):
     from dw_tpu_amd.dense_fp8 import matmul_w8a8
     from dw_tpu_amd.workloads import make_dense_workload
