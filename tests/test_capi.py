@@ -156,3 +156,28 @@ def test_missing_library_is_loud(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "nope.so"))
     with pytest.raises(_lib.LibraryMissing):
         _lib.load()
+
+
+def test_last_error_is_per_thread():
+    import threading
+    lib = _lib.load()
+    null = None
+    # this thread fails an argument check ...
+    assert lib.dwm_gmm_fp4(null, 8, 192, null, null, null, 4, null, 4, 64, null, _lib.BF16, 0, 0, null) \
+        == _lib.ERR_UNSUPPORTED
+    mine = lib.dwm_last_error()
+    assert mine
+    seen = {}
+
+    def other():
+        seen["fresh"] = lib.dwm_last_error()
+        lib.dwm_gmm_fp4(null, 8, 128, null, null, null, 4, null, 4, 64, null, 7, 0, 0, null)  # bad dtype
+        seen["own"] = lib.dwm_last_error()
+
+    t = threading.Thread(target=other)
+    t.start()
+    t.join()
+    # ... another thread starts clean, sees only its own failure, and leaves ours alone
+    assert seen["fresh"] == b""
+    assert b"dtype" in seen["own"]
+    assert lib.dwm_last_error() == mine
