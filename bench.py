@@ -487,6 +487,8 @@ def main():
     log("bench: decode_gate_up gmm")
     wl, b, ms = bench_gmm("decode_gate_up", dev, args.steps, args.warmup)
     main_res = gmm_result(wl, ms)
+    # Spread: 7 more samples of the same K steps, right after the timed ones.
+    samples = sorted(time_steps(b.step, args.steps, 0) for _ in range(7))
     e_chk = int(np.flatnonzero(wl.group_sizes > 0)[0])
     r0 = int(wl.group_sizes[:e_chk].sum())
     gpu_check = (e_chk, b.out[0][r0:r0 + int(wl.group_sizes[e_chk])].float().cpu().numpy())
@@ -533,7 +535,9 @@ def main():
         "config": {"workload": "decode_gate_up: 32 local experts, 256 tokens x top-8 (M=2048 routed rows, 4 empty "
                                "experts), K=7168, N=4096, fp4 e2m1 weights with e8m0 block-32 scales, bf16 out",
                    "TFLOP_s": main_res["TFLOP_s"], "mfma_bf16_frac": main_res["mfma_bf16_frac"],
-                   "bytes_per_step": main_res["bytes"], "flops_per_step": main_res["flops"]},
+                   "bytes_per_step": main_res["bytes"], "flops_per_step": main_res["flops"],
+                   "ms_per_step_7_samples": {"median": round(samples[3], 5), "min": round(samples[0], 5),
+                                             "max": round(samples[-1], 5)}},
         "roofline": {"bound": "hbm", "achieved": main_res["GB_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": main_res["hbm_frac"], "traffic": profiled_traffic()},
         "cpu_baseline": cpu,
