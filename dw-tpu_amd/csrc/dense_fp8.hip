@@ -8,9 +8,14 @@
 // weights with 128x128 block f32 scales sw:
 // acc += part * (sx[m, kb] * sw[kb, n / 128]).
 //
-// Both run on bf16 MFMA 16x16x32: e4m3 -> bf16 is exact (3 mantissa bits,
-// exponents inside bf16's range), so every product equals the fp8 product and
-// the 128-K partial is an f32 sum of exact products.
+// Kernels:
+// - M > 16, N % 128 == 0: dense_fp8_mfma_kernel.  W8A16 decodes e4m3 -> bf16
+//   (exact: 3 mantissa bits, exponents inside bf16's range) for bf16 MFMA
+//   32x32x16; W8A8 runs the fp8 MFMA 32x32x64 on the codes.
+// - M <= 16: dense_fp8_skinny_kernel (see below).
+// - Other shapes: dense_fp8_kernel, bf16 MFMA 16x16x32 on decoded codes.
+// Every product is the exact fp8 (or bf16 x fp8) product; the 128-K partial
+// is an f32 sum of them.
 //
 // Prepacked weight layout (load time, dwm_dense_fp8_prepack):
 //   w[(nb * K/128 + kb) * 2048 + lane * 32 + j], lane = 16*q + c,
