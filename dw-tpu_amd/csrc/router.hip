@@ -6,7 +6,8 @@
 // One wavefront per token: lane l holds experts l, l + 64, ... (coalesced
 // loads of the logits row), the scores are computed in registers, and the
 // top-k runs as k wave-wide arg-max rounds (larger key first, then the lower
-// expert id, as lax.top_k orders ties) over one 64-bit word per candidate.
+// expert id, as lax.top_k orders ties): a 32-bit max of the keys, then a
+// ballot per slot for the lowest id holding it.
 // Lane j keeps result j, so the outputs are written by lanes 0 .. k-1
 // without a staging buffer.
 #include "common.h"
@@ -49,37 +50,24 @@ __device__ __forceinline__ float wave_sum_f32(float v) {
 }
 
 // Selection order: a larger key first, then the lower expert id (lax.top_k's
-// tie order).  Each candidate is one 64-bit word that orders that way as an
-// unsigned integer: the key's bits made monotone (flip all bits of a
-// negative, set the sign bit of a non-negative) above the inverted expert id.
-// A taken expert is 0 and loses to every candidate; a NaN key ranks below
-// every number (ties by id).  -0 is folded into +0 first, as the float
-// comparison treats them as equal.
-__device__ __forceinline__ uint64_t select_word(float key, int e) {
+// tie order).  A candidate's key is its score's bits made monotone as an
+// unsigned integer (flip all bits of a negative, set the sign bit of a
+// non-negative); -0 is folded into +0 first, as the float comparison treats
+// them as equal.  Every number then maps to at least 0x007FFFFF (-inf), a
+// NaN to 1 (below every number; NaNs tie by id), and a taken expert or a
+// lane past E holds 0 and loses to every candidate.
+__device__ __forceinline__ uint32_t select_key(float key) {
   uint32_t b = __builtin_bit_cast(uint32_t, key == 0.0f ? 0.0f : key);
   b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-  if (key != key) b = 0u;
-  return ((uint64_t)b << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)e);
+  return key != key ? 1u : b;
 }
 
-template <int CTRL>
-__device__ __forceinline__ uint64_t max_dpp_u64(uint64_t v) {
-  const uint64_t o = ((uint64_t)dpp_u32<CTRL>((uint32_t)(v >> 32)) << 32) | dpp_u32<CTRL>((uint32_t)v);
-  return o > v ? o : v;
-}
-
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-  v = max_dpp_u64<kDppXor1>(v);
-  v = max_dpp_u64<kDppXor2>(v);
-  v = max_dpp_u64<kDppHalfMirror>(v);
-  v = max_dpp_u64<kDppMirror>(v);
-  uint64_t r = 0;
-#pragma unroll
-  for (int row = 0; row < 4; ++row) {
-    const uint64_t o = ((uint64_t)lane_u32((uint32_t)(v >> 32), 16 * row) << 32) | lane_u32((uint32_t)v, 16 * row);
-    r = o > r ? o : r;
-  }
-  return r;
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, dpp_u32<kDppXor1>(v));
+  v = max(v, dpp_u32<kDppXor2>(v));
+  v = max(v, dpp_u32<kDppHalfMirror>(v));
+  v = max(v, dpp_u32<kDppMirror>(v));
+  return max(max(lane_u32(v, 0), lane_u32(v, 16)), max(lane_u32(v, 32), lane_u32(v, 48)));
 }
 
 template <int VPL>
@@ -125,11 +113,11 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const void *__restrict_
 #pragma unroll
     for (int i = 0; i < VPL; ++i) p[i] = sqrtf(fmaxf(x[i], 0.0f) + log1pf(expf(-fabsf(x[i]))));
   }
-  uint64_t cand[VPL];  // 0 once taken (or for lanes past E)
+  uint32_t cand[VPL];  // selection key of expert lane + 64 i; 0 once taken (or past E)
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
     const int e = lane + 64 * i;
-    cand[i] = e < E ? select_word(bias != nullptr ? p[i] + bias[e] : p[i], e) : 0ull;
+    cand[i] = e < E ? select_key(bias != nullptr ? p[i] + bias[e] : p[i]) : 0u;
   }
   float my_w = 0.0f;  // result j = lane
   int my_id = 0;
@@ -148,21 +136,33 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const void *__restrict_
     }
   } else {
     for (int j = 0; j < topk; ++j) {
-      uint64_t best = cand[0];
+      // The largest key (wave-uniform), then its lowest expert id: experts
+      // of slot i are lane + 64 i, so the first slot holding it wins, and
+      // in that slot the lowest lane.  topk <= E, so a candidate is left.
+      uint32_t best = cand[0];
 #pragma unroll
-      for (int i = 1; i < VPL; ++i) best = cand[i] > best ? cand[i] : best;
-      best = wave_max_u64(best);
-      // Every lane now holds the winner; its owner (lane id % 64) marks it
-      // taken and hands over its unbiased weight.
-      const int id = (int)(0xFFFFFFFFu - (uint32_t)best);
-      const int slot = id >> 6;
+      for (int i = 1; i < VPL; ++i) best = max(best, cand[i]);
+      best = wave_max_u32(best);
+      int slot = 0;
+      uint64_t hit = 0;
+#pragma unroll
+      for (int i = VPL - 1; i >= 0; --i) {
+        const uint64_t b = __ballot(cand[i] == best);
+        if (b != 0) {
+          slot = i;
+          hit = b;
+        }
+      }
+      const int owner = __ffsll((long long)hit) - 1;
+      const int id = owner + 64 * slot;
+      // The owner marks it taken and hands over its unbiased weight.
       float v = 0.0f;
 #pragma unroll
       for (int i = 0; i < VPL; ++i) v = slot == i ? p[i] : v;
-      v = __builtin_bit_cast(float, lane_u32(__builtin_bit_cast(uint32_t, v), id & 63));
-      if (lane == (id & 63)) {
+      v = __builtin_bit_cast(float, lane_u32(__builtin_bit_cast(uint32_t, v), owner));
+      if (lane == owner) {
 #pragma unroll
-        for (int i = 0; i < VPL; ++i) cand[i] = slot == i ? 0ull : cand[i];
+        for (int i = 0; i < VPL; ++i) cand[i] = slot == i ? 0u : cand[i];
       }
       if (lane == j) {
         my_w = v;
