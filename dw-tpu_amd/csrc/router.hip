@@ -83,14 +83,17 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const void *__restrict_
   if (t >= T) return;
   float p[VPL];
   float x[VPL];
+  float bv[VPL];  // the correction bias, loaded with the logits (one memory round trip)
   float m = -__builtin_inff();
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
     const int e = lane + 64 * i;
     float v = -__builtin_inff();
+    bv[i] = 0.0f;
     if (e < E) {
       v = logits_bf16 ? bf16_bits_to_f32(((const uint16_t *)logits)[t * E + e])
                       : ((const float *)logits)[t * E + e];
+      if (bias != nullptr) bv[i] = bias[e];
     }
     x[i] = v;
     m = fmaxf(m, v);
@@ -117,7 +120,7 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const void *__restrict_
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
     const int e = lane + 64 * i;
-    cand[i] = e < E ? select_key(bias != nullptr ? p[i] + bias[e] : p[i]) : 0u;
+    cand[i] = e < E ? select_key(bias != nullptr ? p[i] + bv[i] : p[i]) : 0u;
   }
   float my_w = 0.0f;  // result j = lane
   int my_id = 0;
