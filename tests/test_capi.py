@@ -181,3 +181,22 @@ def test_last_error_is_per_thread():
     assert seen["fresh"] == b""
     assert b"dtype" in seen["own"]
     assert lib.dwm_last_error() == mine
+
+
+@pytest.mark.parametrize("compiler,std", [("gcc", "-std=c99"), ("g++", "-std=c++11")])
+def test_header_is_plain_c(tmp_path, compiler, std):
+    """include/dwtpu_moe.h is a C header (no torch or HIP types): it compiles
+    as strict C99 and as C++, and a C program can link against the library."""
+    import shutil
+    import subprocess
+    if shutil.which(compiler) is None:
+        pytest.skip(f"{compiler} not installed")
+    src = tmp_path / "use.c"
+    src.write_text('#include "dwtpu_moe.h"\nint main(void) { return dwm_version() > 0 ? 0 : 1; }\n')
+    cmd = [compiler, std, "-Wall", "-Wextra", "-Werror", "-I", os.path.dirname(HEADER)]
+    if compiler == "gcc":  # C: compile and link
+        cmd += ["-pedantic", str(src), "-o", str(tmp_path / "use"), _lib.LIB_PATH]
+    else:  # C++: the same header compiles
+        cmd += ["-fsyntax-only", "-x", "c++", str(src)]
+    r = subprocess.run(cmd, capture_output=True, timeout=120)
+    assert r.returncode == 0, r.stderr.decode(errors="replace")
