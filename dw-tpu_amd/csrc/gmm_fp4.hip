@@ -211,7 +211,9 @@ __device__ __forceinline__ float silu_mul_clamp(float gate, float up) {
   return g / (1.0f + expf(-g)) * u;
 }
 
-// Stores 8 consecutive output values of one row (16-byte bf16 or 2 x 16-byte f32 stores).
+// Stores 8 consecutive output values of one row (16-byte bf16 or 2 x 16-byte f32
+// stores), as streaming (non-temporal) vector stores: the output is read back
+// only by a later kernel.
 __device__ __forceinline__ void store8(void *__restrict__ out, int64_t o, const float *v, int out_f32) {
   if (out_f32) {
     u32x4_t lo, hi;
@@ -220,14 +222,14 @@ __device__ __forceinline__ void store8(void *__restrict__ out, int64_t o, const 
       lo[i] = __builtin_bit_cast(uint32_t, v[i]);
       hi[i] = __builtin_bit_cast(uint32_t, v[4 + i]);
     }
-    *(u32x4_t *)((float *)out + o) = lo;
-    *(u32x4_t *)((float *)out + o + 4) = hi;
+    __builtin_nontemporal_store(lo, (u32x4_t *)((float *)out + o));
+    __builtin_nontemporal_store(hi, (u32x4_t *)((float *)out + o + 4));
   } else {
     u32x4_t p;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       p[i] = (uint32_t)f32_to_bf16_bits(v[2 * i]) | ((uint32_t)f32_to_bf16_bits(v[2 * i + 1]) << 16);
-    *(u32x4_t *)((uint16_t *)out + o) = p;
+    __builtin_nontemporal_store(p, (u32x4_t *)((uint16_t *)out + o));
   }
 }
 
