@@ -407,7 +407,7 @@ __global__ __launch_bounds__(256) void mxfp4_requant_tile_kernel(const uint8_t *
     const int row = 32 * p + (t >> 3), ch = t & 7;
     const u32x4_t v = *(const u32x4_t *)&s_out[(row >> 5) * KBW + (row & 31) * 32 + ch * 4];
     const int64_t colbyte = interleave ? (ch < 4 ? 0 : N / 4) + (n0 / 2) / 2 + (ch & 3) * 16 : n0 / 2 + ch * 16;
-    *(u32x4_t *)(codes_out + (e * K + k0 + row) * (N / 2) + colbyte) = v;
+    __builtin_nontemporal_store(v, (u32x4_t *)(codes_out + (e * K + k0 + row) * (N / 2) + colbyte));
   }
   // 8 rows of 256 scale codes, 16 lanes per row.
   if (t < 128) {

@@ -214,7 +214,7 @@ __global__ __launch_bounds__(256) void row_gather_kernel(const char *src, int64_
     const int64_t s = gather_index(idx[r], src_rows);
     const V *sp = (const V *)(src + s * row_bytes);
     V *dp = (V *)(out + r * row_bytes);
-    for (int64_t i = threadIdx.x; i < nv; i += blockDim.x) dp[i] = sp[i];
+    for (int64_t i = threadIdx.x; i < nv; i += blockDim.x) __builtin_nontemporal_store(sp[i], dp + i);
   }
 }
 
