@@ -738,16 +738,19 @@ __global__ void dense_fp8_reduce_kernel(const float *partial, int ksplit, int64_
   }
 }
 
-struct DensePlan {
-  int mb, nbw, ksplit;
-};
+// ---------------------------------------------------------------------------
+// Launch plans.  A dwm_dense_plan names one launch: the kernel family, its
+// block tile, the number of K runs that share an output tile (blocks that
+// write f32 partials summed in run order by dense_fp8_reduce_kernel, or the
+// skinny kernel's waves) and the ring depth.  default_plan() is the library's
+// own choice; check_plan() admits exactly the instantiated configurations.
 
-static DensePlan dense_plan(int64_t M, int64_t K, int64_t N) {
-  DensePlan p;
-  if (M <= 16) p = {1, 1, 0};
-  else if (M <= 64) p = {4, 2, 0};
-  else p = {8, 2, 0};
-  const int64_t tiles = ((N / 16 + p.nbw * 4 - 1) / (p.nbw * 4)) * ((M + 16 * p.mb - 1) / (16 * p.mb));
+// Tiled kernel (any N % 16 == 0): 16 MB rows x 64 NBW columns.
+static dwm_dense_plan tiled_default(int64_t M, int64_t K, int64_t N) {
+  dwm_dense_plan p{DWM_DENSE_TILED, 128, 128, 1, 2};
+  if (M <= 16) p.tile_m = 16, p.tile_n = 64;
+  else if (M <= 64) p.tile_m = 64;
+  const int64_t tiles = ((N + p.tile_n - 1) / p.tile_n) * ((M + p.tile_m - 1) / p.tile_m);
   const int64_t KB = K / 128;
   int ks = 1;
   while (tiles * ks < 512 && ks * 2 <= KB && ks < 16) ks *= 2;  // fill the 256 CUs twice over
@@ -755,8 +758,105 @@ static DensePlan dense_plan(int64_t M, int64_t K, int64_t N) {
   return p;
 }
 
+// MFMA path (M > 16, N % 128 == 0): W8A16 128x128 tiles (4 waves, two or
+// three 25 KB stages: two blocks per CU), 256x128 tiles (8 waves) when those
+// alone fill the grid; W8A8 256x128 tiles (8 waves, three 50 KB stages of
+// one K block each, fragments read one substep ahead) from M >= 256, 128x128
+// below (four 33 KB stages).  K is split over blocks until the grid covers
+// the 256 CUs.
+static bool dense_mfma_ok(int64_t M, int64_t K, int64_t N, int tile_m) {
+  return M > 16 && N % 128 == 0 && M * K * 2 < (1ll << 32) && K * N < (1ll << 32) &&
+         (M + tile_m - 1) / tile_m <= 65535;
+}
+
+// Smallest run count with the same runs: no run is left empty.
+static int whole_runs(int64_t KB, int ks) {
+  const int64_t per = (KB + ks - 1) / ks;
+  return (int)((KB + per - 1) / per);
+}
+
+static dwm_dense_plan default_plan(int64_t M, int64_t K, int64_t N, bool a8) {
+  const int64_t KB = K / 128;
+  if (dense_mfma_ok(M, K, N, 128)) {
+    const int tm = (a8 && M >= 256) ? 256 : 128;
+    const int64_t tiles = (N / 128) * ((M + tm - 1) / tm);
+    int ks = 1;
+    while (tiles * ks < 256 && ks * 2 <= KB && ks < 16) ks *= 2;
+    ks = whole_runs(KB, ks);
+    if (a8) return {DWM_DENSE_MFMA, tm, 128, ks, tm == 256 ? 3 : 4};
+    // Enough rows for 256 x 128 tiles to fill the grid: half the weight
+    // re-reads of 128-row tiles (8 waves, one block per CU).
+    if (ks == 1 && (N / 128) * ((M + 255) / 256) >= 256) return {DWM_DENSE_MFMA, 256, 128, 1, 2};
+    // Two blocks per CU either way; a grid that fits one round takes the
+    // deeper ring.
+    return {DWM_DENSE_MFMA, 128, 128, ks, tiles * ks <= 512 ? 3 : 2};
+  }
+  // 16 waves split K, two K blocks (weights, lhs fragments and scales) in
+  // flight per wave; 4/8/16 waves x 2..7 blocks in flight all measured
+  // within 0.5 us at K=7168, N=4096: the 29 MB stream plus launch and
+  // start-up latency sets the time (8 us at M = 1).
+  if (M <= 16) return {DWM_DENSE_SKINNY, 16, 16, 16, 2};
+  dwm_dense_plan p = tiled_default(M, K, N);
+  p.ksplit = whole_runs(KB, p.ksplit);
+  return p;
+}
+
+static int check_plan(int64_t M, int64_t K, int64_t N, bool a8, const dwm_dense_plan &p) {
+  const int64_t KB = K / 128;
+  const char *const v = a8 ? "w8a8" : "w8a16";
+  if (p.kernel == DWM_DENSE_SKINNY) {
+    // Its 16 waves split K inside the block (idle waves when K/128 < 16).
+    DWM_UNSUPPORTED_IF(M > 16, "dense_fp8 plan: the skinny kernel takes M <= 16 (M=%lld)", (long long)M);
+    DWM_UNSUPPORTED_IF(p.tile_m != 16 || p.tile_n != 16 || p.ksplit != 16 || p.stages != 2,
+                       "dense_fp8 plan: the skinny kernel runs 16 x 16 tiles, 16 K runs, ring depth 2");
+    return DWM_OK;
+  }
+  DWM_UNSUPPORTED_IF(p.ksplit < 1 || p.ksplit > KB || p.ksplit > 65535,
+                     "dense_fp8 plan: ksplit %d outside [1, K/128 = %lld]", p.ksplit, (long long)KB);
+  DWM_UNSUPPORTED_IF(whole_runs(KB, p.ksplit) != p.ksplit, "dense_fp8 plan: ksplit %d leaves an empty K run (K/128 = %lld)",
+                     p.ksplit, (long long)KB);
+  switch (p.kernel) {
+    case DWM_DENSE_MFMA: {
+      DWM_UNSUPPORTED_IF(p.tile_n != 128 || (p.tile_m != 128 && p.tile_m != 256),
+                         "dense_fp8 plan: MFMA tiles are 128 x 128 or 256 x 128 (got %d x %d)", p.tile_m, p.tile_n);
+      DWM_UNSUPPORTED_IF(!dense_mfma_ok(M, K, N, p.tile_m),
+                         "dense_fp8 plan: the MFMA kernel needs M > 16, N %% 128 == 0 and 32-bit operand offsets");
+      // Ring depths that fit 160 KB of LDS (W8A8's prefetching loop needs 3).
+      const bool ok = a8 ? (p.tile_m == 128 ? (p.stages == 3 || p.stages == 4) : p.stages == 3)
+                         : (p.tile_m == 128 ? (p.stages >= 2 && p.stages <= 4) : (p.stages == 2 || p.stages == 3));
+      DWM_UNSUPPORTED_IF(!ok, "dense_fp8 plan: %s %d-row MFMA tiles have no %d-stage ring", v, p.tile_m, p.stages);
+      return DWM_OK;
+    }
+    case DWM_DENSE_TILED: {
+      const bool ok = (p.tile_m == 16 && p.tile_n == 64) || (p.tile_m == 64 && p.tile_n == 128) ||
+                      (p.tile_m == 128 && p.tile_n == 128);
+      DWM_UNSUPPORTED_IF(!ok || p.stages != 2,
+                         "dense_fp8 plan: tiled kernel tiles are 16 x 64, 64 x 128 or 128 x 128 with 2 stages");
+      DWM_UNSUPPORTED_IF((M + p.tile_m - 1) / p.tile_m > 65535, "dense_fp8 plan: M too large for %d-row tiles", p.tile_m);
+      return DWM_OK;
+    }
+    default:
+      DWM_UNSUPPORTED_IF(true, "dense_fp8 plan: unknown kernel %d", p.kernel);
+  }
+}
+
+static int64_t plan_workspace(int64_t M, int64_t N, const dwm_dense_plan &p) {
+  return (p.kernel != DWM_DENSE_SKINNY && p.ksplit > 1) ? (int64_t)p.ksplit * M * N * 4 : 0;
+}
+
+// The plan the last dense call of this thread launched (for tests and traces).
+static thread_local dwm_dense_plan t_last_plan{0, 0, 0, 0, 0};
+
+template <class C, bool A8, int NS>
+static void launch_mfma(const void *x, const float *sx, int64_t M, int64_t K, int64_t N, const uint8_t *w,
+                        const float *sw, int sw_ld, int ks, uint16_t *out, float *partial, hipStream_t st) {
+  const dim3 grid((unsigned)(N / C::BN), (unsigned)((M + C::BM - 1) / C::BM), (unsigned)ks);
+  hipLaunchKernelGGL((dense_fp8_mfma_kernel<C, A8, NS, A8>), grid, dim3(C::THREADS), 0, st, x, sx, M, (int)K, (int)N,
+                     w, sw, sw_ld, ks, out, partial);
+}
+
 template <int MB, int NBW, bool A8>
-static void launch_dense(const void *x, const float *sx, int64_t M, int64_t K, int64_t N, const uint8_t *w,
+static void launch_tiled(const void *x, const float *sx, int64_t M, int64_t K, int64_t N, const uint8_t *w,
                          const float *sw, int sw_ld, int ksplit, uint16_t *out, float *partial, hipStream_t st) {
   const int64_t NT = 64 * NBW, MT = 16 * MB;
   dim3 grid((unsigned)((N + NT - 1) / NT), (unsigned)((M + MT - 1) / MT), (unsigned)ksplit);
@@ -764,105 +864,46 @@ static void launch_dense(const void *x, const float *sx, int64_t M, int64_t K, i
                      w, sw, sw_ld, ksplit, out, partial);
 }
 
-// MFMA path (M > 16, N % 128 == 0): W8A16 128x128 tiles (4 waves, two or
-// three 25 KB stages: two blocks per CU), 256x128 tiles (8 waves) when those
-// alone fill the grid; W8A8 256x128 tiles (8 waves, three 50 KB stages of
-// one K block each, fragments read one substep ahead) from M >= 256, 128x128
-// below (four 33 KB stages).  K is split over blocks until the grid covers
-// the 256 CUs; the f32 partials go to the workspace and
-// dense_fp8_reduce_kernel adds them in split order (deterministic).
-static bool dense_mfma_ok(int64_t M, int64_t K, int64_t N) {
-  return M > 16 && N % 128 == 0 && M * K * 2 < (1ll << 32) && K * N < (1ll << 32) && M / 128 < 65535;
-}
-
-static int dense_mfma_ksplit(int64_t M, int64_t K, int64_t N, bool a8) {
-  const int64_t bm = (a8 && M >= 256) ? 256 : 128;
-  const int64_t tiles = (N / 128) * ((M + bm - 1) / bm);
-  int ks = 1;
-  while (tiles * ks < 256 && ks * 2 <= K / 128 && ks < 16) ks *= 2;
-  return ks;
-}
-
+// Runs one dense GEMM with `plan` (NULL: the default plan).
 template <bool A8>
-static int launch_dense_mfma(const void *x, const float *sx, int64_t M, int64_t K, int64_t N, const uint8_t *w,
-                             const float *sw, int sw_ld, uint16_t *out, void *workspace, int64_t workspace_bytes,
-                             hipStream_t st) {
-  const int ks = dense_mfma_ksplit(M, K, N, A8);
-  float *partial = nullptr;
-  if (ks > 1) {
-    const int64_t need = (int64_t)ks * M * N * 4;
-    DWM_CHECK_ARG(workspace && workspace_bytes >= need, "dense_fp8: workspace of %lld bytes needed", (long long)need);
-    partial = (float *)workspace;
-  }
-  if (A8 && M >= 256) {
-    // 50 KB stages: three fit beside the row-scale buffers.
-    using C = DenseMfmaCfg<4, 2, true>;
-    const dim3 grid((unsigned)(N / C::BN), (unsigned)((M + C::BM - 1) / C::BM), (unsigned)ks);
-    hipLaunchKernelGGL((dense_fp8_mfma_kernel<C, true, 3, true>), grid, dim3(C::THREADS), 0, st, x, sx, M, (int)K,
-                       (int)N, w, sw, sw_ld, ks, out, partial);
-  } else if (A8) {
-    using C = DenseMfmaCfg<2, 2, true>;
-    const dim3 grid((unsigned)(N / C::BN), (unsigned)((M + C::BM - 1) / C::BM), (unsigned)ks);
-    hipLaunchKernelGGL((dense_fp8_mfma_kernel<C, true, 4, true>), grid, dim3(C::THREADS), 0, st, x, sx, M, (int)K,
-                       (int)N, w, sw, sw_ld, ks, out, partial);
-  } else if (ks == 1 && (N / 128) * ((M + 255) / 256) >= 256) {
-    // Enough rows for 256 x 128 tiles to fill the grid: half the weight
-    // re-reads of 128-row tiles (8 waves, one block per CU).
-    using C = DenseMfmaCfg<4, 2, false>;
-    const dim3 grid((unsigned)(N / C::BN), (unsigned)((M + C::BM - 1) / C::BM), 1);
-    hipLaunchKernelGGL((dense_fp8_mfma_kernel<C, false, 2>), grid, dim3(C::THREADS), 0, st, x, sx, M, (int)K,
-                       (int)N, w, sw, sw_ld, ks, out, partial);
+static int run_dense(const void *x, const float *sx, int64_t M, int64_t K, int64_t N, const uint8_t *w,
+                     const float *sw, int sw_ld, uint16_t *out, const dwm_dense_plan *plan, void *workspace,
+                     int64_t workspace_bytes, hipStream_t st) {
+  const dwm_dense_plan p = plan ? *plan : default_plan(M, K, N, A8);
+  int rc = check_plan(M, K, N, A8, p);
+  if (rc != DWM_OK) return rc;
+  const int64_t need = plan_workspace(M, N, p);
+  DWM_CHECK_ARG(need == 0 || (workspace && workspace_bytes >= need), "dense_fp8: workspace of %lld bytes needed",
+                (long long)need);
+  float *const partial = need ? (float *)workspace : nullptr;
+  const int ks = p.ksplit;
+  if (p.kernel == DWM_DENSE_SKINNY) {
+    hipLaunchKernelGGL((dense_fp8_skinny_kernel<16, 2, A8>), dim3((unsigned)(N / 16)), dim3(1024), 0, st, x, sx,
+                       (int)M, (int)K, (int)N, w, sw, sw_ld, out);
+  } else if (p.kernel == DWM_DENSE_MFMA) {
+    if constexpr (A8) {
+      if (p.tile_m == 256) launch_mfma<DenseMfmaCfg<4, 2, true>, true, 3>(x, sx, M, K, N, w, sw, sw_ld, ks, out, partial, st);
+      else if (p.stages == 3) launch_mfma<DenseMfmaCfg<2, 2, true>, true, 3>(x, sx, M, K, N, w, sw, sw_ld, ks, out, partial, st);
+      else launch_mfma<DenseMfmaCfg<2, 2, true>, true, 4>(x, sx, M, K, N, w, sw, sw_ld, ks, out, partial, st);
+    } else {
+      if (p.tile_m == 256 && p.stages == 2) launch_mfma<DenseMfmaCfg<4, 2, false>, false, 2>(x, sx, M, K, N, w, sw, sw_ld, ks, out, partial, st);
+      else if (p.tile_m == 256) launch_mfma<DenseMfmaCfg<4, 2, false>, false, 3>(x, sx, M, K, N, w, sw, sw_ld, ks, out, partial, st);
+      else if (p.stages == 2) launch_mfma<DenseMfmaCfg<2, 2, false>, false, 2>(x, sx, M, K, N, w, sw, sw_ld, ks, out, partial, st);
+      else if (p.stages == 3) launch_mfma<DenseMfmaCfg<2, 2, false>, false, 3>(x, sx, M, K, N, w, sw, sw_ld, ks, out, partial, st);
+      else launch_mfma<DenseMfmaCfg<2, 2, false>, false, 4>(x, sx, M, K, N, w, sw, sw_ld, ks, out, partial, st);
+    }
   } else {
-    using C = DenseMfmaCfg<2, 2, false>;
-    const dim3 grid((unsigned)(N / C::BN), (unsigned)((M + C::BM - 1) / C::BM), (unsigned)ks);
-    // Two blocks per CU either way; a grid that fits one round takes the
-    // deeper ring.
-    if ((int64_t)grid.x * grid.y * grid.z <= 512)
-      hipLaunchKernelGGL((dense_fp8_mfma_kernel<C, false, 3>), grid, dim3(C::THREADS), 0, st, x, sx, M, (int)K,
-                         (int)N, w, sw, sw_ld, ks, out, partial);
-    else
-      hipLaunchKernelGGL((dense_fp8_mfma_kernel<C, false, 2>), grid, dim3(C::THREADS), 0, st, x, sx, M, (int)K,
-                         (int)N, w, sw, sw_ld, ks, out, partial);
+    if (p.tile_m == 16) launch_tiled<1, 1, A8>(x, sx, M, K, N, w, sw, sw_ld, ks, out, partial, st);
+    else if (p.tile_m == 64) launch_tiled<4, 2, A8>(x, sx, M, K, N, w, sw, sw_ld, ks, out, partial, st);
+    else launch_tiled<8, 2, A8>(x, sx, M, K, N, w, sw, sw_ld, ks, out, partial, st);
   }
-  int rc = launch_status("dense_fp8");
-  if (rc != DWM_OK || ks == 1) return rc;
+  rc = launch_status("dense_fp8");
+  if (rc != DWM_OK) return rc;
+  t_last_plan = p;
+  if (!partial) return DWM_OK;
   const int64_t MN = M * N;
   const int64_t blocks = (MN + 255) / 256 < 4096 ? (MN + 255) / 256 : 4096;
   hipLaunchKernelGGL(dense_fp8_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, st, partial, ks, MN, out);
-  return launch_status("dense_fp8 reduce");
-}
-
-template <bool A8>
-static int run_dense(const void *x, const float *sx, int64_t M, int64_t K, int64_t N, const uint8_t *w,
-                     const float *sw, int sw_ld, uint16_t *out, void *workspace, int64_t workspace_bytes,
-                     hipStream_t st) {
-  if (dense_mfma_ok(M, K, N))
-    return launch_dense_mfma<A8>(x, sx, M, K, N, w, sw, sw_ld, out, workspace, workspace_bytes, st);
-  if (M <= 16) {
-    // 16 waves split K, two K blocks (weights, lhs fragments and scales) in
-    // flight per wave; 4/8/16 waves x 2..7 blocks in flight all measured
-    // within 0.5 us at K=7168, N=4096: the 29 MB stream plus launch and start-up
-    // latency sets the time (8 us at M = 1).
-    hipLaunchKernelGGL((dense_fp8_skinny_kernel<16, 2, A8>), dim3((unsigned)(N / 16)), dim3(1024), 0, st, x, sx,
-                       (int)M, (int)K, (int)N, w, sw, sw_ld, out);
-    return launch_status("dense_fp8");
-  }
-  const DensePlan p = dense_plan(M, K, N);
-  float *partial = nullptr;
-  if (p.ksplit > 1) {
-    const int64_t need = (int64_t)p.ksplit * M * N * 4;
-    DWM_CHECK_ARG(workspace && workspace_bytes >= need, "dense_fp8: workspace of %lld bytes needed", (long long)need);
-    partial = (float *)workspace;
-  }
-  DWM_UNSUPPORTED_IF((M + 16 * p.mb - 1) / (16 * p.mb) > 65535, "dense_fp8: M too large");
-  if (p.mb == 1) launch_dense<1, 1, A8>(x, sx, M, K, N, w, sw, sw_ld, p.ksplit, out, partial, st);
-  else if (p.mb == 4) launch_dense<4, 2, A8>(x, sx, M, K, N, w, sw, sw_ld, p.ksplit, out, partial, st);
-  else launch_dense<8, 2, A8>(x, sx, M, K, N, w, sw, sw_ld, p.ksplit, out, partial, st);
-  int rc = launch_status("dense_fp8");
-  if (rc != DWM_OK || p.ksplit == 1) return rc;
-  const int64_t MN = M * N;
-  const int64_t blocks = (MN + 255) / 256 < 4096 ? (MN + 255) / 256 : 4096;
-  hipLaunchKernelGGL(dense_fp8_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, st, partial, p.ksplit, MN, out);
   return launch_status("dense_fp8 reduce");
 }
 
@@ -890,37 +931,76 @@ extern "C" int dwm_dense_fp8_prepack(const uint8_t *w, int64_t K, int64_t N, uin
   return launch_status("dense_fp8_prepack");
 }
 
+extern "C" int dwm_dense_fp8_plan(int64_t M, int64_t K, int64_t N, int w8a8, dwm_dense_plan *plan) {
+  clear_error();
+  int rc = check_dense(M, K, N);
+  if (rc != DWM_OK) return rc;
+  DWM_CHECK_ARG(plan, "dense_fp8_plan: null pointer");
+  DWM_UNSUPPORTED_IF(w8a8 && N % 128 != 0, "dense_fp8_w8a8: N %% 128 == 0 required (128x128 weight blocks)");
+  *plan = default_plan(M < 1 ? 1 : M, K, N, w8a8 != 0);
+  return DWM_OK;
+}
+
+extern "C" int dwm_dense_fp8_plan_check(int64_t M, int64_t K, int64_t N, int w8a8, const dwm_dense_plan *plan) {
+  clear_error();
+  int rc = check_dense(M, K, N);
+  if (rc != DWM_OK) return rc;
+  DWM_CHECK_ARG(plan, "dense_fp8_plan_check: null pointer");
+  DWM_UNSUPPORTED_IF(w8a8 && N % 128 != 0, "dense_fp8_w8a8: N %% 128 == 0 required (128x128 weight blocks)");
+  return check_plan(M < 1 ? 1 : M, K, N, w8a8 != 0, *plan);
+}
+
+extern "C" int dwm_dense_fp8_plan_workspace_size(int64_t M, int64_t K, int64_t N, const dwm_dense_plan *plan,
+                                                 int64_t *bytes) {
+  clear_error();
+  int rc = check_dense(M, K, N);
+  if (rc != DWM_OK) return rc;
+  DWM_CHECK_ARG(plan && bytes, "dense_fp8_plan_workspace_size: null pointer");
+  *bytes = plan_workspace(M, N, *plan);
+  return DWM_OK;
+}
+
+extern "C" int dwm_dense_fp8_last_plan(dwm_dense_plan *plan) {
+  clear_error();
+  DWM_CHECK_ARG(plan, "dense_fp8_last_plan: null pointer");
+  *plan = t_last_plan;
+  return DWM_OK;
+}
+
 extern "C" int dwm_dense_fp8_workspace_size(int64_t M, int64_t K, int64_t N, int64_t *bytes) {
   clear_error();
   int rc = check_dense(M, K, N);
   if (rc != DWM_OK) return rc;
   DWM_CHECK_ARG(bytes, "dense_fp8_workspace_size: null pointer");
-  if (dense_mfma_ok(M, K, N)) {
-    // the larger of the W8A16 and W8A8 splits
-    const int ks = max(dense_mfma_ksplit(M, K, N, false), dense_mfma_ksplit(M, K, N, true));
-    *bytes = ks > 1 ? (int64_t)ks * M * N * 4 : 0;
-    return DWM_OK;
-  }
-  const DensePlan p = dense_plan(M, K, N);
-  *bytes = (M > 16 && p.ksplit > 1) ? (int64_t)p.ksplit * M * N * 4 : 0;
+  const int64_t m = M < 1 ? 1 : M;
+  // the larger of the W8A16 and W8A8 default plans' needs
+  int64_t b = plan_workspace(M, N, default_plan(m, K, N, false));
+  if (N % 128 == 0) b = max(b, plan_workspace(M, N, default_plan(m, K, N, true)));
+  *bytes = b;
   return DWM_OK;
 }
 
-extern "C" int dwm_dense_fp8_w8a16(const uint16_t *x, int64_t M, int64_t K, int64_t N, const uint8_t *w,
-                                   const float *s, uint16_t *out, void *workspace, int64_t workspace_bytes,
-                                   void *stream) {
+extern "C" int dwm_dense_fp8_w8a16_plan(const uint16_t *x, int64_t M, int64_t K, int64_t N, const uint8_t *w,
+                                        const float *s, uint16_t *out, const dwm_dense_plan *plan, void *workspace,
+                                        int64_t workspace_bytes, void *stream) {
   clear_error();
   int rc = check_dense(M, K, N);
   if (rc != DWM_OK) return rc;
   if (M == 0) return DWM_OK;
   DWM_CHECK_ARG(x && w && s && out, "dense_fp8_w8a16: null pointer");
   DWM_CHECK_ARG((uintptr_t)x % 16 == 0 && (uintptr_t)w % 16 == 0, "dense_fp8_w8a16: x and w must be 16-byte aligned");
-  return run_dense<false>(x, nullptr, M, K, N, w, s, (int)N, out, workspace, workspace_bytes, as_stream(stream));
+  return run_dense<false>(x, nullptr, M, K, N, w, s, (int)N, out, plan, workspace, workspace_bytes, as_stream(stream));
 }
 
-extern "C" int dwm_dense_fp8_w8a8(const uint8_t *xq, const float *sx, int64_t M, int64_t K, int64_t N,
-                                  const uint8_t *w, const float *sw, uint16_t *out, void *workspace,
-                                  int64_t workspace_bytes, void *stream) {
+extern "C" int dwm_dense_fp8_w8a16(const uint16_t *x, int64_t M, int64_t K, int64_t N, const uint8_t *w,
+                                   const float *s, uint16_t *out, void *workspace, int64_t workspace_bytes,
+                                   void *stream) {
+  return dwm_dense_fp8_w8a16_plan(x, M, K, N, w, s, out, nullptr, workspace, workspace_bytes, stream);
+}
+
+extern "C" int dwm_dense_fp8_w8a8_plan(const uint8_t *xq, const float *sx, int64_t M, int64_t K, int64_t N,
+                                       const uint8_t *w, const float *sw, uint16_t *out, const dwm_dense_plan *plan,
+                                       void *workspace, int64_t workspace_bytes, void *stream) {
   clear_error();
   int rc = check_dense(M, K, N);
   if (rc != DWM_OK) return rc;
@@ -928,5 +1008,12 @@ extern "C" int dwm_dense_fp8_w8a8(const uint8_t *xq, const float *sx, int64_t M,
   DWM_UNSUPPORTED_IF(N % 128 != 0, "dense_fp8_w8a8: N %% 128 == 0 required (128x128 weight blocks)");
   DWM_CHECK_ARG(xq && sx && w && sw && out, "dense_fp8_w8a8: null pointer");
   DWM_CHECK_ARG((uintptr_t)xq % 16 == 0 && (uintptr_t)w % 16 == 0, "dense_fp8_w8a8: xq and w must be 16-byte aligned");
-  return run_dense<true>(xq, sx, M, K, N, w, sw, (int)(N / 128), out, workspace, workspace_bytes, as_stream(stream));
+  return run_dense<true>(xq, sx, M, K, N, w, sw, (int)(N / 128), out, plan, workspace, workspace_bytes,
+                         as_stream(stream));
+}
+
+extern "C" int dwm_dense_fp8_w8a8(const uint8_t *xq, const float *sx, int64_t M, int64_t K, int64_t N,
+                                  const uint8_t *w, const float *sw, uint16_t *out, void *workspace,
+                                  int64_t workspace_bytes, void *stream) {
+  return dwm_dense_fp8_w8a8_plan(xq, sx, M, K, N, w, sw, out, nullptr, workspace, workspace_bytes, stream);
 }

@@ -43,12 +43,30 @@ SIGNATURES = {
     "dwm_dense_fp8_workspace_size": [_i64, _i64, _i64, _p],
     "dwm_dense_fp8_w8a16": [_p, _i64, _i64, _i64, _p, _p, _p, _p, _i64, _p],
     "dwm_dense_fp8_w8a8": [_p, _p, _i64, _i64, _i64, _p, _p, _p, _p, _i64, _p],
+    "dwm_dense_fp8_plan": [_i64, _i64, _i64, _i32, _p],
+    "dwm_dense_fp8_plan_check": [_i64, _i64, _i64, _i32, _p],
+    "dwm_dense_fp8_plan_workspace_size": [_i64, _i64, _i64, _p, _p],
+    "dwm_dense_fp8_w8a16_plan": [_p, _i64, _i64, _i64, _p, _p, _p, _p, _p, _i64, _p],
+    "dwm_dense_fp8_w8a8_plan": [_p, _p, _i64, _i64, _i64, _p, _p, _p, _p, _p, _i64, _p],
+    "dwm_dense_fp8_last_plan": [_p],
     "dwm_mxfp4_requant": [_p, _p, _i64, _i64, _i64, _i32, _p, _p, _p, _p],
     "dwm_fp8_block_requant": [_p, _p, _i64, _i64, _i32, _p, _p, _p, _p],
     "dwm_route_topk": [_p, _i32, _i64, _i64, _i32, _i32, _p, _p, _i32, _p, _p, _i32, _p, _p],
     "dwm_dedupe_topk": [_p, _p, _i64, _i32, _i64, _p, _p, _p],
 }
 _RESTYPES = {"dwm_last_error": ctypes.c_char_p}
+
+# enum dwm_dense_kernel
+DENSE_SKINNY, DENSE_MFMA, DENSE_TILED = 1, 2, 3
+
+
+class DensePlan(ctypes.Structure):
+    """struct dwm_dense_plan: one launch configuration of the dense GEMM."""
+    _fields_ = [("kernel", ctypes.c_int32), ("tile_m", ctypes.c_int32), ("tile_n", ctypes.c_int32),
+                ("ksplit", ctypes.c_int32), ("stages", ctypes.c_int32)]
+
+    def astuple(self):
+        return (self.kernel, self.tile_m, self.tile_n, self.ksplit, self.stages)
 
 
 class LibraryMissing(RuntimeError):

@@ -10,6 +10,10 @@ accumulated in f32 and stored as bf16 (the reference's "native" mode).
 Weights: ``prepack_fp8`` relayouts a stored e4m3 weight [K, N] once (load
 time) into the kernel's K-major chunks and returns an ``Fp8Weight``; raw
 weight tensors are prepacked on every call (one extra pass over the weight).
+
+Tiles: ``select_tile`` returns the ``(mode, tm, tk, tn)`` of the launch the
+library will make (``dense_fp8_tiles`` maps it to and from the C plan), and
+``matmul`` passes a given tile through to the kernel.
 """
 import ctypes
 from dataclasses import dataclass
@@ -17,7 +21,7 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
-from .dense_fp8_tiles import overrides
+from .dense_fp8_tiles import DenseTile, default_plan, overrides, plan_to_tile, tile_to_plan
 
 E4M3 = torch.float8_e4m3fn
 
@@ -51,10 +55,16 @@ def prepack_fp8(weight: torch.Tensor) -> Fp8Weight:
     return Fp8Weight(out, k, n)
 
 
-def _workspace(m, k, n, dev):
+def _plan_and_workspace(m, k, n, dev, tile, w8a8):
+    """(plan pointer or None, workspace tensor or None, workspace bytes)."""
+    plan = None if tile is None else tile_to_plan(tile, max(m, 1), k, n, w8a8)
     b = ctypes.c_int64(0)
-    _lib.call("dwm_dense_fp8_workspace_size", m, k, n, ctypes.byref(b))
-    return None if b.value == 0 else torch.empty(b.value, dtype=torch.uint8, device=dev), b.value
+    if plan is None:
+        _lib.call("dwm_dense_fp8_workspace_size", m, k, n, ctypes.byref(b))
+    else:
+        _lib.call("dwm_dense_fp8_plan_workspace_size", m, k, n, ctypes.byref(plan), ctypes.byref(b))
+    ws = None if b.value == 0 else torch.empty(b.value, dtype=torch.uint8, device=dev)
+    return (None if plan is None else ctypes.byref(plan)), ws, b.value
 
 
 def _aligned(t):
@@ -62,12 +72,16 @@ def _aligned(t):
     return t.clone() if t.data_ptr() % 16 else t
 
 
-def matmul(x, w, s, *, tn=1024, tk=1024, tm=16, mode="native"):
+def matmul(x, w, s, *, tn=None, tk=None, tm=None, mode="native", stages=0):
     """W8A16 dense GEMM: x [M, K] bf16, w [K, N] e4m3 (or ``Fp8Weight``),
-    s [K/128, 1, N] f32 -> bf16 [M, N].  The tile arguments of the TPU kernel
-    are accepted and ignored; ``mode`` other than "native" is unsupported
-    here (the other reference modes are tiling variants or, for "pre", a
-    different rounding)."""
+    s [K/128, 1, N] f32 -> bf16 [M, N].
+
+    With tm, tk and tn left unset the library launches its own plan.  Given,
+    they name a launch (``dense_fp8_tiles``: mode "native" = the skinny or
+    MFMA kernel, "megablox" = the general tiled kernel; tk = the K depth per
+    block; ``stages`` = ring depth) and a tile this build has no kernel for
+    raises ValueError.  The reference's "pre" mode (weights scaled in bf16
+    before the dot) is a different rounding and is not provided."""
     if mode not in ("native", "megablox"):
         raise NotImplementedError(f"dense_fp8 mode {mode!r} is not supported")
     pw = prepack_fp8(w)
@@ -78,17 +92,19 @@ def matmul(x, w, s, *, tn=1024, tk=1024, tm=16, mode="native"):
     x = _aligned(x)
     sc = s.reshape(k // 128, n).to(torch.float32).contiguous()
     dev = _lib.require_cuda(x, pw.weight, sc)
+    tile = None if (tm, tk, tn) == (None, None, None) else DenseTile(mode, tm, tk, tn, stages)
+    plan, ws, wsb = _plan_and_workspace(m, k, n, dev, tile, False)
     out = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
-    ws, wsb = _workspace(m, k, n, dev)
-    _lib.call("dwm_dense_fp8_w8a16", _lib.ptr(x), m, k, n, _lib.ptr(pw.weight), _lib.ptr(sc), _lib.ptr(out),
-              _lib.ptr(ws), wsb, _lib.stream_handle(dev))
+    _lib.call("dwm_dense_fp8_w8a16_plan", _lib.ptr(x), m, k, n, _lib.ptr(pw.weight), _lib.ptr(sc), _lib.ptr(out),
+              plan, _lib.ptr(ws), wsb, _lib.stream_handle(dev))
     return out
 
 
-def matmul_w8a8(xq, sx, w, sw):
+def matmul_w8a8(xq, sx, w, sw, *, tile=None):
     """W8A8 block GEMM: xq [M, K] e4m3 with sx [M, K/128] f32; w [K, N] e4m3
     (or ``Fp8Weight``) with 128x128 block scales sw [K/128, N/128] f32 ->
-    bf16 [M, N]."""
+    bf16 [M, N].  ``tile``: a ``(mode, tm, tk, tn)`` launch as for ``matmul``
+    (None: the library's plan)."""
     pw = prepack_fp8(w)
     xq = xq.view(torch.uint8) if xq.dtype == E4M3 else xq
     m, k = xq.shape
@@ -99,29 +115,35 @@ def matmul_w8a8(xq, sx, w, sw):
     sx = sx.to(torch.float32).contiguous()
     sw = sw.to(torch.float32).contiguous()
     dev = _lib.require_cuda(xq, sx, pw.weight, sw)
+    plan, ws, wsb = _plan_and_workspace(m, k, n, dev, tile, True)
     out = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
-    ws, wsb = _workspace(m, k, n, dev)
-    _lib.call("dwm_dense_fp8_w8a8", _lib.ptr(xq), _lib.ptr(sx), m, k, n, _lib.ptr(pw.weight), _lib.ptr(sw),
-              _lib.ptr(out), _lib.ptr(ws), wsb, _lib.stream_handle(dev))
+    _lib.call("dwm_dense_fp8_w8a8_plan", _lib.ptr(xq), _lib.ptr(sx), m, k, n, _lib.ptr(pw.weight), _lib.ptr(sw),
+              _lib.ptr(out), plan, _lib.ptr(ws), wsb, _lib.stream_handle(dev))
     return out
 
 
-def select_tile(m, k, n):
-    """(mode, tm, tk, tn) of the kernel for an M x K x N problem, or None.
+def last_plan():
+    """The ``_lib.DensePlan`` of the last dense GEMM this thread launched."""
+    plan = _lib.DensePlan()
+    _lib.call("dwm_dense_fp8_last_plan", ctypes.byref(plan))
+    return plan
 
-    A valid entry of the tile-override table wins (``baseline`` entries
-    return None, keeping the caller's path); otherwise any K % 128 == 0,
-    N % 16 == 0 problem is supported and the tiles describe the HIP kernel's
-    own choice (16/64/128 rows, 64/128 columns, full 128-deep K steps).
+
+def select_tile(m, k, n):
+    """The ``(mode, tm, tk, tn)`` launch for an M x K x N W8A16 problem, or
+    None to keep the caller's path.
+
+    An entry of the override file wins (a "baseline" entry gives None);
+    otherwise the library's own plan for the shape (``dwm_dense_fp8_plan``),
+    i.e. exactly what ``matmul`` launches with no tile given.  Shapes the
+    kernels do not take (K % 128, N % 16, M < 1) give None.
     """
     table = overrides()
     if (m, k, n) in table:
         return table[m, k, n]
-    if k % 128 or n % 16 or m < 1:
+    if m < 1 or k < 128 or k % 128 or n < 16 or n % 16:
         return None
-    tm = 16 if m <= 16 else (64 if m <= 64 else 128)
-    tn = 64 if m <= 16 else 128
-    return ("native", tm, 128, tn)
+    return plan_to_tile(default_plan(m, k, n), k)
 
 
 def try_dense_fp8(x, weight, scale):
@@ -142,7 +164,9 @@ def try_dense_fp8(x, weight, scale):
         return None
     if not x.is_cuda:
         return None
+    mode, tm, tk, tn = entry
     try:
-        return matmul(x, weight, scale.reshape(k // 128, 1, n))
+        return matmul(x, weight, scale.reshape(k // 128, 1, n), tm=tm, tk=tk, tn=tn, mode=mode,
+                      stages=getattr(entry, "stages", 0))
     except _lib.Unsupported:
         return None

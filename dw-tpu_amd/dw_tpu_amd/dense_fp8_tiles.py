@@ -1,63 +1,159 @@
-"""Validated, immutable per-process dense FP8 tile overrides (no device work).
+"""Dense FP8 launch selection: tiles as the reference names them, plans as
+this library launches them, and the per-process override file.
 
-Mirrors kernels/tpu_inference/kernels/experimental/dense_fp8_tiles.py:11-58:
-a JSON table named by the DSV4_DENSE_FP8_TILES environment variable, read
-once and validated fail-closed (ValueError on any malformed entry).  Entries
-select per-(M, K, N) tiles or "baseline" (keep the caller's path).  The
-device string is this build's target.
+The reference picks a dense tile as ``(mode, tm, tk, tn)``
+(kernels/tpu_inference/kernels/experimental/dense_fp8.py:80-138) and lets a
+JSON file named by ``DSV4_DENSE_FP8_TILES`` pin it per (M, K, N)
+(dense_fp8_tiles.py:11-58).  Both the tuple and the file's schema are kept,
+so a caller's table and its unpacking of ``select_tile`` work unchanged.
+What they mean here is a launch of this library's kernels
+(``struct dwm_dense_plan``):
+
+  mode "native"    tm = tn = 16: the skinny kernel (M <= 16; its 16 waves
+                   split K inside one block, so tk = K);
+                   tm = 128 or 256, tn = 128: the MFMA tile kernel;
+  mode "megablox"  the general tiled kernel, tm x tn = 16 x 64, 64 x 128 or
+                   128 x 128 (any N % 16 == 0);
+  tk               the K depth one block covers: K / tk blocks share an
+                   output tile and their f32 partials are added in order;
+  "stages"         optional ring depth (LDS stages of the MFMA kernel);
+  mode "baseline"  no launch: ``try_dense_fp8`` returns None.
+
+Table entries are checked by the library's own plan rules when the file is
+read (``dwm_dense_fp8_plan_check``, host code only), so a table can name
+only launches that exist.  A malformed file raises ValueError.
 """
+import ctypes
 import functools
 import json
 import os
 
+from . import _lib
+
+ENV_VAR = "DSV4_DENSE_FP8_TILES"
 DEVICE = "AMD Instinct MI355X"
-ROWS = frozenset(range(1, 34)) | {64, 65, 128, 129, 256, 257, 512, 513, 1024, 4096}
-MODES = ("native", "megablox")
+FORMAT_VERSION = 1
+
+_KERNEL_OF_MODE = {"native": None, "megablox": _lib.DENSE_TILED}
 
 
-def validate_table(data):
-    if not isinstance(data, dict) or type(data.get("version")) is not int or data["version"] != 1:
-        raise ValueError("dense FP8 tile table requires version=1")
+class DenseTile(tuple):
+    """``(mode, tm, tk, tn)`` -- the reference's ``select_tile`` value --
+    with the ring depth as ``.stages`` (0: the library's usual depth for the
+    tile)."""
+
+    def __new__(cls, mode, tm, tk, tn, stages=0):
+        self = super().__new__(cls, (mode, tm, tk, tn))
+        self.stages = stages
+        return self
+
+    mode = property(lambda self: self[0])
+    tm = property(lambda self: self[1])
+    tk = property(lambda self: self[2])
+    tn = property(lambda self: self[3])
+
+    def __repr__(self):
+        return f"DenseTile{tuple(self)!r}(stages={self.stages})"
+
+
+def _usual_stages(kernel, tile_m, w8a8):
+    if kernel == _lib.DENSE_MFMA:
+        if w8a8:
+            return 4 if tile_m == 128 else 3
+        return 3 if tile_m == 128 else 2
+    return 2
+
+
+def plan_to_tile(plan, k):
+    """The ``DenseTile`` describing a ``_lib.DensePlan`` at depth K."""
+    kb = k // 128
+    if plan.kernel == _lib.DENSE_SKINNY:
+        return DenseTile("native", plan.tile_m, k, plan.tile_n, plan.stages)
+    tk = 128 * -(-kb // plan.ksplit)
+    mode = "megablox" if plan.kernel == _lib.DENSE_TILED else "native"
+    return DenseTile(mode, plan.tile_m, tk, plan.tile_n, plan.stages)
+
+
+def tile_to_plan(tile, m, k, n, w8a8=False):
+    """The ``_lib.DensePlan`` a tile names at M x K x N; ValueError if the
+    tile names no launch of this library (checked by the library itself)."""
+    mode, tm, tk, tn = tile
+    stages = getattr(tile, "stages", 0)
+    if mode not in _KERNEL_OF_MODE:
+        raise ValueError(f"dense tile mode {mode!r} is not one of {sorted(_KERNEL_OF_MODE)}")
+    if any(type(v) is not int for v in (tm, tk, tn, stages)):
+        raise ValueError(f"dense tile sizes must be integers: {tile!r}")
+    if tk <= 0 or tk % 128:
+        raise ValueError(f"tk={tk} must be a positive multiple of 128 (the scale block)")
+    kernel = _KERNEL_OF_MODE[mode]
+    if kernel is None:
+        kernel = _lib.DENSE_SKINNY if (tm, tn) == (16, 16) else _lib.DENSE_MFMA
+    if kernel == _lib.DENSE_SKINNY:
+        if tk != k:
+            raise ValueError(f"the skinny kernel covers all of K in one block: tk must be {k}")
+        ksplit = 16
+    else:
+        ksplit = -(-(k // 128) // (tk // 128))
+    plan = _lib.DensePlan(kernel, tm, tn, ksplit, stages or _usual_stages(kernel, tm, w8a8))
+    if kernel != _lib.DENSE_SKINNY and plan_to_tile(plan, k)[2] != tk:
+        raise ValueError(f"tk={tk} does not split K={k} into whole runs of its own depth")
+    try:
+        _lib.call("dwm_dense_fp8_plan_check", m, k, n, int(bool(w8a8)), ctypes.byref(plan))
+    except _lib.Unsupported as exc:
+        raise ValueError(str(exc)) from None
+    return plan
+
+
+def default_plan(m, k, n, w8a8=False):
+    """The plan the library launches when none is given."""
+    plan = _lib.DensePlan()
+    _lib.call("dwm_dense_fp8_plan", m, k, n, int(bool(w8a8)), ctypes.byref(plan))
+    return plan
+
+
+def parse_table(data):
+    """JSON document -> {(m, k, n): DenseTile or None}."""
+    if not isinstance(data, dict):
+        raise ValueError("dense tile file: the document must be a JSON object")
+    if data.get("version") != FORMAT_VERSION or type(data.get("version")) is not int:
+        raise ValueError(f"dense tile file: version must be {FORMAT_VERSION}")
     if data.get("device") != DEVICE:
-        raise ValueError(f"dense FP8 tile table requires device {DEVICE!r}")
-    if not isinstance(data.get("entries"), list):
-        raise ValueError("dense FP8 tile table requires entries list")
-    table = {}
-    for row in data["entries"]:
+        raise ValueError(f"dense tile file: written for {data.get('device')!r}, this build runs on {DEVICE!r}")
+    rows = data.get("entries")
+    if not isinstance(rows, list):
+        raise ValueError("dense tile file: 'entries' must be a list")
+    out = {}
+    for i, row in enumerate(rows):
         if not isinstance(row, dict):
-            raise ValueError("tile entry must be an object")
-        dims = tuple(row.get(key) for key in ("m", "k", "n"))
-        if any(type(x) is not int for x in dims):
-            raise ValueError("tile dimensions must be integers")
-        m, k, n = dims
-        if m not in ROWS or k % 128 or n % 16 or k <= 0 or n <= 0 or dims in table:
-            raise ValueError(f"unsupported or duplicate dense tile: {dims}")
-        mode = row.get("mode")
-        if mode == "baseline":
-            table[dims] = None
+            raise ValueError(f"dense tile file: entry {i} is not an object")
+        key = tuple(row.get(f) for f in ("m", "k", "n"))
+        if any(type(v) is not int or v <= 0 for v in key):
+            raise ValueError(f"dense tile file: entry {i} needs positive integer m, k, n")
+        if key in out:
+            raise ValueError(f"dense tile file: (m, k, n) = {key} appears twice")
+        if row.get("mode") == "baseline":
+            out[key] = None
             continue
-        if mode not in MODES:
-            raise ValueError("only native/megablox/baseline tiles are supported")
-        tile = tuple(row.get(key) for key in ("tm", "tk", "tn"))
-        if any(type(x) is not int or x <= 0 for x in tile):
-            raise ValueError("tile sizes must be positive integers")
-        tm, tk, tn = tile
-        if m % tm or k % tk or n % tn or tk % 128 or tn % 16:
-            raise ValueError("tile must divide dimensions; K tiles align to 128, N tiles to 16")
-        if tm != m and tm % 16:
-            raise ValueError("partial M tiles must align to 16")
-        table[dims] = (mode, tm, tk, tn)
-    return table
+        tile = DenseTile(row.get("mode"), row.get("tm"), row.get("tk"), row.get("tn"), row.get("stages", 0))
+        try:
+            plan = tile_to_plan(tile, *key)
+        except ValueError as exc:
+            raise ValueError(f"dense tile file: entry {i} {key}: {exc}") from None
+        out[key] = DenseTile(*tile, plan.stages)
+    return out
+
+
+validate_table = parse_table  # the reference's name for the same check
 
 
 @functools.lru_cache(maxsize=None)
-def _load(path):
-    # Read once: changing the file later cannot change the process's choices.
-    with open(path, encoding="utf-8") as handle:
-        return validate_table(json.load(handle))
+def _read(path):
+    with open(path, encoding="utf-8") as fh:
+        return parse_table(json.load(fh))
 
 
 def overrides():
-    """Set DSV4_DENSE_FP8_TILES before startup; absent means unchanged defaults."""
-    path = os.environ.get("DSV4_DENSE_FP8_TILES", "")
-    return _load(path) if path else {}
+    """{(m, k, n): DenseTile or None} from the file named by
+    DSV4_DENSE_FP8_TILES ({} when unset).  The file is read once per path."""
+    path = os.environ.get(ENV_VAR)
+    return _read(path) if path else {}

@@ -241,6 +241,61 @@ int dwm_dense_fp8_w8a8(const uint8_t *xq, const float *sx, int64_t M, int64_t K,
                        const uint8_t *w, const float *sw, uint16_t *out, void *workspace,
                        int64_t workspace_bytes, void *stream);
 
+/* Launch plans of the dense GEMM: what the reference's tile selection
+ * (select_tile, _TUNED, _DECODE_TILES and the tile-override table,
+ * kernels/tpu_inference/kernels/experimental/dense_fp8.py:80-138,
+ * dense_fp8_tiles.py:11-58) and matmul's tm/tk/tn (dense_fp8.py:15-76) choose
+ * there, expressed in this library's kernels. */
+enum dwm_dense_kernel {
+  /* M <= 16: one block per 16 columns; its 16 waves split K (ksplit = 16)
+   * and add their f32 partial sums in wave order; register ring depth 2. */
+  DWM_DENSE_SKINNY = 1,
+  /* tile_m x 128 tiles (tile_m 128 or 256), 32x32 MFMA (bf16 for W8A16, fp8
+   * for W8A8) fed by an LDS ring of `stages` K steps.  Needs M > 16 and
+   * N % 128 == 0. */
+  DWM_DENSE_MFMA = 2,
+  /* General tiles for any N % 16 == 0: 16 x 64, 64 x 128 or 128 x 128,
+   * 16x16x32 bf16 MFMA, double-buffered LDS (stages = 2). */
+  DWM_DENSE_TILED = 3
+};
+
+typedef struct dwm_dense_plan {
+  int32_t kernel; /* enum dwm_dense_kernel */
+  int32_t tile_m; /* output rows per block */
+  int32_t tile_n; /* output columns per block */
+  int32_t ksplit; /* K runs per output tile (blocks, or the skinny kernel's waves),
+                     each ceil(K/128 / ksplit) 128-deep blocks, none empty; their
+                     f32 partials are added in run order and rounded once */
+  int32_t stages; /* ring depth (LDS stages, or the skinny kernel's register ring) */
+} dwm_dense_plan;
+
+/* The plan the library launches by default for M x K x N (w8a8 != 0: the
+ * W8A8 variant).  M = 0 plans as M = 1. */
+int dwm_dense_fp8_plan(int64_t M, int64_t K, int64_t N, int w8a8, dwm_dense_plan *plan);
+
+/* DWM_OK if `plan` is a configuration this library has a kernel for at
+ * M x K x N, else DWM_ERR_UNSUPPORTED with the reason in dwm_last_error(). */
+int dwm_dense_fp8_plan_check(int64_t M, int64_t K, int64_t N, int w8a8, const dwm_dense_plan *plan);
+
+/* Workspace bytes `plan` needs (ksplit > 1 outside the skinny kernel:
+ * ksplit * M * N f32 partials). */
+int dwm_dense_fp8_plan_workspace_size(int64_t M, int64_t K, int64_t N, const dwm_dense_plan *plan,
+                                      int64_t *bytes);
+
+/* dwm_dense_fp8_w8a16 / dwm_dense_fp8_w8a8 with an explicit launch plan
+ * (NULL: the default plan).  Every plan gives the same products and the same
+ * 128-K partial sums; only the order in which K runs are added differs. */
+int dwm_dense_fp8_w8a16_plan(const uint16_t *x, int64_t M, int64_t K, int64_t N, const uint8_t *w,
+                             const float *s, uint16_t *out, const dwm_dense_plan *plan, void *workspace,
+                             int64_t workspace_bytes, void *stream);
+int dwm_dense_fp8_w8a8_plan(const uint8_t *xq, const float *sx, int64_t M, int64_t K, int64_t N,
+                            const uint8_t *w, const float *sw, uint16_t *out, const dwm_dense_plan *plan,
+                            void *workspace, int64_t workspace_bytes, void *stream);
+
+/* The plan of the last dense GEMM this thread launched (all zero before the
+ * first), so callers and tests can see which configuration ran. */
+int dwm_dense_fp8_last_plan(dwm_dense_plan *plan);
+
 /* ---------------------------------------------------------------------- */
 /* Checkpoint weight formats (load time).                                  */
 /* ---------------------------------------------------------------------- */

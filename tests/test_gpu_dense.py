@@ -148,3 +148,85 @@ def test_dense_full_size_exact_scaling(dev):
     b8 = matmul_w8a8(xq, sx * 2, pw, sw).float()
     torch.cuda.synchronize()
     assert torch.equal(b8, a8 * 2)
+
+
+_M, _K, _N = 160, 2048, 512  # 2 x 4 MFMA tiles: the default plan splits K 16 ways
+
+
+@pytest.mark.parametrize("tile,plan", [
+    (None, (2, 128, 128, 16, 3)),                            # the library's plan
+    (("native", 256, 2048, 128, 2), (2, 256, 128, 1, 2)),    # one 256-row tile per column tile, no split
+    (("native", 128, 512, 128, 4), (2, 128, 128, 4, 4)),     # 4 K runs, 4-stage ring
+    (("megablox", 64, 1024, 128, 2), (3, 64, 128, 2, 2)),    # the general tiled kernel, 2 K runs
+    (("megablox", 16, 2048, 64, 2), (3, 16, 64, 1, 2)),
+])
+def test_w8a16_tile_choice_is_launched(dev, tile, plan):
+    """A tile given to matmul is the launch the library makes (its plan read
+    back from the library), and every plan stays within the dense bound."""
+    from dw_tpu_amd.dense_fp8 import last_plan, matmul
+    from dw_tpu_amd.dense_fp8_tiles import DenseTile
+    from dw_tpu_amd.workloads import make_dense_workload
+    wl = make_dense_workload(_M, _K, _N, seed=81)
+    x = bf16_tensor(wl.x_bits, dev)
+    w = torch.from_numpy(wl.wq).to(dev).view(torch.float8_e4m3fn)
+    s = torch.from_numpy(wl.s_w8a16).to(dev)
+    if tile is None:
+        out = matmul(x, w, s)
+    else:
+        t = DenseTile(*tile)
+        out = matmul(x, w, s, mode=t.mode, tm=t.tm, tk=t.tk, tn=t.tn, stages=t.stages)
+    torch.cuda.synchronize()
+    assert last_plan().astuple() == plan
+    xf = bf16_to_f32(wl.x_bits)
+    y64 = odf.matmul_w8a16(xf, wl.wq, wl.s_w8a16, out_dtype="float64")
+    print(tile, _check(out, y64, odf.abs_product_w8a16(xf, wl.wq, wl.s_w8a16), _K))
+
+
+def test_override_file_steers_try_dense_fp8(dev, tmp_path, monkeypatch):
+    """An entry of the DSV4_DENSE_FP8_TILES file changes what try_dense_fp8
+    launches (dense_fp8.py:115-163 with dense_fp8_tiles.py:52-58); a
+    "baseline" entry returns None."""
+    import json
+    from dw_tpu_amd import dense_fp8_tiles as tiles
+    from dw_tpu_amd.dense_fp8 import last_plan, try_dense_fp8
+    from dw_tpu_amd.workloads import make_dense_workload
+    p = tmp_path / "tiles.json"
+    p.write_text(json.dumps({"version": 1, "device": tiles.DEVICE, "entries": [
+        {"m": _M, "k": _K, "n": _N, "mode": "native", "tm": 256, "tk": 1024, "tn": 128, "stages": 3},
+        {"m": _M + 1, "k": _K, "n": _N, "mode": "baseline"}]}))
+    monkeypatch.setenv(tiles.ENV_VAR, str(p))
+    tiles._read.cache_clear()
+    try:
+        wl = make_dense_workload(_M, _K, _N, seed=82)
+        w = torch.from_numpy(wl.wq).to(dev).view(torch.float8_e4m3fn)
+        s = torch.from_numpy(wl.s_w8a16).to(dev).reshape(_K // 128, 1, _N)
+        out = try_dense_fp8(bf16_tensor(wl.x_bits, dev), w, s)
+        torch.cuda.synchronize()
+        assert out is not None and last_plan().astuple() == (2, 256, 128, 2, 3)
+        xf = bf16_to_f32(wl.x_bits)
+        _check(out, odf.matmul_w8a16(xf, wl.wq, wl.s_w8a16, out_dtype="float64"),
+               odf.abs_product_w8a16(xf, wl.wq, wl.s_w8a16), _K)
+        x1 = torch.zeros((_M + 1, _K), dtype=torch.bfloat16, device=dev)
+        assert try_dense_fp8(x1, w, s) is None
+    finally:
+        monkeypatch.delenv(tiles.ENV_VAR)
+        tiles._read.cache_clear()
+
+
+@pytest.mark.parametrize("tile,plan", [
+    (None, (2, 128, 128, 16, 4)),
+    (("native", 128, 1024, 128, 3), (2, 128, 128, 2, 3)),
+    (("native", 256, 2048, 128, 3), (2, 256, 128, 1, 3)),
+])
+def test_w8a8_tile_choice_is_launched(dev, tile, plan):
+    from dw_tpu_amd.dense_fp8 import last_plan, matmul_w8a8
+    from dw_tpu_amd.dense_fp8_tiles import DenseTile
+    from dw_tpu_amd.workloads import make_dense_workload
+    wl = make_dense_workload(_M, _K, _N, seed=83)
+    out = matmul_w8a8(torch.from_numpy(wl.xq).to(dev), torch.from_numpy(wl.sx).to(dev),
+                      torch.from_numpy(wl.wq).to(dev), torch.from_numpy(wl.sw).to(dev),
+                      tile=None if tile is None else DenseTile(*tile))
+    torch.cuda.synchronize()
+    assert last_plan().astuple() == plan
+    y64 = odf.matmul_w8a8(wl.xq, wl.sx, wl.wq, wl.sw, out_dtype="float64")
+    print(tile, _check(out, y64, odf.abs_product_w8a8(wl.xq, wl.sx, wl.wq, wl.sw), _K))
