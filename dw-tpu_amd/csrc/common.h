@@ -67,6 +67,17 @@ __device__ __forceinline__ uint32_t cvt_fp4x2_bf16(uint32_t src, float scale) {
   return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(src, scale, SEL));
 }
 
+typedef __attribute__((ext_vector_type(2))) short i16x2_t;
+
+// Four f32 of magnitude <= 448 -> e4m3 codes, round to nearest even (the
+// converter with unit scale; larger magnitudes never reach it here).
+__device__ __forceinline__ uint32_t f32x4_e4m3(const float *v) {
+  i16x2_t r = {0, 0};
+  r = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(r, v[0], v[1], 1.0f, false);
+  r = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(r, v[2], v[3], 1.0f, true);
+  return __builtin_bit_cast(uint32_t, r);
+}
+
 // e8m0 code -> the f32 with that exponent field (2^(c-127) for 1 <= c <= 254).
 __device__ __forceinline__ float e8m0_to_f32(uint32_t code) {
   return __builtin_bit_cast(float, (code & 0xFFu) << 23);

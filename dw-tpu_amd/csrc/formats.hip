@@ -21,7 +21,6 @@
 #include "common.h"
 
 typedef __attribute__((ext_vector_type(2))) float f32x2_t;
-typedef __attribute__((ext_vector_type(2))) short i16x2_t;
 
 namespace dwm {
 
@@ -197,15 +196,6 @@ __device__ __forceinline__ void e4m3x4_f32(uint32_t w, float *v) {
   v[1] = lo[1];
   v[2] = hi[0];
   v[3] = hi[1];
-}
-
-// Four f32 of magnitude <= 448 -> e4m3 codes, round to nearest even (the
-// converter with unit scale; larger magnitudes never reach it here).
-__device__ __forceinline__ uint32_t f32x4_e4m3(const float *v) {
-  i16x2_t r = {0, 0};
-  r = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(r, v[0], v[1], 1.0f, false);
-  r = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(r, v[2], v[3], 1.0f, true);
-  return __builtin_bit_cast(uint32_t, r);
 }
 
 // FP8 block requant, block (kb, nt): K rows kb*128 .. +127, columns nt*64 ..

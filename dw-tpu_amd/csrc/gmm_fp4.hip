@@ -21,57 +21,9 @@
 // block that holds rows.  The dequantised weights are exact (e2m1 x power of
 // two fits bf16), so the products equal the reference's
 // bf16(decode(q)) * bf16(scale) operands; only the f32 summation order differs.
-#include "common.h"
+#include "gmm_tiles.h"
 
 namespace dwm {
-
-constexpr int kMaxGroups = 1024;
-constexpr float kSwigluLimit = 10.0f;  // DeepSeek V4 swiglu_limit of silu_and_mul_with_clamp
-
-// Row tiles are ordered by cost.  A local group of sz rows has sz / MT full
-// row tiles and, when sz % MT != 0, one partial tile; a row tile's class is
-// its count of 32-row MFMA blocks (1 .. MB), the full tiles' class being MB.
-// Wave 0 computes the exclusive row starts of every group and, per class
-// (index 0 = MB blocks, largest first), the exclusive prefix over groups of
-// that class's row tiles; s_cls[a * kClsStride + num_groups] is the class
-// total.
-constexpr int kClsStride = kMaxGroups + 1;
-
-template <int MB>
-__device__ __forceinline__ void tile_classes(const int32_t *group_sizes, int num_groups, int go, int64_t e_local,
-                                             int *s_rowstart, int *s_cls) {
-  constexpr int MT = 32 * MB;
-  const int lane = threadIdx.x & 63;
-  if ((threadIdx.x >> 6) == 0) {
-    int row_carry = 0;
-    int carry[MB];
-#pragma unroll
-    for (int a = 0; a < MB; ++a) carry[a] = 0;
-    for (int base = 0; base < num_groups; base += 64) {
-      const int g = base + lane;
-      int sz = g < num_groups ? group_sizes[g] : 0;
-      sz = sz > 0 ? sz : 0;
-      const bool local = g >= go && (int64_t)g < (int64_t)go + e_local;
-      const int n_full = local ? sz / MT : 0;
-      const int rem = local ? sz % MT : 0;
-      const int rem_cls = (rem + 31) >> 5;  // 0 when there is no partial tile
-      const int ri = wave_inclusive_scan(sz);
-      if (g < num_groups) s_rowstart[g] = row_carry + ri - sz;
-      row_carry += __shfl(ri, 63, 64);
-#pragma unroll
-      for (int a = 0; a < MB; ++a) {
-        const int cnt = (a == 0 ? n_full : 0) + (rem_cls == MB - a ? 1 : 0);
-        const int ci = wave_inclusive_scan(cnt);
-        if (g < num_groups) s_cls[a * kClsStride + g] = carry[a] + ci - cnt;
-        carry[a] += __shfl(ci, 63, 64);
-      }
-    }
-    if (lane == 0) {
-#pragma unroll
-      for (int a = 0; a < MB; ++a) s_cls[a * kClsStride + num_groups] = carry[a];
-    }
-  }
-}
 
 // lhs tile rows hold 8 16-byte chunks; chunk c of row r sits at physical
 // chunk c ^ ((r >> 1) & 7), so that the 16 lanes of one LDS cycle (16
@@ -204,35 +156,6 @@ __device__ __forceinline__ void ws_producer(const uint16_t *__restrict__ lhs, co
   __builtin_amdgcn_s_barrier();
 }
 
-// silu_and_mul_with_clamp on one (gate, up) accumulator pair, in f32.
-__device__ __forceinline__ float silu_mul_clamp(float gate, float up) {
-  const float g = fminf(gate, kSwigluLimit);
-  const float u = fminf(fmaxf(up, -kSwigluLimit), kSwigluLimit);
-  return g / (1.0f + expf(-g)) * u;
-}
-
-// Stores 8 consecutive output values of one row (16-byte bf16 or 2 x 16-byte f32
-// stores), as streaming (non-temporal) vector stores: the output is read back
-// only by a later kernel.
-__device__ __forceinline__ void store8(void *__restrict__ out, int64_t o, const float *v, int out_f32) {
-  if (out_f32) {
-    u32x4_t lo, hi;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      lo[i] = __builtin_bit_cast(uint32_t, v[i]);
-      hi[i] = __builtin_bit_cast(uint32_t, v[4 + i]);
-    }
-    __builtin_nontemporal_store(lo, (u32x4_t *)((float *)out + o));
-    __builtin_nontemporal_store(hi, (u32x4_t *)((float *)out + o + 4));
-  } else {
-    u32x4_t p;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      p[i] = (uint32_t)f32_to_bf16_bits(v[2 * i]) | ((uint32_t)f32_to_bf16_bits(v[2 * i + 1]) << 16);
-    __builtin_nontemporal_store(p, (u32x4_t *)((uint16_t *)out + o));
-  }
-}
-
 template <class C, int AM, bool ACT>
 __device__ __forceinline__ void ws_consumer(int T, uint8_t *s_lds, int cw, int64_t row0, int rows,
                                             int64_t col0, int N, void *__restrict__ out, int out_f32) {
@@ -321,111 +244,8 @@ __device__ __forceinline__ void ws_consumer(int T, uint8_t *s_lds, int cw, int64
   __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
-  constexpr int ES = C::EP_STRIDE;
-  float *const ep = (float *)(s_lds + cw * 32 * ES * 4);
-  constexpr int CO = ACT ? 32 : 64;  // output columns of this wave
-  const int64_t n_out = ACT ? N / 2 : N;
-  const int64_t ocol0 = ACT ? col0 / 2 : col0;
-#pragma unroll
-  for (int mb = 0; mb < AM; ++mb) {
-    // The 32x32 accumulator layout: register r of lane (c32, h) is row
-    // 8 (r / 4) + 4 h + r % 4, column c32.
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int lr = 8 * (r >> 2) + 4 * h + (r & 3);
-      if constexpr (ACT) {
-        // Half 0 of the group is the gate, half 1 the up projection of the
-        // same 32 output columns (gate_up prepack).
-        ep[lr * ES + c32] = silu_mul_clamp(acc[mb][0][r], acc[mb][1][r]);
-      } else {
-        ep[lr * ES + c32] = acc[mb][0][r];
-        ep[lr * ES + 32 + c32] = acc[mb][1][r];
-      }
-    }
-    // Lane q of chunk i covers row q / (CO / 8), columns 8 (q % (CO / 8)) .. + 7.
-#pragma unroll
-    for (int i = 0; i < 32 * CO / 8 / 64; ++i) {
-      const int q = lane + 64 * i;
-      const int lr = q / (CO / 8), c8 = q % (CO / 8);
-      const int row = mb * 32 + lr;
-      const int64_t col = ocol0 + 8 * c8;
-      float v[8];
-      const f32x4_t lo = *(const f32x4_t *)(ep + lr * ES + 8 * c8);
-      const f32x4_t hi = *(const f32x4_t *)(ep + lr * ES + 8 * c8 + 4);
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        v[k] = lo[k];
-        v[4 + k] = hi[k];
-      }
-      if (row < rows && col < n_out) store8(out, (row0 + row) * n_out + col, v, out_f32);
-    }
-  }
-}
-
-// The block's tile: (local group g, rows row0 .. row0 + rows - 1) x column
-// tile nt.
-struct TileRef {
-  int g, rows, nt;
-  int64_t row0;
-};
-
-// Every thread of the block calls this (it holds two block barriers).  Work
-// list: the (row tile, column tile) pairs of class 0 (MB blocks), then class
-// 1, ... (longest first, so the dispatcher's in-order refill of free CUs
-// balances them).  Each class is cut into 8 contiguous runs, one per XCD
-// (blocks equal mod 8 run on one XCD), so a row tile's column tiles share
-// that XCD's L2.  Returns false when the block has no tile.
-template <int MB, int THREADS>
-__device__ __forceinline__ bool find_tile(const int32_t *__restrict__ group_sizes, int num_groups, int go,
-                                          int64_t e_local, int64_t M, int n_tiles, int *s_rowstart, int *s_cls,
-                                          int *s_info, TileRef &ref) {
-  constexpr int MT = 32 * MB;
-  const int tid = threadIdx.x;
-  tile_classes<MB>(group_sizes, num_groups, go, e_local, s_rowstart, s_cls);
-  if (tid == 0) s_info[0] = -1;
-  __syncthreads();
-  const int xcd = blockIdx.x & 7;
-  int64_t j = blockIdx.x >> 3;
-  int cls = -1;
-  int64_t entry = 0;
-#pragma unroll
-  for (int a = 0; a < MB; ++a) {
-    const int64_t n_a = (int64_t)s_cls[a * kClsStride + num_groups] * n_tiles;
-    const int64_t per = (n_a + 7) / 8;
-    const int64_t lo = xcd * per, hi = min(lo + per, n_a);
-    const int64_t len = hi > lo ? hi - lo : 0;
-    if (cls < 0) {
-      if (j < len) {
-        cls = a;
-        entry = lo + j;
-      } else {
-        j -= len;
-      }
-    }
-  }
-  const int trow = cls >= 0 ? (int)(entry / n_tiles) : -1;
-  if (cls >= 0) {
-    const int *const cs = s_cls + cls * kClsStride;
-    for (int g = tid; g < num_groups; g += THREADS) {
-      if (cs[g] <= trow && trow < cs[g + 1]) {
-        const int sz = group_sizes[g];
-        // Class 0 holds the full tiles (then a partial one of MB blocks);
-        // the other classes hold one partial tile per group.
-        const int tt = cls == 0 ? trow - cs[g] : sz / MT;
-        s_info[0] = g;
-        s_info[1] = s_rowstart[g] + tt * MT;
-        s_info[2] = min(MT, sz - tt * MT);
-      }
-    }
-  }
-  __syncthreads();  // also retires the class reads before the stages overwrite them
-  ref.g = s_info[0];
-  if (cls < 0 || ref.g < 0) return false;
-  ref.nt = (int)(entry % n_tiles);
-  ref.row0 = s_info[1];
-  if (ref.row0 >= M) return false;
-  ref.rows = (int)min((int64_t)s_info[2], M - ref.row0);
-  return true;
+  store_tile<AM, ACT, C::EP_STRIDE>(acc, (float *)(s_lds + cw * 32 * C::EP_STRIDE * 4), row0, rows, col0, N, out,
+                                     out_f32);
 }
 
 template <class C, int MB, bool ACT>
@@ -509,6 +329,13 @@ __global__ __launch_bounds__(256) void gmm_zero_rows_kernel(const int32_t *group
   }
 }
 
+int launch_gmm_zero_rows(const int32_t *group_sizes, int num_groups, const int32_t *group_offset, int64_t e_local,
+                         int64_t M, int64_t n_out, void *out, int elem_bytes, hipStream_t st) {
+  hipLaunchKernelGGL(gmm_zero_rows_kernel, dim3((unsigned)((M + 63) / 64)), dim3(256), 0, st, group_sizes, num_groups,
+                     group_offset, e_local, M, n_out, out, elem_bytes);
+  return launch_status("gmm zero rows");
+}
+
 template <int MB, int CW, int JW, int NP, int NS, bool ACT = false>
 static int launch_gmm_ws(const uint16_t *lhs, const int32_t *row_idx, int64_t lhs_rows, int64_t M, int64_t K,
                          const uint8_t *w, const uint8_t *s,
@@ -561,9 +388,7 @@ static int gmm_fp4_impl(const uint16_t *lhs, const int32_t *row_idx, int64_t lhs
   const int elem = out_dtype == DWM_F32 ? 4 : 2;
   if (zero_init) {
     const int64_t n_out = fuse_act != DWM_ACT_NONE ? N / 2 : N;
-    hipLaunchKernelGGL(gmm_zero_rows_kernel, dim3((unsigned)((M + 63) / 64)), dim3(256), 0, st,
-                       group_sizes, num_groups, group_offset, E_local, M, n_out, out, elem);
-    int rc = launch_status("gmm_fp4 zero rows");
+    int rc = launch_gmm_zero_rows(group_sizes, num_groups, group_offset, E_local, M, n_out, out, elem, st);
     if (rc != DWM_OK) return rc;
   }
   if (E_local == 0 || num_groups == 0) return DWM_OK;

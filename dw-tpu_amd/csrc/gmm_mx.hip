@@ -1,0 +1,453 @@
+// MX mode of the ragged grouped matmul: the lhs quantized to OCP e4m3 with
+// one e8m0 scale per 32 values along K, the prepacked e2m1 weights with their
+// e8m0 block-32 scales, contracted by the gfx950 scaled MFMA
+// v_mfma_scale_f32_32x32x64_f8f6f4 (A = e4m3, B = e2m1, both block scales
+// applied in the instruction), f32 accumulation.  This is gmm_v2 with
+// lhs_quant_dtype = float8_e4m3fn: the lhs quantization tokamax applies when
+// the chip has a native low-precision matrix path
+// (patches/tokamax/0001-gmm_v2-fp4-emulation-v6e.patch:89-100), with the
+// reference's own power-of-two block quantizer (quantize_tensor,
+// patches/tpu-inference/0001-dsv4-v6e-enablement.patch:315-350) at block 32.
+//
+// mx_quant_e4m3_kernel: bf16 [rows, K] -> e4m3 codes [rows, K] + e8m0 scale
+// codes [rows, K/32].  Per 32-value block: exponent e = the smallest with
+// absmax <= 448 * 2^e (from absmax's exponent and mantissa bits, no
+// rounding), clamped to >= -126; codes = RNE e4m3 of x * 2^-e (the gfx950
+// converter at unit scale, exact RNE); scale code e + 127.  A block holding
+// a NaN or an infinity gets codes 0x7F and scale code 255.
+//
+// gmm_mx_kernel: the tile scheduler, warp specialisation and epilogue of the
+// bf16 kernel (gmm_fp4.hip, gmm_tiles.h), with these data per 64-deep K step
+// of a 96 x 512 tile:
+//   A   96 rows x 64 bytes of e4m3 codes (chunk c of row r at physical chunk
+//       c ^ ((r >> 2) & 3): the 16 rows one LDS cycle reads hit 16 distinct
+//       16-byte bank groups);
+//   W   the 8 column groups' prepacked e2m1 codes, 2 KiB each (fp4.hip);
+// and, in even steps only (one dword covers a 128-deep block):
+//   AS  the lhs scale dword of each row (K-blocks 4 kb .. 4 kb + 3);
+//   S   the weight scale dword of each group lane (fp4.hip's scale layout).
+// The MFMA's operands need no conversion: lane (c, h) of a weight group's
+// 1 KiB half holds the 32 codes of column c at k = 32 h .. 32 h + 31 of the
+// step -- the e2m1 B operand of the 32x32x64 MFMA -- and byte 2 f + j of its
+// scale dword is that column's scale for K-block h of step 2 kb + f, the
+// MFMA's B scale (opsel j).  The e4m3 A operand of lane (r, h) is row r,
+// k = 16 h .. + 15 and 32 + 16 h .. + 15; its scale is row r's K-block h.
+#include "gmm_tiles.h"
+
+namespace dwm {
+
+typedef __attribute__((ext_vector_type(8))) int i32x8_t;
+
+constexpr int kMxBlock = 32;
+constexpr int kMxMinExp = -126;
+
+// ---------------------------------------------------------------------------
+// Quantization.  Thread i handles values 8 i .. 8 i + 7 of the flat [rows, K]
+// array; the 4 threads of a 32-value block are consecutive lanes.
+
+// The smallest e >= -126 with a <= 448 * 2^e, for finite a >= 0.
+__device__ __forceinline__ int mx_exponent(float a) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, a);
+  const int ef = (int)(u >> 23);
+  if (ef == 0) return kMxMinExp;  // zero or subnormal: far below 448 * 2^-126
+  // a = (1 + m / 2^23) 2^(ef - 127) <= 1.75 * 2^(8 + e)
+  const int e = ef - 127 - 8 + ((u & 0x7FFFFFu) > 0x600000u ? 1 : 0);
+  return e < kMxMinExp ? kMxMinExp : e;
+}
+
+__global__ __launch_bounds__(256) void mx_quant_e4m3_kernel(const uint16_t *__restrict__ x, int64_t n8,
+                                                            uint8_t *__restrict__ codes,
+                                                            uint8_t *__restrict__ scales) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  // n8 is a multiple of 4, so the 4 lanes of a block enter and leave the
+  // loop together and the quad shuffles read active lanes.
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n8; i += stride) {
+    const u32x4_t raw = __builtin_nontemporal_load((const u32x4_t *)(x + 8 * i));
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[2 * j] = bf16_bits_to_f32(raw[j] & 0xFFFFu);
+      v[2 * j + 1] = bf16_bits_to_f32(raw[j] >> 16);
+    }
+    float amax = 0.0f;
+    int bad = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float a = fabsf(v[j]);
+      bad |= !(a <= 3.4028234663852886e38f);  // NaN or infinity
+      amax = fmaxf(amax, bad ? 0.0f : a);
+    }
+    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+    bad |= __shfl_xor(bad, 1, 64);
+    bad |= __shfl_xor(bad, 2, 64);
+    const int e = mx_exponent(amax);
+    uint32_t w0 = 0x7F7F7F7Fu, w1 = 0x7F7F7F7Fu;
+    if (!bad) {
+      float q[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) q[j] = ldexpf(v[j], -e);  // exact: |q| <= 448
+      w0 = f32x4_e4m3(q);
+      w1 = f32x4_e4m3(q + 4);
+    }
+    typedef __attribute__((ext_vector_type(2))) uint32_t u32x2_t;
+    *(u32x2_t *)(codes + 8 * i) = u32x2_t{w0, w1};
+    if ((i & 3) == 0) scales[i >> 2] = (uint8_t)(bad ? 255 : e + 127);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// The MX tile kernel.
+
+template <int MB, int CW, int NP, int NS>
+struct MxCfg {
+  static constexpr int CONS = CW, NPROD = NP, STAGES = NS;
+  static constexpr int GT = CW;                          // 64-column groups per tile, one per consumer
+  static constexpr int THREADS = 64 * (CW + NP);
+  static constexpr int NT = 64 * GT;
+  static constexpr int ROWS = 32 * MB;
+  static constexpr int W = 0;                            // group i: 2 KiB at W + 2048 i
+  static constexpr int A = GT * 2048;                    // ROWS x 64 bytes
+  static constexpr int AS = A + ROWS * 64;               // 128-row groups x 256 bytes (dword per row)
+  static constexpr int AS_LOADS = (ROWS + 63) / 64;      // 256-byte row-scale loads per even step
+  static constexpr int S = AS + AS_LOADS * 256;          // group i: 256 bytes at S + 256 i
+  static constexpr int STAGE = S + GT * 256;
+  static constexpr int A_GROUPS = ROWS / 16;             // 1 KiB lhs loads (16 rows) per step
+  static constexpr int G_LOADS = GT / NP;                // weight groups per producer
+  static constexpr int AHEAD = 2;                        // steps published per barrier
+  static constexpr int EP_STRIDE = 72;
+  static_assert(ROWS % 16 == 0 && G_LOADS * NP == GT, "load split");
+  static_assert(AS_LOADS <= NP, "one row-scale load per producer at most");
+  // Two consecutive steps are one even and one odd step, so with two steps
+  // in flight behind the published pair every wait covers the same loads.
+  static_assert(NS - 1 - AHEAD == 2, "two steps in flight");
+  static_assert(CW * 32 * EP_STRIDE * 4 <= NS * STAGE, "epilogue staging fits the stages");
+};
+
+__device__ __forceinline__ int mx_swizzle(int r) { return (r >> 2) & 3; }
+
+// Producer wave pw: its lhs row groups are pw, pw + NP, ... (< A_GROUPS); NA
+// of them hold rows of the tile (the others are zero in every stage).
+// The last AS_LOADS producers (those with fewer lhs row groups) also load
+// row-scale dwords, 64 rows each.
+template <class C, int NA, bool ASL>
+__device__ __forceinline__ void mx_producer(const uint8_t *__restrict__ lhs, const uint8_t *__restrict__ lsc,
+                                            const int32_t *__restrict__ row_idx, int64_t lhs_rows, int64_t row0,
+                                            int rows, int K, int T, int KB, const uint8_t *__restrict__ wexp,
+                                            const uint8_t *__restrict__ sexp, int g0, int G, uint8_t *s_lds,
+                                            int pw) {
+  constexpr int NP = C::NPROD, NS = C::STAGES;
+  constexpr int MAXA = (C::A_GROUPS + NP - 1) / NP;
+  constexpr int L_ODD = NA + 2 * C::G_LOADS;
+  constexpr int L_EVEN = L_ODD + C::G_LOADS + (ASL ? 1 : 0);
+  constexpr int PENDING = L_EVEN + L_ODD;
+  static_assert(PENDING < 64, "vmcnt range");
+  const int lane = threadIdx.x & 63;
+  for (int i = NA; i < MAXA; ++i) {
+    const int ga = pw + NP * i;
+    if (ga < C::A_GROUPS) {
+#pragma unroll
+      for (int st = 0; st < NS; ++st)
+        *(u32x4_t *)(s_lds + st * C::STAGE + C::A + ga * 1024 + lane * 16) = u32x4_t{0u, 0u, 0u, 0u};
+    }
+  }
+  const int KS = K / kMxBlock;  // row-scale bytes per row
+  auto src_row = [&](int r) -> int64_t {
+    const int rs = r < rows ? r : rows - 1;
+    return row_idx ? gather_index(row_idx[row0 + rs], lhs_rows) : row0 + rs;
+  };
+  // lhs load i: rows 16 (pw + NP i) .. + 15; lane l fills physical chunk
+  // l % 4 of row + l / 4 with the logical chunk of the swizzle.
+  uint32_t aoff[NA > 0 ? NA : 1];
+#pragma unroll
+  for (int i = 0; i < NA; ++i) {
+    const int r = 16 * (pw + NP * i) + (lane >> 2);
+    aoff[i] = (uint32_t)(src_row(r) * K) + (uint32_t)(((lane & 3) ^ mx_swizzle(r)) << 4);
+  }
+  const int aspart = pw - (NP - C::AS_LOADS);  // row-scale load of producers NP - AS_LOADS .. NP - 1
+  const uint32_t asoff = ASL ? (uint32_t)(src_row(64 * aspart + lane) * KS) : 0u;
+  const uint8_t *wsrc[C::G_LOADS];
+  const uint8_t *ssrc[C::G_LOADS];
+#pragma unroll
+  for (int c = 0; c < C::G_LOADS; ++c) {
+    const int g = min(g0 + pw + NP * c, G - 1);  // groups past N feed unstored columns
+    wsrc[c] = wexp + (int64_t)g * T * 2048 + lane * 16;
+    ssrc[c] = sexp + (int64_t)g * KB * 256 + lane * 4;
+  }
+  auto issue = [&](int stage, int t) {
+    uint8_t *const st = s_lds + stage * C::STAGE;
+    const uint8_t *const a = lhs + (int64_t)t * 64;
+#pragma unroll
+    for (int i = 0; i < NA; ++i)
+      __builtin_amdgcn_global_load_lds((const void *)(a + aoff[i]),
+                                       (lds_void_t *)(st + C::A + (pw + NP * i) * 1024), 16, 0, 0);
+#pragma unroll
+    for (int c = 0; c < C::G_LOADS; ++c) {
+      const int gi = pw + NP * c;
+      const uint8_t *const w = wsrc[c] + (int64_t)t * 2048;
+      __builtin_amdgcn_global_load_lds((const void *)w, (lds_void_t *)(st + C::W + gi * 2048), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void *)(w + 1024), (lds_void_t *)(st + C::W + gi * 2048 + 1024), 16,
+                                       0, 0);
+    }
+    if ((t & 1) == 0) {
+#pragma unroll
+      for (int c = 0; c < C::G_LOADS; ++c)
+        __builtin_amdgcn_global_load_lds((const void *)(ssrc[c] + (int64_t)(t >> 1) * 256),
+                                         (lds_void_t *)(st + C::S + (pw + NP * c) * 256), 4, 0, 0);
+      if (ASL)
+        __builtin_amdgcn_global_load_lds((const void *)(lsc + asoff + (t >> 1) * 4),
+                                         (lds_void_t *)(st + C::AS + aspart * 256), 4, 0, 0);
+    }
+  };
+  // Steps past the last one repeat the last step of the same parity, so
+  // every pair of consecutive steps issues the same loads.
+  auto clampt = [&](int t) { return t < T ? t : T - 2 + (t & 1); };
+#pragma unroll
+  for (int t = 0; t < NS - 1; ++t) issue(t, clampt(t));
+  int refill = NS - 1;
+  for (int t = 0; t < T; ++t) {
+    // Steps t, t + 1 have landed once at most the loads of t + 2, t + 3
+    // (one even, one odd step) are pending.
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(PENDING));
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    issue(refill, clampt(t + NS - 1));
+    refill = refill == NS - 1 ? 0 : refill + 1;
+  }
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+}
+
+template <class C, int AM, bool ACT>
+__device__ __forceinline__ void mx_consumer(int T, uint8_t *s_lds, int cw, int64_t row0, int rows, int64_t col0,
+                                            int N, void *__restrict__ out, int out_f32) {
+  constexpr int NS = C::STAGES;
+  const int lane = threadIdx.x & 63, c32 = lane & 31, h = lane >> 5;
+  f32x16_t acc[AM][2];
+#pragma unroll
+  for (int mb = 0; mb < AM; ++mb)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[mb][j][r] = 0.0f;
+  const int woff = C::W + cw * 2048 + lane * 16;
+  const int soff = C::S + cw * 256 + lane * 4;
+  // A fragment of row block mb: row mb * 32 + c32 (same swizzle for all mb),
+  // logical chunks h and 2 + h.
+  const int sw = mx_swizzle(c32);
+  const int alo = C::A + c32 * 64 + ((h ^ sw) << 4);
+  const int ahi = C::A + c32 * 64 + (((2 + h) ^ sw) << 4);
+  u32x4_t wn[2];
+  uint32_t sn = 0, asn[AM];
+  i32x8_t an;
+  auto read_w = [&](const uint8_t *st) {
+    wn[0] = *(const u32x4_t *)(st + woff);
+    wn[1] = *(const u32x4_t *)(st + woff + 1024);
+  };
+  auto read_s = [&](const uint8_t *st) {  // even steps: scale dwords of this and the next step
+    sn = *(const uint32_t *)(st + soff);
+#pragma unroll
+    for (int mb = 0; mb < AM; ++mb) asn[mb] = *(const uint32_t *)(st + C::AS + (mb * 32 + c32) * 4);
+  };
+  auto read_a = [&](const uint8_t *st, int mb) {
+    const u32x4_t lo = *(const u32x4_t *)(st + alo + mb * 32 * 64);
+    const u32x4_t hi = *(const u32x4_t *)(st + ahi + mb * 32 * 64);
+    an = i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+  };
+  uint32_t sw_cur = 0, sa_cur[AM];
+#pragma unroll
+  for (int mb = 0; mb < AM; ++mb) sa_cur[mb] = 0;
+  int cur = 0;
+  for (int t = 0; t < T; ++t) {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    const uint8_t *const st = s_lds + cur * C::STAGE;
+    const int nxt = cur == NS - 1 ? 0 : cur + 1;
+    // Step t + 1 was published at this barrier and its stage is not
+    // refilled before the next one.
+    const uint8_t *const sx = s_lds + nxt * C::STAGE;
+    if (t == 0) {
+      read_w(st);
+      read_s(st);
+      read_a(st, 0);
+    }
+    const u32x4_t w0 = wn[0], w1 = wn[1];
+    if ((t & 1) == 0) {
+      sw_cur = sn;
+#pragma unroll
+      for (int mb = 0; mb < AM; ++mb) sa_cur[mb] = asn[mb];
+    }
+    // Bytes 2 f + j of the weight scale dword (opsel j), byte 2 f + h of a
+    // row's scale dword, f = t & 1.
+    const int sh = 16 * (t & 1);
+    const int sb = sw_cur >> sh;
+    const i32x8_t b0 = {(int)w0[0], (int)w0[1], (int)w0[2], (int)w0[3], 0, 0, 0, 0};
+    const i32x8_t b1 = {(int)w1[0], (int)w1[1], (int)w1[2], (int)w1[3], 0, 0, 0, 0};
+#pragma unroll
+    for (int mb = 0; mb < AM; ++mb) {
+      const i32x8_t a = an;
+      const int sa = (int)((sa_cur[mb] >> (sh + 8 * h)) & 0xFFu);
+      __builtin_amdgcn_sched_barrier(0);
+      if (mb + 1 < AM) {
+        read_a(st, mb + 1);
+      } else {
+        read_a(sx, 0);
+      }
+      if (mb == 0) {
+        read_w(sx);
+        if ((t & 1) == 1) read_s(sx);
+      }
+      acc[mb][0] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b0, acc[mb][0], 0, 4, 0, sa, 0, sb);
+      acc[mb][1] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b1, acc[mb][1], 0, 4, 0, sa, 1, sb);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    cur = nxt;
+  }
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  store_tile<AM, ACT, C::EP_STRIDE>(acc, (float *)(s_lds + cw * 32 * C::EP_STRIDE * 4), row0, rows, col0, N, out,
+                                    out_f32);
+}
+
+template <class C, int MB, bool ACT>
+__global__ __launch_bounds__(C::THREADS) void gmm_mx_kernel(
+    const uint8_t *__restrict__ lhs, const uint8_t *__restrict__ lsc, const int32_t *__restrict__ row_idx,
+    int64_t lhs_rows, int64_t M, int K, const uint8_t *__restrict__ wpk, const uint8_t *__restrict__ spk,
+    const int32_t *__restrict__ group_sizes, int num_groups, const int32_t *__restrict__ group_offset,
+    int64_t e_local, int N, void *__restrict__ out, int out_f32) {
+  constexpr int CW = C::CONS, NP = C::NPROD;
+  static_assert(C::STAGES * C::STAGE >= (kMaxGroups + MB * kClsStride) * 4, "tile classes alias the stages");
+  __shared__ __attribute__((aligned(1024))) uint8_t s_lds[C::STAGES * C::STAGE];
+  __shared__ int s_info[3];
+  int *s_rowstart = (int *)s_lds;
+  int *s_cls = s_rowstart + kMaxGroups;
+
+  const int tid = threadIdx.x, wave = tid >> 6;
+  const int go = group_offset ? group_offset[0] : 0;
+  TileRef ref;
+  if (!find_tile<MB, C::THREADS>(group_sizes, num_groups, go, e_local, M, (N + C::NT - 1) / C::NT, s_rowstart,
+                                 s_cls, s_info, ref))
+    return;
+  const int g = ref.g, nt = ref.nt, rows = ref.rows;
+  const int64_t row0 = ref.row0;
+  const int64_t e = g - go;
+  const int T = K >> 6, KB = K >> 7, G = (N + 63) >> 6;
+  const int g0 = nt * C::GT;
+  if (wave >= CW) {
+    const int pw = wave - CW;
+    const uint8_t *const wexp = wpk + e * G * T * 2048;
+    const uint8_t *const sexp = spk + e * G * KB * 256;
+    // Row groups pw + NP i (i < MAXA, < A_GROUPS) with 16 (pw + NP i) < rows are loaded.
+    int na = 0;
+    for (int ga = pw; ga < C::A_GROUPS; ga += NP) na += 16 * ga < rows ? 1 : 0;
+    const bool asl = pw >= NP - C::AS_LOADS;
+    auto run = [&](auto na_c, auto asl_c) {
+      mx_producer<C, decltype(na_c)::value, decltype(asl_c)::value != 0>(lhs, lsc, row_idx, lhs_rows, row0, rows, K,
+                                                                          T, KB, wexp, sexp, g0, G, s_lds, pw);
+    };
+    // A_GROUPS = 6 over 4 producers: producers 0, 1 own two row groups, 2, 3 one.
+    static_assert(C::A_GROUPS <= 2 * NP, "at most two lhs row groups per producer");
+    if (asl) {
+      if (na >= 2) run(IntC<2>{}, IntC<1>{});
+      else if (na == 1) run(IntC<1>{}, IntC<1>{});
+      else run(IntC<0>{}, IntC<1>{});
+    } else {
+      if (na >= 2) run(IntC<2>{}, IntC<0>{});
+      else if (na == 1) run(IntC<1>{}, IntC<0>{});
+      else run(IntC<0>{}, IntC<0>{});
+    }
+    return;
+  }
+  const int act_mb = (rows + 31) >> 5;
+  const int64_t col0 = (int64_t)(g0 + wave) * 64;
+  if (act_mb <= 1 || MB == 1) mx_consumer<C, 1, ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32);
+  else if (act_mb == 2 || MB == 2) mx_consumer<C, (MB >= 2 ? 2 : 1), ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32);
+  else mx_consumer<C, MB, ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32);
+}
+
+template <int MB, int CW, int NP, int NS, bool ACT>
+static int launch_gmm_mx(const uint8_t *lhs, const uint8_t *lsc, const int32_t *row_idx, int64_t lhs_rows, int64_t M,
+                         int64_t K, const uint8_t *w, const uint8_t *s, const int32_t *gs, int ng, const int32_t *go,
+                         int64_t e_local, int64_t N, void *out, int out_f32, hipStream_t st) {
+  using C = MxCfg<MB, CW, NP, NS>;
+  constexpr int MT = 32 * MB, NT = C::NT;
+  const int64_t n_tiles = (N + NT - 1) / NT;
+  const int64_t max_tiles = ((M + MT - 1) / MT + e_local) * n_tiles;
+  const int64_t grid = ((max_tiles + 7) / 8 + MB) * 8;
+  DWM_UNSUPPORTED_IF(grid > (1ll << 31) - 1, "gmm_fp4_mx: too many tiles (%lld)", (long long)grid);
+  hipLaunchKernelGGL((gmm_mx_kernel<C, MB, ACT>), dim3((unsigned)grid), dim3(C::THREADS), 0, st, lhs, lsc, row_idx,
+                     lhs_rows, M, (int)K, w, s, gs, ng, go, e_local, (int)N, out, out_f32);
+  return launch_status("gmm_fp4_mx");
+}
+
+}  // namespace dwm
+
+using namespace dwm;
+
+extern "C" int dwm_mx_quant_e4m3(const uint16_t *x, int64_t rows, int64_t K, uint8_t *codes, uint8_t *scales,
+                                 void *stream) {
+  clear_error();
+  DWM_CHECK_ARG(rows >= 0 && K > 0, "mx_quant_e4m3: bad sizes rows=%lld K=%lld", (long long)rows, (long long)K);
+  DWM_UNSUPPORTED_IF(K % kMxBlock != 0, "mx_quant_e4m3: K %% 32 == 0 required (K=%lld)", (long long)K);
+  if (rows == 0) return DWM_OK;
+  DWM_CHECK_ARG(x && codes && scales, "mx_quant_e4m3: null pointer");
+  DWM_CHECK_ARG((uintptr_t)x % 16 == 0 && (uintptr_t)codes % 8 == 0,
+                "mx_quant_e4m3: x must be 16-byte and codes 8-byte aligned");
+  const int64_t n8 = rows * K / 8;
+  int64_t blocks = (n8 + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  hipLaunchKernelGGL(mx_quant_e4m3_kernel, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream), x, n8, codes,
+                     scales);
+  return launch_status("mx_quant_e4m3");
+}
+
+extern "C" int dwm_gmm_fp4_mx(const uint8_t *lhs, const uint8_t *lhs_scale, int64_t lhs_rows, const int32_t *row_idx,
+                              int64_t M, int64_t K, const uint8_t *weight, const uint8_t *scale,
+                              const int32_t *group_sizes, int num_groups, const int32_t *group_offset, int64_t E_local,
+                              int64_t N, void *out, int out_dtype, int zero_init, int fuse_act, void *stream) {
+  clear_error();
+  DWM_CHECK_ARG(M >= 0 && K > 0 && N > 0 && E_local >= 0 && num_groups >= 0 && lhs_rows >= 0,
+                "gmm_fp4_mx: bad sizes M=%lld K=%lld N=%lld E_local=%lld groups=%d lhs_rows=%lld", (long long)M,
+                (long long)K, (long long)N, (long long)E_local, num_groups, (long long)lhs_rows);
+  DWM_CHECK_ARG(out_dtype == DWM_BF16 || out_dtype == DWM_F32, "gmm_fp4_mx: bad out dtype %d", out_dtype);
+  DWM_CHECK_ARG(fuse_act == DWM_ACT_NONE || fuse_act == DWM_ACT_SILU_MUL_CLAMP, "gmm_fp4_mx: bad fuse_act %d",
+                fuse_act);
+  DWM_CHECK_ARG(row_idx || lhs_rows == M, "gmm_fp4_mx: without row_idx lhs must have M rows (%lld != %lld)",
+                (long long)lhs_rows, (long long)M);
+  DWM_UNSUPPORTED_IF(fuse_act != DWM_ACT_NONE && N % 64 != 0, "gmm_fp4_mx: fuse_act needs N %% 64 == 0 (N=%lld)",
+                     (long long)N);
+  DWM_UNSUPPORTED_IF(K % 128 != 0 || N % 16 != 0, "gmm_fp4_mx: K %% 128 == 0 and N %% 16 == 0 required");
+  DWM_UNSUPPORTED_IF(num_groups > kMaxGroups, "gmm_fp4_mx: at most %d groups (got %d)", kMaxGroups, num_groups);
+  DWM_UNSUPPORTED_IF(K > (1 << 24) || N > (1 << 30), "gmm_fp4_mx: K <= 2^24, N < 2^30 required");
+  if (M == 0) return DWM_OK;
+  DWM_CHECK_ARG(lhs && lhs_scale && out && (num_groups == 0 || group_sizes) && (!row_idx || lhs_rows > 0),
+                "gmm_fp4_mx: null pointer or empty lhs");
+  // lhs rows are addressed with 32-bit byte offsets.
+  DWM_UNSUPPORTED_IF(lhs_rows * K >= (1ll << 32), "gmm_fp4_mx: lhs of %lld rows is too large", (long long)lhs_rows);
+  DWM_CHECK_ARG(E_local == 0 || (weight && scale), "gmm_fp4_mx: null weight pointer");
+  DWM_CHECK_ARG((uintptr_t)lhs % 16 == 0 && (uintptr_t)weight % 16 == 0 && (uintptr_t)out % 16 == 0 &&
+                    (uintptr_t)scale % 4 == 0 && (uintptr_t)lhs_scale % 4 == 0,
+                "gmm_fp4_mx: lhs, weight and out must be 16-byte aligned, the scales 4-byte aligned");
+  hipStream_t st = as_stream(stream);
+  const int elem = out_dtype == DWM_F32 ? 4 : 2;
+  if (zero_init) {
+    const int64_t n_out = fuse_act != DWM_ACT_NONE ? N / 2 : N;
+    int rc = launch_gmm_zero_rows(group_sizes, num_groups, group_offset, E_local, M, n_out, out, elem, st);
+    if (rc != DWM_OK) return rc;
+  }
+  if (E_local == 0 || num_groups == 0) return DWM_OK;
+  const int out_f32 = out_dtype == DWM_F32;
+  // 96-row x 512-column tiles, 8 consumer + 4 producer waves, five 64-deep
+  // K stages (two published per barrier, two in flight).
+  if (fuse_act == DWM_ACT_SILU_MUL_CLAMP)
+    return launch_gmm_mx<3, 8, 4, 5, true>(lhs, lhs_scale, row_idx, lhs_rows, M, K, weight, scale, group_sizes,
+                                           num_groups, group_offset, E_local, N, out, out_f32, st);
+  return launch_gmm_mx<3, 8, 4, 5, false>(lhs, lhs_scale, row_idx, lhs_rows, M, K, weight, scale, group_sizes,
+                                          num_groups, group_offset, E_local, N, out, out_f32, st);
+}

@@ -35,6 +35,8 @@ SIGNATURES = {
     "dwm_gmm_fp4_prepack_gate_up": [_p, _i32, _p, _i32, _i64, _i64, _i64, _p, _p, _p, _p],
     "dwm_gmm_fp4": [_p, _i64, _i64, _p, _p, _p, _i32, _p, _i64, _i64, _p, _i32, _i32, _i32, _p],
     "dwm_gmm_fp4_gather": [_p, _i64, _p, _i64, _i64, _p, _p, _p, _i32, _p, _i64, _i64, _p, _i32, _i32, _i32, _p],
+    "dwm_mx_quant_e4m3": [_p, _i64, _i64, _p, _p, _p],
+    "dwm_gmm_fp4_mx": [_p, _p, _i64, _p, _i64, _i64, _p, _p, _p, _i32, _p, _i64, _i64, _p, _i32, _i32, _i32, _p],
     "dwm_moe_dispatch_workspace_size": [_i64, _i32, _p],
     "dwm_moe_dispatch": [_p, _i64, _i32, _i32, _p, _p, _p, _p, _p, _p, _p, _p],
     "dwm_row_gather": [_p, _i64, _i64, _p, _i64, _p, _p],

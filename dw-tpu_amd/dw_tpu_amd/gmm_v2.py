@@ -15,6 +15,16 @@ over all experts, as the reference's per-call re-encoding is).
 Tensor conventions (torch has no uint4): a 4-bit array of shape [..., N] is a
 uint8 tensor [..., N/2] with element 2j in the low nibble, or a
 ``torch.float4_e2m1fn_x2`` tensor of the same bytes.
+
+MX mode.  ``gmm_v2(..., lhs_quant_dtype=torch.float8_e4m3fn)`` quantizes the
+lhs to e4m3 with one e8m0 scale per 32 values along K (``mx_quantize``: the
+reference's power-of-two block quantizer, quantize_tensor in
+patches/tpu-inference/0001-dsv4-v6e-enablement.patch:315-350, at block 32)
+and contracts it with the fp4 weights on the gfx950 scaled MFMA -- the lhs
+quantization tokamax performs for chips with a native low-precision matrix
+path (patches/tokamax/0001-...:89-100).  An ``MxLhs`` (already quantized)
+may be passed as ``lhs`` directly.  The default (no lhs_quant_dtype) keeps
+the reference's W4A16 arithmetic: bf16 lhs, weights decoded exactly.
 """
 import ctypes
 from dataclasses import dataclass
@@ -24,6 +34,52 @@ import torch
 from . import _lib
 
 FP4_DTYPES = tuple(t for t in (getattr(torch, "float4_e2m1fn_x2", None),) if t is not None)
+E4M3 = torch.float8_e4m3fn
+MX_BLOCK = 32
+
+
+@dataclass(frozen=True)
+class MxLhs:
+    """An lhs quantized for the MX mode: ``codes`` uint8 [rows, K] (e4m3 bit
+    patterns) and ``scales`` uint8 [rows, K/32] (e8m0 exponent codes, value
+    2^(code - 127))."""
+    codes: torch.Tensor
+    scales: torch.Tensor
+
+    @property
+    def shape(self):
+        return tuple(self.codes.shape)
+
+    @property
+    def device(self):
+        return self.codes.device
+
+    def dequantize(self) -> torch.Tensor:
+        """The float32 values the codes and scales stand for (exact)."""
+        v = self.codes.view(E4M3).float()
+        s = torch.ldexp(torch.ones((), device=self.scales.device), self.scales.to(torch.int32) - 127)
+        rows, k = self.codes.shape
+        return (v.view(rows, k // MX_BLOCK, MX_BLOCK) * s[..., None]).view(rows, k)
+
+
+def mx_quantize(x: torch.Tensor) -> MxLhs:
+    """bf16 [rows, K] -> ``MxLhs``: per 32-value block along K, scale 2^e with
+    e the smallest exponent such that absmax <= 448 * 2^e (at least -126),
+    codes = e4m3 of x * 2^-e rounded to nearest even; a block with a NaN or
+    infinity gets NaN codes and scale code 255.  One device pass."""
+    if x.dtype != torch.bfloat16 or x.dim() != 2:
+        raise ValueError(f"mx_quantize: expected a 2-D bfloat16 tensor, got {x.dtype} {tuple(x.shape)}")
+    rows, k = x.shape
+    if k % MX_BLOCK:
+        raise ValueError(f"mx_quantize: K={k} must be a multiple of {MX_BLOCK}")
+    x = x.contiguous()
+    if x.data_ptr() % 16:
+        x = x.clone()
+    dev = _lib.require_cuda(x)
+    codes = torch.empty((rows, k), dtype=torch.uint8, device=dev)
+    scales = torch.empty((rows, k // MX_BLOCK), dtype=torch.uint8, device=dev)
+    _lib.call("dwm_mx_quant_e4m3", _lib.ptr(x), rows, k, _lib.ptr(codes), _lib.ptr(scales), _lib.stream_handle(dev))
+    return MxLhs(codes, scales)
 
 
 def needs_fp4_emulation(dtype) -> bool:
@@ -177,7 +233,7 @@ def gmm_v2(lhs: torch.Tensor,
            lhs_row_indices: torch.Tensor = None) -> torch.Tensor:
     """Ragged grouped matmul: out[rows of g] = lhs[rows of g] @ dequant(rhs[g - group_offset]).
 
-    lhs: [M, K] bf16, rows sorted by group.  rhs: ``Fp4Weight`` (prepacked)
+    lhs: [M, K] bf16, rows sorted by group (or an ``MxLhs``: the MX mode).  rhs: ``Fp4Weight`` (prepacked)
     or packed fp4 bytes [E, K, N/2] (prepacked per call).  group_sizes:
     int32 [G] device tensor.  group_offset: None, an int, or an int32 [1]
     device tensor (first local group).  Returns [M, N] in
@@ -194,6 +250,12 @@ def gmm_v2(lhs: torch.Tensor,
     semantics), read by the kernel directly -- the dispatch row gather fused
     into the matmul.  ``lhs`` is then the source [rows, K] and the result has
     M = len(lhs_row_indices) rows.
+
+    ``lhs_quant_dtype=torch.float8_e4m3fn`` selects the MX mode (module
+    docstring): the lhs is quantized with ``mx_quantize`` (unless it is an
+    ``MxLhs`` already) and each product is e4m3 x e2m1 with both block scales,
+    on the scaled MFMA.  ``rhs_quant_dtype`` is accepted and ignored (the rhs
+    is fp4 either way).
     """
     if rhs_bias is not None:
         raise NotImplementedError("gmm_v2: rhs_bias is not supported by the fp4 kernel")
@@ -202,8 +264,9 @@ def gmm_v2(lhs: torch.Tensor,
     fused = fuse_act is not None
     if transpose_rhs:
         raise NotImplementedError("gmm_v2: transpose_rhs is not supported")
-    if lhs_quant_dtype is not None:
-        raise NotImplementedError("gmm_v2: lhs quantization is not supported with fp4 codes")
+    if lhs_quant_dtype is not None and lhs_quant_dtype not in (E4M3, "float8_e4m3fn"):
+        raise NotImplementedError(f"gmm_v2: lhs_quant_dtype {lhs_quant_dtype!r}: only float8_e4m3fn (MX) is supported")
+    mx = lhs_quant_dtype is not None or isinstance(lhs, MxLhs)
     if isinstance(rhs, Fp4Weight):
         if rhs_scale is not None:
             raise ValueError("gmm_v2: a prepacked Fp4Weight carries its own scales; pass rhs_scale=None")
@@ -213,19 +276,30 @@ def gmm_v2(lhs: torch.Tensor,
     if w.gate_up != fused:
         raise ValueError("gmm_v2: gate/up-prepacked weights run only (and always) with the fused activation"
                          if w.gate_up else "gmm_v2: the fused activation needs weights prepacked with gate_up=True")
-    out_dtype = lhs.dtype if preferred_element_type is None else preferred_element_type
-    if lhs.dtype != torch.bfloat16:
-        raise ValueError(f"gmm_v2: lhs must be bfloat16, got {lhs.dtype}")
+    if isinstance(lhs, MxLhs):
+        out_dtype = torch.bfloat16 if preferred_element_type is None else preferred_element_type
+    else:
+        if lhs.dtype != torch.bfloat16:
+            raise ValueError(f"gmm_v2: lhs must be bfloat16, got {lhs.dtype}")
+        out_dtype = lhs.dtype if preferred_element_type is None else preferred_element_type
     if out_dtype not in (torch.bfloat16, torch.float32):
         raise ValueError(f"gmm_v2: preferred_element_type must be bfloat16 or float32, got {out_dtype}")
-    if lhs.dim() != 2 or lhs.shape[1] != w.k:
+    if len(lhs.shape) != 2 or lhs.shape[1] != w.k:
         raise ValueError(f"gmm_v2: lhs shape {tuple(lhs.shape)} does not match rhs K={w.k}")
     if group_sizes.dtype != torch.int32 or group_sizes.dim() != 1:
         raise ValueError("gmm_v2: group_sizes must be a 1-D int32 tensor")
-    dev = _lib.require_cuda(lhs, w.weight, group_sizes)
-    lhs = lhs.contiguous()
-    if lhs.data_ptr() % 16:
-        lhs = lhs.clone()  # the kernel streams 16-byte rows
+    if mx and not isinstance(lhs, MxLhs):
+        lhs = mx_quantize(lhs)
+    if isinstance(lhs, MxLhs):
+        if lhs.codes.dtype != torch.uint8 or lhs.scales.dtype != torch.uint8 or \
+                tuple(lhs.scales.shape) != (lhs.shape[0], w.k // MX_BLOCK):
+            raise ValueError("gmm_v2: MxLhs needs uint8 codes [rows, K] and uint8 scales [rows, K/32]")
+        dev = _lib.require_cuda(lhs.codes, lhs.scales, w.weight, group_sizes)
+    else:
+        dev = _lib.require_cuda(lhs, w.weight, group_sizes)
+        lhs = lhs.contiguous()
+        if lhs.data_ptr() % 16:
+            lhs = lhs.clone()  # the kernel streams 16-byte rows
     gs = group_sizes.contiguous()
     if group_offset is None:
         go = None
@@ -234,21 +308,22 @@ def gmm_v2(lhs: torch.Tensor,
     else:
         go = group_offset.reshape(-1)[:1].to(device=dev, dtype=torch.int32).contiguous()
     act = _lib.ACT_SILU_MUL_CLAMP if fused else _lib.ACT_NONE
-    if lhs_row_indices is None:
-        m = lhs.shape[0]
-        out = torch.empty((m, w.n // 2 if fused else w.n), dtype=out_dtype, device=dev)
-        _lib.call("dwm_gmm_fp4", _lib.ptr(lhs), m, w.k, _lib.ptr(w.weight), _lib.ptr(w.scale), _lib.ptr(gs),
-                  gs.numel(), _lib.ptr(go), w.num_experts, w.n, _lib.ptr(out), _lib.dtype_code(out_dtype),
-                  1 if zero_initialize else 0, act, _lib.stream_handle(dev))
-        return out
     idx = lhs_row_indices
-    if idx.dtype != torch.int32 or idx.dim() != 1:
-        raise ValueError("gmm_v2: lhs_row_indices must be a 1-D int32 tensor")
-    _lib.require_cuda(idx)
-    idx = idx.contiguous()
-    m = idx.numel()
+    if idx is not None:
+        if idx.dtype != torch.int32 or idx.dim() != 1:
+            raise ValueError("gmm_v2: lhs_row_indices must be a 1-D int32 tensor")
+        _lib.require_cuda(idx)
+        idx = idx.contiguous()
+    m = lhs.shape[0] if idx is None else idx.numel()
     out = torch.empty((m, w.n // 2 if fused else w.n), dtype=out_dtype, device=dev)
-    _lib.call("dwm_gmm_fp4_gather", _lib.ptr(lhs), lhs.shape[0], _lib.ptr(idx), m, w.k, _lib.ptr(w.weight),
-              _lib.ptr(w.scale), _lib.ptr(gs), gs.numel(), _lib.ptr(go), w.num_experts, w.n, _lib.ptr(out),
-              _lib.dtype_code(out_dtype), 1 if zero_initialize else 0, act, _lib.stream_handle(dev))
+    tail = (_lib.ptr(w.weight), _lib.ptr(w.scale), _lib.ptr(gs), gs.numel(), _lib.ptr(go), w.num_experts, w.n,
+            _lib.ptr(out), _lib.dtype_code(out_dtype), 1 if zero_initialize else 0, act, _lib.stream_handle(dev))
+    if mx:
+        codes = lhs.codes.contiguous()
+        scales = lhs.scales.contiguous()
+        _lib.call("dwm_gmm_fp4_mx", _lib.ptr(codes), _lib.ptr(scales), codes.shape[0], _lib.ptr(idx), m, w.k, *tail)
+    elif idx is None:
+        _lib.call("dwm_gmm_fp4", _lib.ptr(lhs), m, w.k, *tail)
+    else:
+        _lib.call("dwm_gmm_fp4_gather", _lib.ptr(lhs), lhs.shape[0], _lib.ptr(idx), m, w.k, *tail)
     return out

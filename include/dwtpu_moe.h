@@ -169,6 +169,39 @@ int dwm_gmm_fp4_gather(const uint16_t *lhs, int64_t lhs_rows, const int32_t *row
                        int zero_init, int fuse_act, void *stream);
 
 /* ---------------------------------------------------------------------- */
+/* MX mode: e4m3 activations with e8m0 block-32 scales (scaled MFMA).      */
+/* ---------------------------------------------------------------------- */
+
+/* bf16 x [rows, K] -> e4m3 codes [rows, K] and e8m0 scale codes
+ * [rows, K/32]: the reference's power-of-two block quantizer
+ * quantize_tensor(e4m3, x, axis=-1, 32, power_of_two_scale=True)
+ * (patches/tpu-inference/0001-dsv4-v6e-enablement.patch:315-350) applied to
+ * the gmm lhs, as gmm_v2 quantizes its lhs for a native low-precision matrix
+ * path (lhs_quant_dtype, patches/tokamax/0001-gmm_v2-fp4-emulation-v6e.patch:
+ * 89-100).  Per 32-value block: scale 2^e with e the smallest exponent such
+ * that absmax <= 448 * 2^e, kept >= -126; codes = e4m3 of x * 2^-e, round to
+ * nearest even; scale code = e + 127 (codes 1..254).  A block holding a NaN
+ * or infinity gets codes 0x7F (NaN) and scale code 255.  Bit-exact.
+ * Requires K % 32 == 0; x 16-byte and codes 8-byte aligned. */
+int dwm_mx_quant_e4m3(const uint16_t *x, int64_t rows, int64_t K, uint8_t *codes, uint8_t *scales,
+                      void *stream);
+
+/* The grouped matmul of dwm_gmm_fp4 / dwm_gmm_fp4_gather on MX operands:
+ * lhs e4m3 codes [lhs_rows, K] with e8m0 scales lhs_scale [lhs_rows, K/32]
+ * (dwm_mx_quant_e4m3), the same prepacked weights, one gfx950 scaled MFMA
+ * (e4m3 x e2m1, 32x32x64, both block scales in the instruction) per 64-deep
+ * K step, f32 accumulation.  Every product e4m3 * 2^a * e2m1 * 2^b is exact;
+ * the result differs from dwm_gmm_fp4's by the lhs quantization.  Row r of
+ * the grouped operand is row r of lhs, or row row_idx[r] (JAX gather
+ * semantics) when row_idx is not NULL (then lhs_rows may differ from M).
+ * Other arguments and rules as dwm_gmm_fp4; lhs_rows * K < 2^32; lhs_scale
+ * 4-byte aligned.  Replaces gmm_v2(..., lhs_quant_dtype=float8_e4m3fn). */
+int dwm_gmm_fp4_mx(const uint8_t *lhs, const uint8_t *lhs_scale, int64_t lhs_rows, const int32_t *row_idx,
+                   int64_t M, int64_t K, const uint8_t *weight, const uint8_t *scale,
+                   const int32_t *group_sizes, int num_groups, const int32_t *group_offset, int64_t E_local,
+                   int64_t N, void *out, int out_dtype, int zero_init, int fuse_act, void *stream);
+
+/* ---------------------------------------------------------------------- */
 /* MoE dispatch and combine.                                               */
 /* ---------------------------------------------------------------------- */
 

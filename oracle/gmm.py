@@ -141,3 +141,45 @@ def acceptance_policy(y, y_base, y64, mask=None):
     mx, mx_b = float(np.abs(d).max()), float(np.abs(db).max())
     st = {"rms": rms, "rms_base": rms_b, "max_abs": mx, "max_abs_base": mx_b}
     return rms <= 1.10 * rms_b and mx <= 2.0 * mx_b, st
+
+
+MX_BLOCK_TERM = 2.0 ** -11
+
+
+def block_max_product(lhs, w, group_sizes, group_offset: int = 0, block: int = 32):
+    """sum over 32-value K-blocks b of max_{k in b} |a_mk| |w_kn| per output
+    element (float64): the scale of the scaled MFMA's in-block alignment
+    error in the MX tolerance below."""
+    lhs = np.abs(np.asarray(lhs, np.float64))
+    m, k = lhs.shape
+    starts = group_starts(group_sizes)
+    gs = np.asarray(group_sizes, np.int64)
+    out = np.zeros((m, w.shape[2]), np.float64)
+    for g in range(group_offset, min(group_offset + w.shape[0], len(gs))):
+        r0, r1 = int(starts[g]), min(int(starts[g] + gs[g]), m)
+        if r1 <= r0:
+            continue
+        wg = np.abs(np.asarray(w[g - group_offset], np.float64))
+        for b0 in range(0, k, block):
+            a = lhs[r0:r1, b0:b0 + block]
+            wb = wg[b0:b0 + block]
+            mx = np.zeros((r1 - r0, wg.shape[1]))
+            for kk in range(a.shape[1]):
+                np.maximum(mx, a[:, kk:kk + 1] * wb[kk:kk + 1, :], out=mx)
+            out[r0:r1] += mx
+    return out
+
+
+def mx_error_bound(y64, absprod, blockmax, k: int, out_dtype: str = "bfloat16"):
+    """Stated tolerance of the MX mode (e4m3 lhs x e2m1 rhs on the gfx950
+    scaled MFMA) against the float64 product of the dequantized operands:
+
+        |y - y64| <= u_out |y64| + K 2^-24 sum_k |a_k w_k|
+                     + 2^-11 sum_b max_{k in b} |a_k w_k|
+
+    The last term is the instruction's own accumulation: within one 32-value
+    K-block it aligns the products to the block's largest and truncates
+    toward zero (measured on MI355X: errors up to 2^-12 of that product;
+    sums of different blocks combine exact to 2^-20), taken here with a
+    factor 2 margin.  The first two terms are those of ``error_bound``."""
+    return error_bound(y64, absprod, k, out_dtype) + MX_BLOCK_TERM * blockmax

@@ -107,3 +107,58 @@ def quantize_fp8_rows(x: np.ndarray, block: int = 128):
     scale = (amax / np.float32(448.0)).astype(np.float32)
     safe = np.where(scale == 0, np.float32(1), scale)
     return to_e4m3((xb / safe[:, :, None]).reshape(m, k)), scale
+
+
+MX_BLOCK = 32
+MX_MIN_EXP = -126  # scale exponents kept inside e8m0 codes 1..254
+
+
+def mx_quantize_e4m3(x: np.ndarray, block: int = MX_BLOCK):
+    """MX e4m3 activations for the scaled-MFMA grouped matmul
+    (gmm_v2(lhs_quant_dtype=float8_e4m3fn)).
+
+    The reference's quantize_tensor(e4m3, x, axis=-1, block,
+    power_of_two_scale=True) (patches/tpu-inference/0001-dsv4-v6e-
+    enablement.patch:315-350): per block of ``block`` consecutive values
+    along the last axis, scale = 2^ceil(log2(absmax / 448)) and codes =
+    round-to-nearest-even e4m3 of x / scale (|x / scale| <= 448, so no
+    saturation).  The scale is stored as its e8m0 exponent code
+    (e8m0_scale.py:28-35: code = exponent + 127), with the exponent kept in
+    [-126, 127] (codes 1..254): an all-zero block, or one whose absmax is
+    below 448 * 2^-126, gets exponent -126 (its values stay exact or round
+    as e4m3 subnormals).  A block holding a NaN or an infinity gets scale
+    code 255 (NaN) and element codes 0x7F (NaN).
+
+    The exponent is found without rounding: absmax = mf * 2^ef with mf in
+    [0.5, 1) (frexp); absmax <= 448 * 2^e = 0.875 * 2^(9 + e) holds from
+    e = ef - 9 when mf <= 0.875, else from e = ef - 8.
+
+    x: float32 values [..., K] with K % block == 0.  Returns (codes uint8
+    [..., K], scale codes uint8 [..., K / block]).
+    """
+    x = np.asarray(x, np.float32)
+    shp = x.shape
+    xb = x.reshape(shp[:-1] + (shp[-1] // block, block))
+    bad = ~np.all(np.isfinite(xb), axis=-1)
+    amax = np.where(bad, 0, np.abs(np.where(np.isfinite(xb), xb, 0)).max(axis=-1)).astype(np.float64)
+    mf, ef = np.frexp(amax)
+    e = np.where(mf > 0.875, ef - 8, ef - 9)
+    e = np.where(amax == 0, MX_MIN_EXP, np.maximum(e, MX_MIN_EXP)).astype(np.int64)
+    finite = np.where(np.isfinite(xb), xb, 0).astype(np.float64)
+    q = np.ldexp(finite, -e[..., None]).astype(np.float32)  # exact: a power-of-two rescale
+    codes = to_e4m3(q)
+    codes = np.where(bad[..., None], np.uint8(0x7F), codes).astype(np.uint8)
+    scale_codes = np.where(bad, 255, e + 127).astype(np.uint8)
+    return codes.reshape(shp), scale_codes
+
+
+def mx_dequantize(codes: np.ndarray, scale_codes: np.ndarray, block: int = MX_BLOCK) -> np.ndarray:
+    """e4m3 codes [..., K] and e8m0 scale codes [..., K / block] -> the
+    float32 values they stand for (each e4m3 value times 2^(code - 127),
+    exact in f32; scale code 255 gives NaN)."""
+    v = E4M3_VALUES[np.asarray(codes, np.uint8)].astype(np.float64)
+    sc = np.asarray(scale_codes, np.int64)
+    s = np.where(sc == 255, np.nan, np.ldexp(1.0, sc - 127))
+    shp = v.shape
+    out = v.reshape(shp[:-1] + (shp[-1] // block, block)) * s[..., None]
+    return out.reshape(shp).astype(np.float32)
