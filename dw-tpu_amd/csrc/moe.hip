@@ -14,6 +14,8 @@
 //
 // This file is compiled with -ffp-contract=off: the combine's f32 products
 // and sums must stay separately rounded (moe_fast_combine.py:44-54).
+#include <mutex>
+
 #include "common.h"
 
 namespace dwm {
@@ -306,6 +308,77 @@ __global__ __launch_bounds__(256) void combine_kernel(const void *x, int64_t x_r
   }
 }
 
+// The dispatch launches for n = T * topk ids with chunk counters `counts`
+// (nchunks * (E + 1) int32, fully written by the count kernel before they are
+// read, so they need no clearing).
+static int dispatch_launch(const int32_t *topk_ids, int64_t n, int topk, int num_experts, int32_t *perm,
+                           int32_t *tok_sorted, int32_t *revert, int32_t *group_sizes, int32_t *group_offsets,
+                           int32_t *flags, int32_t *counts, hipStream_t st) {
+  const int64_t nchunks = (n + kChunk - 1) / kChunk;
+  if (n == 0) {
+    hipLaunchKernelGGL(dispatch_scan_kernel, dim3(1), dim3(1024), 0, st, counts, 0, num_experts,
+                       group_sizes, group_offsets);
+    return launch_status("moe_dispatch");
+  }
+  if (n <= kFusedMax) {
+    hipLaunchKernelGGL(dispatch_fused_kernel, dim3(1), dim3(kFusedThreads), 0, st, topk_ids, n, topk,
+                       num_experts, perm, tok_sorted, revert, group_sizes, group_offsets, flags);
+    return launch_status("moe_dispatch");
+  }
+  hipLaunchKernelGGL(dispatch_count_kernel, dim3((unsigned)nchunks), dim3(kDispThreads), 0, st,
+                     topk_ids, n, num_experts, counts, flags);
+  hipLaunchKernelGGL(dispatch_scan_kernel, dim3(1), dim3(1024), 0, st, counts, (int)nchunks,
+                     num_experts, group_sizes, group_offsets);
+  hipLaunchKernelGGL(dispatch_scatter_kernel, dim3((unsigned)nchunks), dim3(kDispThreads), 0, st,
+                     topk_ids, n, topk, num_experts, counts, perm, tok_sorted, revert);
+  return launch_status("moe_dispatch");
+}
+
+static int dispatch_check(const int32_t *topk_ids, int64_t T, int topk, int num_experts, int32_t *perm,
+                          int32_t *tok_sorted, int32_t *revert, int32_t *group_sizes) {
+  DWM_CHECK_ARG(T >= 0 && topk > 0 && num_experts > 0, "moe_dispatch: bad sizes T=%lld topk=%d E=%d",
+                (long long)T, topk, num_experts);
+  DWM_UNSUPPORTED_IF(num_experts > kMaxExperts, "moe_dispatch: at most %d experts (got %d)", kMaxExperts,
+                     num_experts);
+  const int64_t n = T * topk;
+  DWM_CHECK_ARG(n < (1ll << 31), "moe_dispatch: T*topk must be < 2^31");
+  DWM_CHECK_ARG(group_sizes, "moe_dispatch: null pointer");
+  DWM_CHECK_ARG(n == 0 || (topk_ids && perm && tok_sorted && revert), "moe_dispatch: null pointer");
+  return DWM_OK;
+}
+
+// ---- the allocation-free dispatch ----------------------------------------
+// Chunk counters of dwm_moe_dispatch_noalloc: a file-scope device array, one
+// copy per GPU, held until the process ends.  Host code uses the address
+// hipGetSymbolAddress returns for the current device, never the symbol.
+constexpr int64_t kNoAllocWords = 1 << 20;  // 4 MiB: nchunks * (E + 1) int32
+static __device__ __align__(256) int32_t scratch[kNoAllocWords];
+
+constexpr int kMaxDevices = 64;
+static std::once_flag g_scratch_once[kMaxDevices];
+static int32_t *g_scratch[kMaxDevices];
+static hipError_t g_scratch_err[kMaxDevices];
+
+// This device's copy of `scratch` (looked up once per device, with the
+// device current), or NULL with the error message set.
+static int32_t *device_scratch() {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error("moe_dispatch_noalloc: no usable current device (%s)", hipGetErrorString(e));
+    return nullptr;
+  }
+  std::call_once(g_scratch_once[dev], [dev] {
+    void *p = nullptr;
+    g_scratch_err[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    g_scratch[dev] = g_scratch_err[dev] == hipSuccess ? (int32_t *)p : nullptr;
+  });
+  if (!g_scratch[dev])
+    set_error("moe_dispatch_noalloc: hipGetSymbolAddress failed on device %d (%s)", dev,
+              hipGetErrorString(g_scratch_err[dev]));
+  return g_scratch[dev];
+}
+
 }  // namespace dwm
 
 using namespace dwm;
@@ -325,34 +398,30 @@ extern "C" int dwm_moe_dispatch(const int32_t *topk_ids, int64_t T, int topk, in
                                 int32_t *group_sizes, int32_t *group_offsets, int32_t *flags,
                                 void *workspace, void *stream) {
   clear_error();
-  DWM_CHECK_ARG(T >= 0 && topk > 0 && num_experts > 0, "moe_dispatch: bad sizes T=%lld topk=%d E=%d",
-                (long long)T, topk, num_experts);
-  DWM_UNSUPPORTED_IF(num_experts > kMaxExperts, "moe_dispatch: at most %d experts (got %d)", kMaxExperts,
-                     num_experts);
+  int rc = dispatch_check(topk_ids, T, topk, num_experts, perm, tok_sorted, revert, group_sizes);
+  if (rc != DWM_OK) return rc;
+  DWM_CHECK_ARG(workspace, "moe_dispatch: null pointer");
+  return dispatch_launch(topk_ids, T * topk, topk, num_experts, perm, tok_sorted, revert, group_sizes,
+                         group_offsets, flags, (int32_t *)workspace, as_stream(stream));
+}
+
+extern "C" int dwm_moe_dispatch_noalloc(const int32_t *topk_ids, int64_t T, int topk, int num_experts,
+                                        int32_t *perm, int32_t *tok_sorted, int32_t *revert,
+                                        int32_t *group_sizes, int32_t *group_offsets, int32_t *flags,
+                                        void *stream) {
+  clear_error();
+  int rc = dispatch_check(topk_ids, T, topk, num_experts, perm, tok_sorted, revert, group_sizes);
+  if (rc != DWM_OK) return rc;
   const int64_t n = T * topk;
-  DWM_CHECK_ARG(n < (1ll << 31), "moe_dispatch: T*topk must be < 2^31");
-  DWM_CHECK_ARG(group_sizes && workspace, "moe_dispatch: null pointer");
-  hipStream_t st = as_stream(stream);
-  const int64_t nchunks = (n + kChunk - 1) / kChunk;
-  int32_t *counts = (int32_t *)workspace;
-  if (n == 0) {
-    hipLaunchKernelGGL(dispatch_scan_kernel, dim3(1), dim3(1024), 0, st, counts, 0, num_experts,
-                       group_sizes, group_offsets);
-    return launch_status("moe_dispatch");
-  }
-  DWM_CHECK_ARG(topk_ids && perm && tok_sorted && revert, "moe_dispatch: null pointer");
-  if (n <= kFusedMax) {
-    hipLaunchKernelGGL(dispatch_fused_kernel, dim3(1), dim3(kFusedThreads), 0, st, topk_ids, n, topk,
-                       num_experts, perm, tok_sorted, revert, group_sizes, group_offsets, flags);
-    return launch_status("moe_dispatch");
-  }
-  hipLaunchKernelGGL(dispatch_count_kernel, dim3((unsigned)nchunks), dim3(kDispThreads), 0, st,
-                     topk_ids, n, num_experts, counts, flags);
-  hipLaunchKernelGGL(dispatch_scan_kernel, dim3(1), dim3(1024), 0, st, counts, (int)nchunks,
-                     num_experts, group_sizes, group_offsets);
-  hipLaunchKernelGGL(dispatch_scatter_kernel, dim3((unsigned)nchunks), dim3(kDispThreads), 0, st,
-                     topk_ids, n, topk, num_experts, counts, perm, tok_sorted, revert);
-  return launch_status("moe_dispatch");
+  const int64_t words = (n + kChunk - 1) / kChunk * (int64_t)(num_experts + 1);
+  DWM_UNSUPPORTED_IF(n > kFusedMax && words > kNoAllocWords,
+                     "moe_dispatch_noalloc: %lld ids over %d experts need %lld counter words, more than the "
+                     "%lld of its static scratch (use dwm_moe_dispatch with a workspace)",
+                     (long long)n, num_experts, (long long)words, (long long)kNoAllocWords);
+  int32_t *counts = device_scratch();
+  if (!counts) return DWM_ERR_HIP;
+  return dispatch_launch(topk_ids, n, topk, num_experts, perm, tok_sorted, revert, group_sizes, group_offsets,
+                         flags, counts, as_stream(stream));
 }
 
 extern "C" int dwm_row_gather(const void *src, int64_t src_rows, int64_t row_bytes,

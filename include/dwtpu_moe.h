@@ -221,6 +221,20 @@ int dwm_moe_dispatch(const int32_t *topk_ids, int64_t T, int topk, int num_exper
                      int32_t *perm, int32_t *tok_sorted, int32_t *revert, int32_t *group_sizes,
                      int32_t *group_offsets, int32_t *flags, void *workspace, void *stream);
 
+/* dwm_moe_dispatch without a workspace argument and without allocating: no
+ * counterpart in the reference; it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops).  The
+ * chunk counters of batches above 8192 ids live in a 4 MiB device array of
+ * the library (one per GPU, held until the process ends), so
+ * ceil(T*topk / 1024) * (num_experts + 1) must be <= 2^20 (e.g. T*topk <=
+ * 4,177,920 at 256 experts); larger requests return DWM_ERR_UNSUPPORTED
+ * before any device work.  Every call on a GPU uses that GPU's one array:
+ * calls that overlap on one GPU (on different streams) race and must not be
+ * issued.  Results are bit-identical to dwm_moe_dispatch's. */
+int dwm_moe_dispatch_noalloc(const int32_t *topk_ids, int64_t T, int topk, int num_experts, int32_t *perm,
+                             int32_t *tok_sorted, int32_t *revert, int32_t *group_sizes, int32_t *group_offsets,
+                             int32_t *flags, void *stream);
+
 /* out[j, :] = src[idx[j], :] for j < rows, bitwise, with JAX gather index
  * semantics (a negative index wraps once, then indices clamp into
  * [0, src_rows)).  Replaces dispatch_gather_pallas / hidden[tok_sorted]
