@@ -10,12 +10,17 @@ copies larger than the 256 MB Infinity Cache so the stream comes from HBM.
 
 `value` is algorithmic HBM GB/s (non-empty experts' packed weights + scales,
 lhs once, output once) divided by the average step time measured with HIP
-events on the stream the kernels run on.  `extra` reports the other workloads
-(decode down-projection with dispatch / combine, prefill) the same way, and
+events on the stream the kernels run on.  The headline runs the reference's
+W4A16 arithmetic (bf16 lhs, exactly decoded fp4 weights, bf16 MFMA).
+`extra` reports the other workloads (decode down-projection with dispatch /
+combine, prefill) the same way, each gmm workload again in the MX mode
+(`<name>_mx`: e4m3 lhs with e8m0 block-32 scales on the scaled MFMA, a
+lossier computation, with the quantization kernel timed alone and with the
+gmm), the expert block, dense FP8, router and format kernels.
 `cpu_baseline` times the numpy oracle of the same math on a bounded sample of
-experts on this host (and one expert on one thread), and reports the max abs
-and relative Frobenius error of one expert's GPU output rows against the
-oracle's float64 product.
+experts on this host's cores (and one expert on one thread), the same for
+prefill and a dense GEMM, and reports the max abs and relative Frobenius
+error of one expert's GPU output rows against the oracle's float64 product.
 
 The default warmup (200 launches, ~30 ms of decode work) brings the GPU to
 its sustained clock before the timed region: the power manager ramps the
@@ -40,6 +45,8 @@ for _p in (ROOT, os.path.join(ROOT, "dw-tpu_amd")):
 METRIC = "FP4 MoE gmm TFLOP/s + HBM GB/s (% of peak) at decode & prefill sizes"
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
+FP8_PEAK_TFLOPS = 5000.0
+ONLY_CHOICES = ("decode_gate_up", "decode_down", "prefill", "decode_gate_up_mx", "decode_down_mx", "prefill_mx")
 MALL_BYTES = 256 * 2 ** 20
 
 
@@ -54,34 +61,58 @@ def _to_dev_bf16(bits, dev):
 
 
 class GmmBench:
-    """Device-resident inputs of one gmm workload plus a raw C-ABI launcher."""
+    """Device-resident inputs of one gmm workload plus a raw C-ABI launcher.
 
-    def __init__(self, wl, dev, copies):
+    mode "bf16": dwm_gmm_fp4 (the reference's W4A16 arithmetic); mode "mx":
+    dwm_gmm_fp4_mx on the lhs quantized once beforehand (e4m3 codes + e8m0
+    block-32 scales), and ``quant_step`` times that quantization."""
+
+    def __init__(self, wl, dev, copies, mode="bf16"):
         import torch
-        from dw_tpu_amd import _lib, fp4_weight_to_codes
+        from dw_tpu_amd import _lib, fp4_weight_to_codes, mx_quantize
         self.wl = wl
+        self.mode = mode
         self.lib = _lib.load()
         rhs = torch.from_numpy(wl.rhs_e2m1).to(dev)
         sc = torch.from_numpy(wl.scale_codes).to(dev)
         self.weights = [fp4_weight_to_codes(rhs, sc) for _ in range(copies)]
         del rhs, sc
-        self.lhs = [_to_dev_bf16(wl.lhs_bits, dev) for _ in range(copies)]
+        self.lhs = [_to_dev_bf16(wl.lhs_bits, dev) for _ in range(copies if mode == "bf16" else 1)]
         self.gs = torch.from_numpy(wl.group_sizes).to(dev)
         self.out = [torch.empty((wl.M, wl.N), dtype=torch.bfloat16, device=dev) for _ in range(copies)]
         self.stream = _lib.stream_handle(dev)
+        P = ctypes.c_void_p
         self.args = []
+        if mode == "mx":
+            self.mx = mx_quantize(self.lhs[0])
+            self.qcodes = torch.empty_like(self.mx.codes)
+            self.qscales = torch.empty_like(self.mx.scales)
+            self.quant_args = (P(self.lhs[0].data_ptr()), wl.M, wl.K, P(self.qcodes.data_ptr()),
+                               P(self.qscales.data_ptr()), self.stream)
         for i in range(copies):
             w = self.weights[i]
-            self.args.append((ctypes.c_void_p(self.lhs[i].data_ptr()), wl.M, wl.K, ctypes.c_void_p(w.weight.data_ptr()),
-                              ctypes.c_void_p(w.scale.data_ptr()), ctypes.c_void_p(self.gs.data_ptr()), wl.E, None,
-                              wl.E, wl.N, ctypes.c_void_p(self.out[i].data_ptr()), _lib.BF16, 0, _lib.ACT_NONE,
-                              self.stream))
-        self.fn = self.lib.dwm_gmm_fp4
+            tail = (P(w.weight.data_ptr()), P(w.scale.data_ptr()), P(self.gs.data_ptr()), wl.E, None, wl.E, wl.N,
+                    P(self.out[i].data_ptr()), _lib.BF16, 0, _lib.ACT_NONE, self.stream)
+            if mode == "mx":
+                self.args.append((P(self.mx.codes.data_ptr()), P(self.mx.scales.data_ptr()), wl.M, None, wl.M,
+                                  wl.K) + tail)
+            else:
+                self.args.append((P(self.lhs[i].data_ptr()), wl.M, wl.K) + tail)
+        self.fn = self.lib.dwm_gmm_fp4_mx if mode == "mx" else self.lib.dwm_gmm_fp4
 
     def step(self, i):
         rc = self.fn(*self.args[i % len(self.args)])
         if rc:
             raise RuntimeError(self.lib.dwm_last_error().decode())
+
+    def quant_step(self, i):
+        rc = self.lib.dwm_mx_quant_e4m3(*self.quant_args)
+        if rc:
+            raise RuntimeError(self.lib.dwm_last_error().decode())
+
+    def quant_and_step(self, i):
+        self.quant_step(i)
+        self.step(i)
 
 
 def time_steps(step, steps, warmup):
@@ -101,34 +132,67 @@ def time_steps(step, steps, warmup):
     return start.elapsed_time(end) / steps
 
 
-def gmm_result(wl, ms):
+def gmm_result(wl, ms, mode="bf16"):
+    """Throughput of one gmm launch.  Algorithmic bytes: the non-empty
+    experts' packed weights and e8m0 scales, the lhs once (bf16, or e4m3
+    codes + block-32 scales in the MX mode) and the bf16 output once."""
     bts = wl.algorithmic_bytes()
+    if mode == "mx":
+        bts += wl.M * wl.K // 32 - wl.M * wl.K  # e4m3 codes + scales in place of bf16
     fl = wl.flops()
     gbs = bts / (ms * 1e-3) / 1e9
     tfl = fl / (ms * 1e-3) / 1e12
-    return {"ms": round(ms, 5), "GB_s": round(gbs, 1), "TFLOP_s": round(tfl, 1),
-            "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "mfma_bf16_frac": round(tfl / BF16_PEAK_TFLOPS, 4),
-            "bytes": bts, "flops": fl, "M": wl.M, "K": wl.K, "N": wl.N, "E": wl.E,
-            "nonempty_groups": int((wl.group_sizes > 0).sum())}
+    r = {"ms": round(ms, 5), "GB_s": round(gbs, 1), "TFLOP_s": round(tfl, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+    if mode == "mx":
+        r["mfma_fp8_frac"] = round(tfl / FP8_PEAK_TFLOPS, 4)
+        r["dtype"] = "e4m3 lhs (e8m0 block-32 scales) x e2m1 weights, scaled MFMA, f32 accumulate"
+    else:
+        r["mfma_bf16_frac"] = round(tfl / BF16_PEAK_TFLOPS, 4)
+    r.update({"bytes": bts, "flops": fl, "M": wl.M, "K": wl.K, "N": wl.N, "E": wl.E,
+              "nonempty_groups": int((wl.group_sizes > 0).sum())})
+    return r
 
 
 def copies_for(wl):
     return max(1, min(4, -(-2 * MALL_BYTES // max(1, wl.weight_bytes()))))
 
 
-def bench_gmm(name, dev, steps, warmup):
+def bench_gmm(name, dev, steps, warmup, mode="bf16"):
     from dw_tpu_amd.workloads import make_gmm_workload
     wl = make_gmm_workload(name)
-    b = GmmBench(wl, dev, copies_for(wl))
+    b = GmmBench(wl, dev, copies_for(wl), mode)
     ms = time_steps(b.step, steps, warmup)
     return wl, b, ms
+
+
+def bench_gmm_mx(name, dev, steps, warmup):
+    """The MX mode of one gmm workload: the gmm on the quantized lhs, the
+    lhs quantization (bf16 [M, K] -> e4m3 + scales), and the two back to back
+    (what gmm_v2(lhs_quant_dtype=float8_e4m3fn) runs on a bf16 lhs)."""
+    wl, b, ms = bench_gmm(name, dev, steps, warmup, "mx")
+    r = gmm_result(wl, ms, "mx")
+    q_ms = time_steps(b.quant_step, steps, min(warmup, 20))
+    qb = wl.M * wl.K * 2 + wl.M * wl.K + wl.M * wl.K // 32
+    r["quant"] = {"ms": round(q_ms, 5), "GB_s": round(qb / (q_ms * 1e-3) / 1e9, 1),
+                  "hbm_frac": round(qb / (q_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "bytes": qb}
+    both = time_steps(b.quant_and_step, steps, min(warmup, 20))
+    r["ms_with_quant"] = round(both, 5)
+    r["TFLOP_s_with_quant"] = round(wl.flops() / (both * 1e-3) / 1e12, 1)
+    return r, b
 
 
 def bench_dispatch_combine(dev, steps, warmup):
     """decode_down routing through the C ABI with preallocated outputs:
     dispatch indices for 512 tokens x top-8 over 32 experts, the row gather
     of hidden [512, 2048] into [4096, 2048], and the combine of the
-    down-projection output [4096, 7168] back to [512, 7168]."""
+    down-projection output [4096, 7168] back to [512, 7168].
+
+    The gather and combine rotate over input/output sets of more than twice
+    the 256 MB Infinity Cache, so each launch reads its inputs from HBM.
+    Algorithmic bytes: the gather reads each source row once (the 2 MB
+    hidden, whose rows it reads 8 times from cache) and writes the 16.8 MB
+    routed copy; the combine reads y once, writes out once, plus indices and
+    weights."""
     import numpy as np
     import torch
     from dw_tpu_amd import _lib
@@ -147,13 +211,9 @@ def bench_dispatch_combine(dev, steps, warmup):
     P = _lib.ptr
     disp_args = (P(ids), wl.T, wl.topk, wl.E, P(perm), P(tok), P(rev), P(gs), P(goff), P(flags), P(ws), st)
     rng = np.random.Generator(np.random.PCG64(11))
-    hidden = torch.from_numpy(rng.standard_normal((wl.T, wl.K), dtype=np.float32)).to(torch.bfloat16).to(dev)
-    x = torch.empty((n, wl.K), dtype=torch.bfloat16, device=dev)
-    y = torch.from_numpy(rng.standard_normal((n, wl.N), dtype=np.float32)).to(torch.bfloat16).to(dev)
+    hidden0 = torch.from_numpy(rng.standard_normal((wl.T, wl.K), dtype=np.float32)).to(torch.bfloat16).to(dev)
+    y0 = torch.from_numpy(rng.standard_normal((n, wl.N), dtype=np.float32)).to(torch.bfloat16).to(dev)
     w = torch.from_numpy(wl.topk_weights).to(dev)
-    out = torch.empty((wl.T, wl.N), dtype=torch.bfloat16, device=dev)
-    gather_args = (P(hidden), wl.T, wl.K * 2, P(tok), n, P(x), st)
-    comb_args = (P(y), _lib.BF16, n, wl.N, P(rev), P(w), _lib.F32, wl.T, wl.topk, P(out), _lib.BF16, st)
 
     def run(fn, args):
         rc = fn(*args)
@@ -162,15 +222,32 @@ def bench_dispatch_combine(dev, steps, warmup):
 
     res = {}
     ms = time_steps(lambda i: run(lib.dwm_moe_dispatch, disp_args), steps, warmup)
-    res["dispatch"] = {"ms": round(ms, 5), "ids": n, "experts": wl.E, "kernels": 1 if n <= 8192 else 3}
-    ms = time_steps(lambda i: run(lib.dwm_row_gather, gather_args), steps, warmup)
-    gb = 2 * n * wl.K * 2 + n * 4
+    res["dispatch"] = {"ms": round(ms, 5), "ids": n, "experts": wl.E, "kernels": 1 if n <= 8192 else 3,
+                       "note": "launch-latency bound (one 1024-thread block)"}
+    run(lib.dwm_moe_dispatch, disp_args)
+    set_bytes = (wl.T + n) * wl.K * 2
+    gc = -(-2 * MALL_BYTES // set_bytes)
+    hiddens = [hidden0.clone() for _ in range(gc)]
+    xs = [torch.empty((n, wl.K), dtype=torch.bfloat16, device=dev) for _ in range(gc)]
+    gargs = [(P(hiddens[c]), wl.T, wl.K * 2, P(tok), n, P(xs[c]), st) for c in range(gc)]
+    ms = time_steps(lambda i: run(lib.dwm_row_gather, gargs[i % gc]), steps, warmup)
+    gb = wl.T * wl.K * 2 + n * wl.K * 2 + n * 4
     res["row_gather"] = {"ms": round(ms, 5), "GB_s": round(gb / (ms * 1e-3) / 1e9, 1), "rows": n, "H": wl.K,
-                         "hbm_frac": round(gb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
-    ms = time_steps(lambda i: run(lib.dwm_moe_combine, comb_args), steps, warmup)
+                         "hbm_frac": round(gb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "bytes": gb,
+                         "rotated_sets": gc}
+    del hiddens, xs
+    set_bytes = (n + wl.T) * wl.N * 2
+    cc = -(-2 * MALL_BYTES // set_bytes)
+    ys = [y0.clone() for _ in range(cc)]
+    outs = [torch.empty((wl.T, wl.N), dtype=torch.bfloat16, device=dev) for _ in range(cc)]
+    cargs = [(P(ys[c]), _lib.BF16, n, wl.N, P(rev), P(w), _lib.F32, wl.T, wl.topk, P(outs[c]), _lib.BF16, st)
+             for c in range(cc)]
+    ms = time_steps(lambda i: run(lib.dwm_moe_combine, cargs[i % cc]), steps, warmup)
     gb = n * wl.N * 2 + wl.T * wl.N * 2 + n * 8
     res["combine"] = {"ms": round(ms, 5), "GB_s": round(gb / (ms * 1e-3) / 1e9, 1), "T": wl.T, "topk": wl.topk,
-                      "H": wl.N, "hbm_frac": round(gb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+                      "H": wl.N, "hbm_frac": round(gb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "bytes": gb,
+                      "rotated_sets": cc}
+    del ys, outs
     return res
 
 
@@ -389,26 +466,38 @@ def profiled_traffic(name="gmm_fp4_decode_gate_up.md"):
     return int(m.group(1)) if m else None
 
 
-def cpu_baseline(wl, budget_s, gpu_check=None):
-    """numpy oracle of the same math (exact dequant to f32, per-expert f32
-    matmul, bf16 round) over as many non-empty experts as fit the budget, on
-    the BLAS threads numpy has, plus one expert on one thread.
+def cpu_workers():
+    """CPU threads for the baseline: this process's cores, at most 16 (one
+    GPU's share of the host)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+def cpu_gmm_baseline(wl, budget_s, gpu_check=None):
+    """numpy oracle of the same math -- exact fp4 dequant to f32, per-expert
+    f32 matmul, bf16 round -- over the non-empty experts, one expert per
+    worker thread (each with a one-thread BLAS), the workers together on
+    ``cpu_workers()`` cores; experts not started within ``budget_s`` are
+    skipped (a bounded sample).  Plus one expert on one thread.
 
     gpu_check = (expert, rows as f32) of the GPU output: the oracle also
     checks those rows against its float64 product (max abs error and
     relative Frobenius error, the bf16 output rounding included)."""
+    from concurrent.futures import ThreadPoolExecutor
+
     import numpy as np
+    from threadpoolctl import threadpool_limits
+
     from oracle import fp4
     from oracle import gmm as ogmm
     from oracle.numerics import bf16_to_f32, round_bf16
-    try:
-        from threadpoolctl import threadpool_info, threadpool_limits
-        threads = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
-    except Exception:
-        threadpool_limits = None
-        threads = 1
+    workers = cpu_workers()
     starts = np.concatenate([[0], np.cumsum(wl.group_sizes)])
     lhs = bf16_to_f32(wl.lhs_bits)
+    nonempty = [e for e in range(wl.E) if wl.group_sizes[e] > 0]
 
     def expert_bytes(sz):
         return wl.K * wl.N // 2 + (wl.K // 32) * wl.N + sz * wl.K * 2 + sz * wl.N * 2
@@ -417,27 +506,33 @@ def cpu_baseline(wl, budget_s, gpu_check=None):
         codes = fp4.e2m1_to_codes(fp4.unpack_nibbles(wl.rhs_e2m1[e]))
         return fp4.dequant_fp4_block(codes, fp4.e8m0_decode(wl.scale_codes[e]))
 
-    done, bts, t0 = 0, 0, time.perf_counter()
-    for e in range(wl.E):
-        sz = int(wl.group_sizes[e])
-        if sz == 0:
-            continue
+    def one(e):
         round_bf16(lhs[starts[e]:starts[e + 1]] @ dequant(e))
-        done += 1
-        bts += expert_bytes(sz)
-        if time.perf_counter() - t0 > budget_s:
-            break
-    dt = time.perf_counter() - t0
-    res = {"value": round(bts / dt / 1e9, 4), "unit": "GB/s", "cores": int(threads), "kind": "port",
-           "sample": f"{done} of {int((wl.group_sizes > 0).sum())} non-empty experts of {wl.name} "
-                     f"(numpy oracle: dequant single-threaded, f32 matmul on {threads} BLAS threads), {dt:.1f} s"}
-    e1 = int(np.flatnonzero(wl.group_sizes > 0)[0])
-    if threadpool_limits is not None:
-        with threadpool_limits(limits=1):
-            t1 = time.perf_counter()
-            round_bf16(lhs[starts[e1]:starts[e1 + 1]] @ dequant(e1))
-            dt1 = time.perf_counter() - t1
-        res["value_1thread"] = round(expert_bytes(int(wl.group_sizes[e1])) / dt1 / 1e9, 4)
+
+    t0 = time.perf_counter()
+    deadline = t0 + budget_s
+
+    def task(e):
+        if time.perf_counter() > deadline:
+            return None
+        one(e)
+        return e
+
+    with threadpool_limits(limits=1):
+        with ThreadPoolExecutor(workers) as ex:
+            done = [e for e in ex.map(task, nonempty) if e is not None]
+        dt = time.perf_counter() - t0
+        e1 = nonempty[0]
+        t1 = time.perf_counter()
+        one(e1)
+        dt1 = time.perf_counter() - t1
+    bts = sum(expert_bytes(int(wl.group_sizes[e])) for e in done)
+    fl = sum(2 * int(wl.group_sizes[e]) * wl.K * wl.N for e in done)
+    res = {"value": round(bts / dt / 1e9, 4), "unit": "GB/s", "cores": workers, "kind": "port",
+           "TFLOP_s": round(fl / dt / 1e12, 4),
+           "sample": f"{len(done)} of {len(nonempty)} non-empty experts of {wl.name} (numpy oracle: exact fp4 "
+                     f"dequant, f32 matmul, bf16 round; one expert per thread on {workers} threads), {dt:.1f} s",
+           "value_1thread": round(expert_bytes(int(wl.group_sizes[e1])) / dt1 / 1e9, 4)}
     if gpu_check is not None:
         e, y = gpu_check
         a = lhs[starts[e]:starts[e + 1]].astype(np.float64)
@@ -455,6 +550,32 @@ def cpu_baseline(wl, budget_s, gpu_check=None):
     return res
 
 
+def cpu_dense_baseline(m, budget_s):
+    """numpy oracle of the dense W8A16 GEMM (K=7168, N=4096): e4m3 decode,
+    per-128-K-block f32 dot times the block scale, f32 accumulate, on
+    ``cpu_workers()`` BLAS threads; repeated within the budget."""
+    from threadpoolctl import threadpool_limits
+
+    from dw_tpu_amd.workloads import make_dense_workload
+    from oracle import dense_fp8 as odf
+    from oracle.numerics import bf16_to_f32
+    wl = make_dense_workload(m)
+    x = bf16_to_f32(wl.x_bits)
+    workers = cpu_workers()
+    n_runs, t0 = 0, time.perf_counter()
+    with threadpool_limits(limits=workers):
+        while True:
+            odf.matmul_w8a16(x, wl.wq, wl.s_w8a16, accumulate="f32")
+            n_runs += 1
+            if time.perf_counter() - t0 > budget_s:
+                break
+    dt = (time.perf_counter() - t0) / n_runs
+    fl = 2 * m * wl.K * wl.N
+    return {"value": round(fl / dt / 1e12, 4), "unit": "TFLOP/s", "cores": workers, "kind": "port", "ms": round(dt * 1e3, 2),
+            "sample": f"{n_runs} run(s) of dense W8A16 M={m}, K={wl.K}, N={wl.N} (numpy oracle, f32 "
+                      f"per-K-block products on {workers} BLAS threads)"}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -465,6 +586,9 @@ def main():
                     help="seconds of CPU-baseline work (0 skips it)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy (byte-counter calibration)")
+    ap.add_argument("--only", choices=ONLY_CHOICES, default=None,
+                    help="profiling aid: time one gmm workload line (name, or name_mx for the MX mode) and print "
+                         "it as {\"only\": name, ...}; not the benchmark line")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -484,6 +608,15 @@ def main():
         torch.cuda.synchronize()
         log("calib copy: 3 x 1 GiB device-to-device copies done")
         return
+    if args.only:
+        name = args.only[:-3] if args.only.endswith("_mx") else args.only
+        if args.only.endswith("_mx"):
+            r, _ = bench_gmm_mx(name, dev, args.steps, args.warmup)
+        else:
+            wl1, _, ms1 = bench_gmm(name, dev, args.steps, args.warmup)
+            r = gmm_result(wl1, ms1)
+        print(json.dumps({"only": args.only, "result": r}), flush=True)
+        return
     log("bench: decode_gate_up gmm")
     wl, b, ms = bench_gmm("decode_gate_up", dev, args.steps, args.warmup)
     main_res = gmm_result(wl, ms)
@@ -502,6 +635,12 @@ def main():
             extra[name] = gmm_result(wl2, ms2)
         del b
         torch.cuda.empty_cache()
+        for name in ("decode_gate_up", "decode_down", "prefill"):
+            log(f"bench: {name} gmm, MX mode")
+            r, bmx = bench_gmm_mx(name, dev, args.steps, args.warmup)
+            extra[f"{name}_mx"] = r
+            del bmx
+            torch.cuda.empty_cache()
         log("bench: dispatch / gather / combine")
         extra.update(bench_dispatch_combine(dev, args.steps, args.warmup))
         log("bench: moe block (decode)")
@@ -517,7 +656,13 @@ def main():
     cpu = None
     if args.cpu_budget > 0:
         log("bench: cpu baseline")
-        cpu = cpu_baseline(wl, args.cpu_budget, gpu_check)
+        cpu = cpu_gmm_baseline(wl, args.cpu_budget, gpu_check)
+        if args.extra == "all":
+            from dw_tpu_amd.workloads import make_gmm_workload
+            cpu["other_workloads"] = {
+                "prefill": cpu_gmm_baseline(make_gmm_workload("prefill"), args.cpu_budget / 2),
+                "dense_w8a16_M1024": cpu_dense_baseline(1024, args.cpu_budget / 4),
+            }
     line = {
         "metric": METRIC,
         "value": main_res["GB_s"],

@@ -16,9 +16,10 @@
 // converter at unit scale, exact RNE); scale code e + 127.  A block holding
 // a NaN or an infinity gets codes 0x7F and scale code 255.
 //
-// gmm_mx_kernel: the tile scheduler, warp specialisation and epilogue of the
-// bf16 kernel (gmm_fp4.hip, gmm_tiles.h), with these data per 64-deep K step
-// of a 96 x 512 tile:
+// gmm_mx_kernel (K < 4096) and gmm_mx128_kernel (K >= 4096, 128-deep steps,
+// described with its config below): the tile scheduler, warp
+// specialisation and epilogue of the bf16 kernel (gmm_fp4.hip,
+// gmm_tiles.h), with these data per 64-deep K step of a 96 x 512 tile:
 //   A   96 rows x 64 bytes of e4m3 codes (chunk c of row r at physical chunk
 //       c ^ ((r >> 2) & 3): the 16 rows one LDS cycle reads hit 16 distinct
 //       16-byte bank groups);
@@ -40,6 +41,12 @@ typedef __attribute__((ext_vector_type(8))) int i32x8_t;
 
 constexpr int kMxBlock = 32;
 constexpr int kMxMinExp = -126;
+// K at and above which the 128-deep kernel runs.  Measured on MI355X with
+// 96 x 512 tiles: at K = 7168 it is faster than the 64-deep kernel (prefill
+// 1.70 -> 1.53 ms, decode gate/up 96 -> 88 us: half the barriers per MFMA),
+// at K = 2048 slower (decode down 107 -> 116 us: 16 steps leave too little
+// to pipeline behind one step in flight).
+constexpr int kMx128MinK = 4096;
 
 // ---------------------------------------------------------------------------
 // Quantization.  Thread i handles values 8 i .. 8 i + 7 of the flat [rows, K]
@@ -118,9 +125,8 @@ struct MxCfg {
   static constexpr int EP_STRIDE = 72;
   static_assert(ROWS % 16 == 0 && G_LOADS * NP == GT, "load split");
   static_assert(AS_LOADS <= NP, "one row-scale load per producer at most");
-  // Two consecutive steps are one even and one odd step, so with two steps
-  // in flight behind the published pair every wait covers the same loads.
-  static_assert(NS - 1 - AHEAD == 2, "two steps in flight");
+  static constexpr int INFLIGHT = NS - 1 - AHEAD;        // steps loading behind the published pair
+  static_assert(INFLIGHT >= 1, "stage count");
   static_assert(CW * 32 * EP_STRIDE * 4 <= NS * STAGE, "epilogue staging fits the stages");
 };
 
@@ -140,8 +146,12 @@ __device__ __forceinline__ void mx_producer(const uint8_t *__restrict__ lhs, con
   constexpr int MAXA = (C::A_GROUPS + NP - 1) / NP;
   constexpr int L_ODD = NA + 2 * C::G_LOADS;
   constexpr int L_EVEN = L_ODD + C::G_LOADS + (ASL ? 1 : 0);
-  constexpr int PENDING = L_EVEN + L_ODD;
-  static_assert(PENDING < 64, "vmcnt range");
+  // Before barrier t the loads of steps t + 2 .. t + NS - 2 may be pending:
+  // INFLIGHT steps alternating in parity from t's.
+  constexpr int P_HI = (C::INFLIGHT + 1) / 2, P_LO = C::INFLIGHT / 2;
+  constexpr int PENDING_T_EVEN = P_HI * L_EVEN + P_LO * L_ODD;
+  constexpr int PENDING_T_ODD = P_LO * L_EVEN + P_HI * L_ODD;
+  static_assert(PENDING_T_EVEN < 64 && PENDING_T_ODD < 64, "vmcnt range");
   const int lane = threadIdx.x & 63;
   for (int i = NA; i < MAXA; ++i) {
     const int ga = pw + NP * i;
@@ -206,9 +216,10 @@ __device__ __forceinline__ void mx_producer(const uint8_t *__restrict__ lhs, con
   for (int t = 0; t < NS - 1; ++t) issue(t, clampt(t));
   int refill = NS - 1;
   for (int t = 0; t < T; ++t) {
-    // Steps t, t + 1 have landed once at most the loads of t + 2, t + 3
-    // (one even, one odd step) are pending.
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(PENDING));
+    // Steps t, t + 1 have landed once at most the loads of t + 2 .. t + NS - 2
+    // are pending.
+    if (t & 1) __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(PENDING_T_ODD));
+    else __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(PENDING_T_EVEN));
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
@@ -371,18 +382,249 @@ __global__ __launch_bounds__(C::THREADS) void gmm_mx_kernel(
   else mx_consumer<C, MB, ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32);
 }
 
-template <int MB, int CW, int NP, int NS, bool ACT>
+// ---------------------------------------------------------------------------
+// 128-deep steps: one scale dword per row and per weight-group lane covers a
+// whole step (K-blocks 4 kb .. 4 kb + 3), so every step issues the same
+// loads.  Per step and 96 x 512 tile: W 8 groups x 4 KiB (the two 64-deep
+// halves of fp4.hip's layout, contiguous), A 96 rows x 128 bytes (chunk c of
+// row r at physical chunk c ^ ((r >> 1) & 7)), AS 128 row dwords, S 8 x 256
+// bytes.  Stage t is published at barrier t (one step ahead of the
+// consumers' reads) and the stage of step t - 1 is refilled with step
+// t + NS - 1.
+template <int MB, int CW, int NP, int NS>
+struct Mx128Cfg {
+  static constexpr int CONS = CW, NPROD = NP, STAGES = NS;
+  static constexpr int GT = CW;
+  static constexpr int THREADS = 64 * (CW + NP);
+  static constexpr int NT = 64 * GT;
+  static constexpr int ROWS = 32 * MB;
+  static constexpr int W = 0;                            // group i: 4 KiB at W + 4096 i
+  static constexpr int A = GT * 4096;                    // ROWS x 128 bytes
+  static constexpr int AS_LOADS = (ROWS + 63) / 64;
+  static constexpr int AS = A + ROWS * 128;              // AS_LOADS x 256 bytes (dword per row)
+  static constexpr int S = AS + AS_LOADS * 256;          // group i: 256 bytes at S + 256 i
+  static constexpr int STAGE = S + GT * 256;
+  static constexpr int A_LOADS = ROWS / 8 / NP;          // 1 KiB lhs loads (8 rows) per producer
+  static constexpr int G_LOADS = GT / NP;
+  static constexpr int EP_STRIDE = 72;
+  static_assert(A_LOADS * NP * 8 == ROWS && G_LOADS * NP == GT, "load split");
+  static_assert(AS_LOADS <= NP && NS >= 2, "config");
+  static_assert(CW * 32 * EP_STRIDE * 4 <= NS * STAGE, "epilogue staging fits the stages");
+};
+
+template <class C, int NA, bool ASL>
+__device__ __forceinline__ void mx128_producer(const uint8_t *__restrict__ lhs, const uint8_t *__restrict__ lsc,
+                                               const int32_t *__restrict__ row_idx, int64_t lhs_rows, int64_t row0,
+                                               int rows, int K, int T, const uint8_t *__restrict__ wexp,
+                                               const uint8_t *__restrict__ sexp, int g0, int G, uint8_t *s_lds,
+                                               int pw) {
+  constexpr int NP = C::NPROD, NS = C::STAGES;
+  constexpr int LOADS = NA + 5 * C::G_LOADS + (ASL ? 1 : 0);
+  constexpr int PENDING = LOADS * (NS - 2);  // steps t + 1 .. t + NS - 2 may be pending at barrier t
+  static_assert(PENDING < 64, "vmcnt range");
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int i = NA; i < C::A_LOADS; ++i)
+#pragma unroll
+    for (int st = 0; st < NS; ++st)
+      *(u32x4_t *)(s_lds + st * C::STAGE + C::A + (pw + NP * i) * 1024 + lane * 16) = u32x4_t{0u, 0u, 0u, 0u};
+  const int KS = K / kMxBlock;
+  auto src_row = [&](int r) -> int64_t {
+    const int rs = r < rows ? r : rows - 1;
+    return row_idx ? gather_index(row_idx[row0 + rs], lhs_rows) : row0 + rs;
+  };
+  uint32_t aoff[NA > 0 ? NA : 1];
+#pragma unroll
+  for (int i = 0; i < NA; ++i) {
+    const int r = 8 * (pw + NP * i) + (lane >> 3);
+    aoff[i] = (uint32_t)(src_row(r) * K) + (uint32_t)(((lane & 7) ^ ((r >> 1) & 7)) << 4);
+  }
+  const int aspart = pw - (NP - C::AS_LOADS);
+  const uint32_t asoff = ASL ? (uint32_t)(src_row(64 * aspart + lane) * KS) : 0u;
+  const uint8_t *wsrc[C::G_LOADS];
+  const uint8_t *ssrc[C::G_LOADS];
+#pragma unroll
+  for (int c = 0; c < C::G_LOADS; ++c) {
+    const int g = min(g0 + pw + NP * c, G - 1);
+    wsrc[c] = wexp + (int64_t)g * T * 4096 + lane * 16;
+    ssrc[c] = sexp + (int64_t)g * T * 256 + lane * 4;
+  }
+  auto issue = [&](int stage, int t) {
+    uint8_t *const st = s_lds + stage * C::STAGE;
+    const uint8_t *const a = lhs + (int64_t)t * 128;
+#pragma unroll
+    for (int i = 0; i < NA; ++i)
+      __builtin_amdgcn_global_load_lds((const void *)(a + aoff[i]),
+                                       (lds_void_t *)(st + C::A + (pw + NP * i) * 1024), 16, 0, 0);
+#pragma unroll
+    for (int c = 0; c < C::G_LOADS; ++c) {
+      const int gi = pw + NP * c;
+      const uint8_t *const w = wsrc[c] + (int64_t)t * 4096;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        __builtin_amdgcn_global_load_lds((const void *)(w + 1024 * q),
+                                         (lds_void_t *)(st + C::W + gi * 4096 + 1024 * q), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void *)(ssrc[c] + (int64_t)t * 256),
+                                       (lds_void_t *)(st + C::S + gi * 256), 4, 0, 0);
+    }
+    if (ASL)
+      __builtin_amdgcn_global_load_lds((const void *)(lsc + asoff + t * 4),
+                                       (lds_void_t *)(st + C::AS + aspart * 256), 4, 0, 0);
+  };
+#pragma unroll
+  for (int t = 0; t < NS - 1; ++t) issue(t, min(t, T - 1));
+  int refill = NS - 1;
+  for (int t = 0; t < T; ++t) {
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(PENDING));
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    issue(refill, min(t + NS - 1, T - 1));
+    refill = refill == NS - 1 ? 0 : refill + 1;
+  }
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+}
+
+template <class C, int AM, bool ACT>
+__device__ __forceinline__ void mx128_consumer(int T, uint8_t *s_lds, int cw, int64_t row0, int rows, int64_t col0,
+                                               int N, void *__restrict__ out, int out_f32) {
+  constexpr int NS = C::STAGES;
+  const int lane = threadIdx.x & 63, c32 = lane & 31, h = lane >> 5;
+  f32x16_t acc[AM][2];
+#pragma unroll
+  for (int mb = 0; mb < AM; ++mb)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[mb][j][r] = 0.0f;
+  const int woff = C::W + cw * 4096 + lane * 16;
+  const int soff = C::S + cw * 256 + lane * 4;
+  const int sw = (c32 >> 1) & 7;  // rows mb * 32 + c32 share it
+  const int arow = C::A + c32 * 128;
+  u32x4_t wa[2], wb[2];
+  i32x8_t an;
+  auto read_a = [&](const uint8_t *st, int f, int mb) {
+    const u32x4_t lo = *(const u32x4_t *)(st + arow + mb * 32 * 128 + (((4 * f + h) ^ sw) << 4));
+    const u32x4_t hi = *(const u32x4_t *)(st + arow + mb * 32 * 128 + (((4 * f + 2 + h) ^ sw) << 4));
+    an = i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+  };
+  int cur = 0;
+  for (int t = 0; t < T; ++t) {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    const uint8_t *const st = s_lds + cur * C::STAGE;
+    wa[0] = *(const u32x4_t *)(st + woff);
+    wa[1] = *(const u32x4_t *)(st + woff + 1024);
+    const uint32_t sd = *(const uint32_t *)(st + soff);
+    uint32_t sa[AM];
+#pragma unroll
+    for (int mb = 0; mb < AM; ++mb) sa[mb] = *(const uint32_t *)(st + C::AS + (mb * 32 + c32) * 4);
+    read_a(st, 0, 0);
+#pragma unroll
+    for (int f = 0; f < 2; ++f) {
+      const u32x4_t w0 = f == 0 ? wa[0] : wb[0], w1 = f == 0 ? wa[1] : wb[1];
+      const i32x8_t b0 = {(int)w0[0], (int)w0[1], (int)w0[2], (int)w0[3], 0, 0, 0, 0};
+      const i32x8_t b1 = {(int)w1[0], (int)w1[1], (int)w1[2], (int)w1[3], 0, 0, 0, 0};
+      const int sb = (int)(sd >> (16 * f));
+#pragma unroll
+      for (int mb = 0; mb < AM; ++mb) {
+        const i32x8_t a = an;
+        const int sa_l = (int)((sa[mb] >> (16 * f + 8 * h)) & 0xFFu);
+        __builtin_amdgcn_sched_barrier(0);
+        if (mb + 1 < AM) read_a(st, f, mb + 1);
+        else if (f == 0) read_a(st, 1, 0);
+        if (f == 0 && mb == 0) {
+          wb[0] = *(const u32x4_t *)(st + woff + 2048);
+          wb[1] = *(const u32x4_t *)(st + woff + 3072);
+        }
+        acc[mb][0] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b0, acc[mb][0], 0, 4, 0, sa_l, 0, sb);
+        acc[mb][1] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b1, acc[mb][1], 0, 4, 0, sa_l, 1, sb);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    cur = cur == NS - 1 ? 0 : cur + 1;
+  }
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  store_tile<AM, ACT, C::EP_STRIDE>(acc, (float *)(s_lds + cw * 32 * C::EP_STRIDE * 4), row0, rows, col0, N, out,
+                                    out_f32);
+}
+
+template <class C, int MB, bool ACT>
+__global__ __launch_bounds__(C::THREADS) void gmm_mx128_kernel(
+    const uint8_t *__restrict__ lhs, const uint8_t *__restrict__ lsc, const int32_t *__restrict__ row_idx,
+    int64_t lhs_rows, int64_t M, int K, const uint8_t *__restrict__ wpk, const uint8_t *__restrict__ spk,
+    const int32_t *__restrict__ group_sizes, int num_groups, const int32_t *__restrict__ group_offset,
+    int64_t e_local, int N, void *__restrict__ out, int out_f32) {
+  constexpr int CW = C::CONS, NP = C::NPROD;
+  static_assert(C::STAGES * C::STAGE >= (kMaxGroups + MB * kClsStride) * 4, "tile classes alias the stages");
+  __shared__ __attribute__((aligned(1024))) uint8_t s_lds[C::STAGES * C::STAGE];
+  __shared__ int s_info[3];
+  int *s_rowstart = (int *)s_lds;
+  int *s_cls = s_rowstart + kMaxGroups;
+  const int tid = threadIdx.x, wave = tid >> 6;
+  const int go = group_offset ? group_offset[0] : 0;
+  TileRef ref;
+  if (!find_tile<MB, C::THREADS>(group_sizes, num_groups, go, e_local, M, (N + C::NT - 1) / C::NT, s_rowstart,
+                                 s_cls, s_info, ref))
+    return;
+  const int g = ref.g, nt = ref.nt, rows = ref.rows;
+  const int64_t row0 = ref.row0;
+  const int64_t e = g - go;
+  const int T = K >> 7, G = (N + 63) >> 6;
+  const int g0 = nt * C::GT;
+  if (wave >= CW) {
+    const int pw = wave - CW;
+    const uint8_t *const wexp = wpk + e * G * T * 4096;
+    const uint8_t *const sexp = spk + e * G * T * 256;
+    const int na = min(C::A_LOADS, (rows + 8 * NP - 1 - 8 * pw) / (8 * NP));
+    const bool asl = pw >= NP - C::AS_LOADS;
+    auto run = [&](auto na_c, auto asl_c) {
+      mx128_producer<C, decltype(na_c)::value, decltype(asl_c)::value != 0>(lhs, lsc, row_idx, lhs_rows, row0, rows,
+                                                                             K, T, wexp, sexp, g0, G, s_lds, pw);
+    };
+    static_assert(C::A_LOADS == 3, "three lhs row groups per producer");
+    if (asl) {
+      if (na >= 3) run(IntC<3>{}, IntC<1>{});
+      else if (na == 2) run(IntC<2>{}, IntC<1>{});
+      else if (na == 1) run(IntC<1>{}, IntC<1>{});
+      else run(IntC<0>{}, IntC<1>{});
+    } else {
+      if (na >= 3) run(IntC<3>{}, IntC<0>{});
+      else if (na == 2) run(IntC<2>{}, IntC<0>{});
+      else if (na == 1) run(IntC<1>{}, IntC<0>{});
+      else run(IntC<0>{}, IntC<0>{});
+    }
+    return;
+  }
+  const int act_mb = (rows + 31) >> 5;
+  const int64_t col0 = (int64_t)(g0 + wave) * 64;
+  if (act_mb <= 1 || MB == 1) mx128_consumer<C, 1, ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32);
+  else if (act_mb == 2 || MB == 2) mx128_consumer<C, (MB >= 2 ? 2 : 1), ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32);
+  else mx128_consumer<C, MB, ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32);
+}
+
+template <class C, int MB, bool ACT, bool STEP128>
 static int launch_gmm_mx(const uint8_t *lhs, const uint8_t *lsc, const int32_t *row_idx, int64_t lhs_rows, int64_t M,
                          int64_t K, const uint8_t *w, const uint8_t *s, const int32_t *gs, int ng, const int32_t *go,
                          int64_t e_local, int64_t N, void *out, int out_f32, hipStream_t st) {
-  using C = MxCfg<MB, CW, NP, NS>;
   constexpr int MT = 32 * MB, NT = C::NT;
   const int64_t n_tiles = (N + NT - 1) / NT;
   const int64_t max_tiles = ((M + MT - 1) / MT + e_local) * n_tiles;
   const int64_t grid = ((max_tiles + 7) / 8 + MB) * 8;
   DWM_UNSUPPORTED_IF(grid > (1ll << 31) - 1, "gmm_fp4_mx: too many tiles (%lld)", (long long)grid);
-  hipLaunchKernelGGL((gmm_mx_kernel<C, MB, ACT>), dim3((unsigned)grid), dim3(C::THREADS), 0, st, lhs, lsc, row_idx,
-                     lhs_rows, M, (int)K, w, s, gs, ng, go, e_local, (int)N, out, out_f32);
+  if constexpr (STEP128)
+    hipLaunchKernelGGL((gmm_mx128_kernel<C, MB, ACT>), dim3((unsigned)grid), dim3(C::THREADS), 0, st, lhs, lsc,
+                       row_idx, lhs_rows, M, (int)K, w, s, gs, ng, go, e_local, (int)N, out, out_f32);
+  else
+    hipLaunchKernelGGL((gmm_mx_kernel<C, MB, ACT>), dim3((unsigned)grid), dim3(C::THREADS), 0, st, lhs, lsc, row_idx,
+                       lhs_rows, M, (int)K, w, s, gs, ng, go, e_local, (int)N, out, out_f32);
   return launch_status("gmm_fp4_mx");
 }
 
@@ -443,11 +685,25 @@ extern "C" int dwm_gmm_fp4_mx(const uint8_t *lhs, const uint8_t *lhs_scale, int6
   }
   if (E_local == 0 || num_groups == 0) return DWM_OK;
   const int out_f32 = out_dtype == DWM_F32;
-  // 96-row x 512-column tiles, 8 consumer + 4 producer waves, five 64-deep
-  // K stages (two published per barrier, two in flight).
+  // 96-row x 512-column tiles, 8 consumer + 4 producer waves, a ring of
+  // 64-deep K stages (two published per barrier, the rest in flight).
+  // 96-row x 512-column tiles, 8 consumer + 4 producer waves.  64-deep K
+  // steps in a five-stage ring (two published per barrier, two in flight),
+  // or 128-deep steps in a three-stage ring (one published, one in flight).
+  using C64 = MxCfg<3, 8, 4, 5>;
+  using C128 = Mx128Cfg<3, 8, 4, 3>;
+  const bool deep = K >= kMx128MinK;
   if (fuse_act == DWM_ACT_SILU_MUL_CLAMP)
-    return launch_gmm_mx<3, 8, 4, 5, true>(lhs, lhs_scale, row_idx, lhs_rows, M, K, weight, scale, group_sizes,
-                                           num_groups, group_offset, E_local, N, out, out_f32, st);
-  return launch_gmm_mx<3, 8, 4, 5, false>(lhs, lhs_scale, row_idx, lhs_rows, M, K, weight, scale, group_sizes,
-                                          num_groups, group_offset, E_local, N, out, out_f32, st);
+    return deep ? launch_gmm_mx<C128, 3, true, true>(lhs, lhs_scale, row_idx, lhs_rows, M, K, weight, scale,
+                                                      group_sizes, num_groups, group_offset, E_local, N, out,
+                                                      out_f32, st)
+                : launch_gmm_mx<C64, 3, true, false>(lhs, lhs_scale, row_idx, lhs_rows, M, K, weight, scale,
+                                                      group_sizes, num_groups, group_offset, E_local, N, out,
+                                                      out_f32, st);
+  return deep ? launch_gmm_mx<C128, 3, false, true>(lhs, lhs_scale, row_idx, lhs_rows, M, K, weight, scale,
+                                                     group_sizes, num_groups, group_offset, E_local, N, out, out_f32,
+                                                     st)
+              : launch_gmm_mx<C64, 3, false, false>(lhs, lhs_scale, row_idx, lhs_rows, M, K, weight, scale,
+                                                     group_sizes, num_groups, group_offset, E_local, N, out, out_f32,
+                                                     st);
 }

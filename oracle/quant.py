@@ -144,7 +144,7 @@ def mx_quantize_e4m3(x: np.ndarray, block: int = MX_BLOCK):
     mf, ef = np.frexp(amax)
     e = np.where(mf > 0.875, ef - 8, ef - 9)
     e = np.where(amax == 0, MX_MIN_EXP, np.maximum(e, MX_MIN_EXP)).astype(np.int64)
-    finite = np.where(np.isfinite(xb), xb, 0).astype(np.float64)
+    finite = np.where(np.isfinite(xb) & ~bad[..., None], xb, 0).astype(np.float64)
     q = np.ldexp(finite, -e[..., None]).astype(np.float32)  # exact: a power-of-two rescale
     codes = to_e4m3(q)
     codes = np.where(bad[..., None], np.uint8(0x7F), codes).astype(np.uint8)

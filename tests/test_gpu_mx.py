@@ -135,13 +135,16 @@ def _gmm_mx(dev, lhs_bits, rhs, sc, gs, out_dtype=torch.bfloat16, group_offset=N
     return out
 
 
-CASES = [
+CASES = [  # K < 4096: the 64-deep kernel; K >= 4096: the 128-deep one
     ([5], 128, 16),
     ([1, 0, 15, 16, 17], 128, 96),
     ([31, 32, 33, 0, 3], 256, 272),
     ([127, 128, 129, 0, 3], 256, 272),
     ([300, 0, 0, 64, 257], 1024, 512),
     ([0, 0, 0], 128, 64),
+    ([5], 4096, 16),
+    ([1, 0, 15, 16, 17, 95, 97], 4096, 96),
+    ([127, 0, 129, 8], 4224, 656),
 ]
 
 
@@ -169,26 +172,28 @@ def test_gmm_mx_prequantized_lhs_and_repeat_runs(dev, rng):
     assert torch.equal(a.view(torch.int16), c.view(torch.int16))
 
 
-def test_gmm_mx_group_offset_and_zero_init(dev, rng):
+@pytest.mark.parametrize("K", [128, 4096])
+def test_gmm_mx_group_offset_and_zero_init(dev, rng, K):
     sizes = [20, 35, 0, 50, 9]
-    lhs_bits, rhs, sc, gs = _mx_case(rng, sizes, 128, 64, extra_rows=7)
+    lhs_bits, rhs, sc, gs = _mx_case(rng, sizes, K, 64, extra_rows=7)
     out = _gmm_mx(dev, lhs_bits, rhs[1:4], sc[1:4], gs, group_offset=1)
     y64, ap, written = _oracle_mx(lhs_bits, _w(rhs[1:4], sc[1:4]), gs, group_offset=1)
     assert list(np.nonzero(written)[0]) == list(range(20, 105))
     y = out.float().cpu().numpy()
     assert np.all(y[~written] == 0)
-    _check(out, y64, ap, 128, torch.bfloat16, mask=written)
+    _check(out, y64, ap, K, torch.bfloat16, mask=written)
     out2 = _gmm_mx(dev, lhs_bits, rhs[1:4], sc[1:4], gs, group_offset=1, zero_init=False)
     assert torch.equal(out2[20:105].view(torch.int16), out[20:105].view(torch.int16))
 
 
+@pytest.mark.parametrize("K", [256, 4096])
 @pytest.mark.parametrize("fused_act", [False, True])
-def test_gmm_mx_fused_row_gather_equals_gather_then_gmm(dev, rng, fused_act):
+def test_gmm_mx_fused_row_gather_equals_gather_then_gmm(dev, rng, fused_act, K):
     """lhs_row_indices in the MX mode gives the bits of quantizing the
     gathered rows: quantization is per row, so quantizing the tokens once and
     gathering their codes and scales is the same."""
     from dw_tpu_amd import fp4_weight_to_codes, gmm_v2, mx_quantize, row_gather
-    T, K, N = 150, 256, 192
+    T, N = 150, 192
     sizes = [37, 0, 120, 64, 9]
     M = sum(sizes)
     hidden = bf16_tensor(to_bf16_bits(rng.standard_normal((T, K)).astype(np.float32)), dev)
@@ -207,12 +212,13 @@ def test_gmm_mx_fused_row_gather_equals_gather_then_gmm(dev, rng, fused_act):
     assert torch.equal(got.view(torch.int16), want.view(torch.int16))
 
 
-def test_gmm_mx_fused_activation(dev, rng):
+@pytest.mark.parametrize("K", [512, 4096])
+def test_gmm_mx_fused_activation(dev, rng, K):
     """gmm1 with the fused activation in the MX mode against the oracle's
     activation of the float64 MX product (oracle.moe_block's propagated
     bound)."""
     from oracle import moe_block as omb
-    K, N = 512, 256
+    N = 256
     lhs_bits, rhs, sc, gs = _mx_case(rng, [60, 0, 130, 7], K, N)
     out = _gmm_mx(dev, lhs_bits, rhs, sc, gs, fuse_act="silu_and_mul_with_clamp")
     y64, (ap, bm), _ = _oracle_mx(lhs_bits, _w(rhs, sc), gs)
