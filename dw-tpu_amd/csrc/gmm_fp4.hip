@@ -158,7 +158,8 @@ __device__ __forceinline__ void ws_producer(const uint16_t *__restrict__ lhs, co
 
 template <class C, int AM, bool ACT>
 __device__ __forceinline__ void ws_consumer(int T, uint8_t *s_lds, int cw, int64_t row0, int rows,
-                                            int64_t col0, int N, void *__restrict__ out, int out_f32) {
+                                            int64_t col0, int N, void *__restrict__ out, int out_f32,
+                                            const void *bias, const GmmEpilogue &ep) {
   constexpr int JW = C::JWAVE, NS = C::STAGES;
   const int lane = threadIdx.x & 63, c32 = lane & 31, h = lane >> 5;
   f32x16_t acc[AM][JW];
@@ -245,7 +246,7 @@ __device__ __forceinline__ void ws_consumer(int T, uint8_t *s_lds, int cw, int64
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
   store_tile<AM, ACT, C::EP_STRIDE>(acc, (float *)(s_lds + cw * 32 * C::EP_STRIDE * 4), row0, rows, col0, N, out,
-                                     out_f32);
+                                     out_f32, bias, ep.bias_bf16, ep.act);
 }
 
 template <class C, int MB, bool ACT>
@@ -254,7 +255,7 @@ __global__ __launch_bounds__(C::THREADS) void gmm_fp4_ws_kernel(
     const uint8_t *__restrict__ wpk,
     const uint8_t *__restrict__ spk, const int32_t *__restrict__ group_sizes, int num_groups,
     const int32_t *__restrict__ group_offset, int64_t e_local, int N, void *__restrict__ out,
-    int out_f32) {
+    int out_f32, GmmEpilogue ep) {
   constexpr int NT = C::NT;
   constexpr int CW = C::CONS;
   static_assert(C::STAGES * C::STAGE >= (kMaxGroups + MB * kClsStride) * 4, "tile classes alias the stages");
@@ -290,10 +291,13 @@ __global__ __launch_bounds__(C::THREADS) void gmm_fp4_ws_kernel(
   const int64_t col0 = (int64_t)(g0 + wave) * 64;
   // Every consumer runs exactly T + 1 barriers (the producers' count),
   // whatever its row-block count.
-  if (act_mb <= 1 || MB == 1) ws_consumer<C, 1, ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32);
-  else if (act_mb == 2 || MB == 2) ws_consumer<C, (MB >= 2 ? 2 : 1), ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32);
-  else if (act_mb == 3 || MB == 3) ws_consumer<C, (MB >= 3 ? 3 : 1), ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32);
-  else ws_consumer<C, MB, ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32);
+  const void *const bias = expert_bias(ep, e, N);
+  if (act_mb <= 1 || MB == 1) ws_consumer<C, 1, ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32, bias, ep);
+  else if (act_mb == 2 || MB == 2)
+    ws_consumer<C, (MB >= 2 ? 2 : 1), ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32, bias, ep);
+  else if (act_mb == 3 || MB == 3)
+    ws_consumer<C, (MB >= 3 ? 3 : 1), ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32, bias, ep);
+  else ws_consumer<C, MB, ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32, bias, ep);
 }
 
 // zero_initialize: zero rows outside [start(go), start(go + E_local)).
@@ -340,7 +344,7 @@ template <int MB, int CW, int JW, int NP, int NS, bool ACT = false>
 static int launch_gmm_ws(const uint16_t *lhs, const int32_t *row_idx, int64_t lhs_rows, int64_t M, int64_t K,
                          const uint8_t *w, const uint8_t *s,
                          const int32_t *gs, int ng, const int32_t *go, int64_t e_local, int64_t N, void *out,
-                         int out_f32, hipStream_t st) {
+                         int out_f32, const GmmEpilogue &ep, hipStream_t st) {
   using C = WsCfg<MB, CW, JW, NP, NS>;
   constexpr int MT = 32 * MB, NT = C::NT;
   const int64_t n_tiles = (N + NT - 1) / NT;
@@ -351,65 +355,97 @@ static int launch_gmm_ws(const uint16_t *lhs, const int32_t *row_idx, int64_t lh
   DWM_UNSUPPORTED_IF(K > (1 << 24), "gmm_fp4: K <= 2^24 required");
   hipLaunchKernelGGL((gmm_fp4_ws_kernel<C, MB, ACT>), dim3((unsigned)grid), dim3(C::THREADS), 0, st, lhs, row_idx,
                      lhs_rows, M, (int)K, w,
-                     s, gs, ng, go, e_local, (int)N, out, out_f32);
+                     s, gs, ng, go, e_local, (int)N, out, out_f32, ep);
   return launch_status("gmm_fp4");
+}
+
+// The bf16 grouped matmul (arguments checked by the caller).
+int launch_gmm_bf16(const uint16_t *lhs, const int32_t *row_idx, int64_t lhs_rows, int64_t M, int64_t K,
+                    const uint8_t *weight, const uint8_t *scale, const int32_t *group_sizes, int num_groups,
+                    const int32_t *group_offset, int64_t E_local, int64_t N, void *out, int out_f32, bool gated,
+                    const GmmEpilogue &ep, hipStream_t st) {
+  // 96-row x 512-column tiles, 8 consumer + 4 producer waves, four 64-deep
+  // K stages (120 KB of LDS, under 168 VGPRs: one block of 12 waves per CU).
+  // Measured fastest on the decode and prefill workloads among the tile,
+  // wave-split and pipeline-depth variants tried.
+  if (gated)
+    return launch_gmm_ws<3, 8, 2, 4, 4, true>(lhs, row_idx, lhs_rows, M, K, weight, scale, group_sizes, num_groups,
+                                              group_offset, E_local, N, out, out_f32, ep, st);
+  return launch_gmm_ws<3, 8, 2, 4, 4>(lhs, row_idx, lhs_rows, M, K, weight, scale, group_sizes, num_groups,
+                                      group_offset, E_local, N, out, out_f32, ep, st);
+}
+
+// Checks shared by every form of the grouped matmul, then the launch.
+static int gmm_run(const dwm_gmm_lhs &L, int64_t M, int64_t K, const uint8_t *weight, const uint8_t *scale,
+                   const void *bias, int bias_dtype, const int32_t *group_sizes, int num_groups,
+                   const int32_t *group_offset, int64_t E_local, int64_t N, void *out, int out_dtype, int zero_init,
+                   int fuse_act, void *stream) {
+  const bool mx = L.scale != nullptr;
+  const char *const what = mx ? "gmm_fp4_mx" : (L.row_idx ? "gmm_fp4_gather" : "gmm_fp4");
+  DWM_CHECK_ARG(M >= 0 && K > 0 && N > 0 && E_local >= 0 && num_groups >= 0 && L.rows >= 0,
+                "%s: bad sizes M=%lld K=%lld N=%lld E_local=%lld groups=%d lhs_rows=%lld", what, (long long)M,
+                (long long)K, (long long)N, (long long)E_local, num_groups, (long long)L.rows);
+  DWM_CHECK_ARG(out_dtype == DWM_BF16 || out_dtype == DWM_F32, "%s: bad out dtype %d", what, out_dtype);
+  DWM_CHECK_ARG(fuse_act >= DWM_ACT_NONE && fuse_act <= DWM_ACT_SWIGLUOAI, "%s: bad fuse_act %d", what, fuse_act);
+  DWM_CHECK_ARG(!bias || bias_dtype == DWM_F32 || bias_dtype == DWM_BF16, "%s: bias dtype must be f32 or bf16", what);
+  DWM_CHECK_ARG(L.row_idx || L.rows == M, "%s: without row_idx lhs must have M rows (%lld != %lld)", what,
+                (long long)L.rows, (long long)M);
+  DWM_UNSUPPORTED_IF(fuse_act != DWM_ACT_NONE && N % 64 != 0, "%s: fuse_act needs N %% 64 == 0 (N=%lld)", what,
+                     (long long)N);
+  DWM_UNSUPPORTED_IF(K % 128 != 0 || N % 16 != 0, "%s: K %% 128 == 0 and N %% 16 == 0 required", what);
+  DWM_UNSUPPORTED_IF(num_groups > kMaxGroups, "%s: at most %d groups (got %d)", what, kMaxGroups, num_groups);
+  DWM_UNSUPPORTED_IF(K > (1 << 24) || N > (1 << 30), "%s: K <= 2^24 and N < 2^30 required", what);
+  if (M == 0) return DWM_OK;
+  DWM_CHECK_ARG(L.data && out && (num_groups == 0 || group_sizes) && (!L.row_idx || L.rows > 0),
+                "%s: null pointer or empty lhs with rows to read", what);
+  // The MX kernels and the fused gather address lhs rows with 32-bit byte offsets.
+  DWM_UNSUPPORTED_IF((mx || L.row_idx) && L.rows * K * (mx ? 1 : 2) >= (1ll << 32),
+                     "%s: lhs of %lld rows is too large", what, (long long)L.rows);
+  DWM_CHECK_ARG(E_local == 0 || (weight && scale), "%s: null weight pointer", what);
+  DWM_CHECK_ARG((uintptr_t)L.data % 16 == 0 && (uintptr_t)weight % 16 == 0 && (uintptr_t)out % 16 == 0 &&
+                    (uintptr_t)scale % 4 == 0 && (uintptr_t)L.scale % 4 == 0,
+                "%s: lhs, weight and out must be 16-byte aligned, the scales 4-byte aligned", what);
+  DWM_CHECK_ARG(!bias || (uintptr_t)bias % 4 == 0, "%s: bias must be 4-byte aligned", what);
+  hipStream_t st = as_stream(stream);
+  if (zero_init) {
+    const int64_t n_out = fuse_act != DWM_ACT_NONE ? N / 2 : N;
+    int rc = launch_gmm_zero_rows(group_sizes, num_groups, group_offset, E_local, M, n_out, out,
+                                  out_dtype == DWM_F32 ? 4 : 2, st);
+    if (rc != DWM_OK) return rc;
+  }
+  if (E_local == 0 || num_groups == 0) return DWM_OK;
+  const GmmEpilogue ep{bias, bias && bias_dtype == DWM_BF16 ? 1 : 0, fuse_act};
+  const int out_f32 = out_dtype == DWM_F32;
+  const bool gated = fuse_act != DWM_ACT_NONE;
+  if (mx)
+    return launch_gmm_mx((const uint8_t *)L.data, L.scale, L.row_idx, L.rows, M, K, weight, scale, group_sizes,
+                         num_groups, group_offset, E_local, N, out, out_f32, gated, ep, st);
+  return launch_gmm_bf16((const uint16_t *)L.data, L.row_idx, L.rows, M, K, weight, scale, group_sizes, num_groups,
+                         group_offset, E_local, N, out, out_f32, gated, ep, st);
 }
 
 }  // namespace dwm
 
 using namespace dwm;
 
-static int gmm_fp4_impl(const uint16_t *lhs, const int32_t *row_idx, int64_t lhs_rows, int64_t M, int64_t K,
-                        const uint8_t *weight,
-                           const uint8_t *scale, const int32_t *group_sizes, int num_groups,
-                           const int32_t *group_offset, int64_t E_local, int64_t N, void *out,
-                           int out_dtype, int zero_init, int fuse_act, void *stream) {
+extern "C" int dwm_gmm_fp4_ex(const dwm_gmm_lhs *lhs, int64_t M, int64_t K, const uint8_t *weight,
+                              const uint8_t *scale, const void *rhs_bias, int bias_dtype, const int32_t *group_sizes,
+                              int num_groups, const int32_t *group_offset, int64_t E_local, int64_t N, void *out,
+                              int out_dtype, int zero_init, int fuse_act, void *stream) {
   clear_error();
-  DWM_CHECK_ARG(M >= 0 && K > 0 && N > 0 && E_local >= 0 && num_groups >= 0,
-                "gmm_fp4: bad sizes M=%lld K=%lld N=%lld E_local=%lld groups=%d", (long long)M,
-                (long long)K, (long long)N, (long long)E_local, num_groups);
-  DWM_CHECK_ARG(out_dtype == DWM_BF16 || out_dtype == DWM_F32, "gmm_fp4: bad out dtype %d", out_dtype);
-  DWM_CHECK_ARG(fuse_act == DWM_ACT_NONE || fuse_act == DWM_ACT_SILU_MUL_CLAMP, "gmm_fp4: bad fuse_act %d", fuse_act);
-  DWM_UNSUPPORTED_IF(fuse_act != DWM_ACT_NONE && N % 64 != 0, "gmm_fp4: fuse_act needs N %% 64 == 0 (N=%lld)",
-                     (long long)N);
-  DWM_UNSUPPORTED_IF(K % 128 != 0 || N % 16 != 0, "gmm_fp4: K %% 128 == 0 and N %% 16 == 0 required");
-  DWM_UNSUPPORTED_IF(num_groups > kMaxGroups, "gmm_fp4: at most %d groups (got %d)", kMaxGroups, num_groups);
-  DWM_UNSUPPORTED_IF(K > (1 << 30) || N > (1 << 30), "gmm_fp4: K, N must be < 2^30");
-  if (M == 0) return DWM_OK;
-  DWM_CHECK_ARG(lhs && out && (num_groups == 0 || group_sizes), "gmm_fp4: null pointer");
-  // The fused gather addresses lhs rows with 32-bit byte offsets.
-  DWM_UNSUPPORTED_IF(row_idx && lhs_rows * K * 2 >= (1ll << 32), "gmm_fp4_gather: lhs of %lld rows is too large",
-                     (long long)lhs_rows);
-  DWM_CHECK_ARG(E_local == 0 || (weight && scale), "gmm_fp4: null weight pointer");
-  DWM_CHECK_ARG((uintptr_t)lhs % 16 == 0 && (uintptr_t)weight % 16 == 0 && (uintptr_t)out % 16 == 0 &&
-                    (uintptr_t)scale % 4 == 0,
-                "gmm_fp4: lhs, weight and out must be 16-byte aligned, scale 4-byte aligned");
-  hipStream_t st = as_stream(stream);
-  const int elem = out_dtype == DWM_F32 ? 4 : 2;
-  if (zero_init) {
-    const int64_t n_out = fuse_act != DWM_ACT_NONE ? N / 2 : N;
-    int rc = launch_gmm_zero_rows(group_sizes, num_groups, group_offset, E_local, M, n_out, out, elem, st);
-    if (rc != DWM_OK) return rc;
-  }
-  if (E_local == 0 || num_groups == 0) return DWM_OK;
-  const int out_f32 = out_dtype == DWM_F32;
-  // 96-row x 512-column tiles, 8 consumer + 4 producer waves, four 64-deep
-  // K stages (120 KB of LDS, under 168 VGPRs: one block of 12 waves per CU).
-  // Measured fastest on the decode and prefill workloads among the tile,
-  // wave-split and pipeline-depth variants tried.
-  if (fuse_act == DWM_ACT_SILU_MUL_CLAMP)
-    return launch_gmm_ws<3, 8, 2, 4, 4, true>(lhs, row_idx, lhs_rows, M, K, weight, scale, group_sizes, num_groups, group_offset,
-                                              E_local, N, out, out_f32, st);
-  return launch_gmm_ws<3, 8, 2, 4, 4>(lhs, row_idx, lhs_rows, M, K, weight, scale, group_sizes, num_groups, group_offset, E_local, N,
-                                      out, out_f32, st);
+  DWM_CHECK_ARG(lhs, "gmm_fp4_ex: null lhs descriptor");
+  return gmm_run(*lhs, M, K, weight, scale, rhs_bias, bias_dtype, group_sizes, num_groups, group_offset, E_local, N,
+                 out, out_dtype, zero_init, fuse_act, stream);
 }
 
 extern "C" int dwm_gmm_fp4(const uint16_t *lhs, int64_t M, int64_t K, const uint8_t *weight,
                            const uint8_t *scale, const int32_t *group_sizes, int num_groups,
                            const int32_t *group_offset, int64_t E_local, int64_t N, void *out,
                            int out_dtype, int zero_init, int fuse_act, void *stream) {
-  return gmm_fp4_impl(lhs, nullptr, M, M, K, weight, scale, group_sizes, num_groups, group_offset, E_local, N, out,
-                      out_dtype, zero_init, fuse_act, stream);
+  clear_error();
+  const dwm_gmm_lhs L{lhs, nullptr, M, nullptr};
+  return gmm_run(L, M, K, weight, scale, nullptr, 0, group_sizes, num_groups, group_offset, E_local, N, out,
+                 out_dtype, zero_init, fuse_act, stream);
 }
 
 extern "C" int dwm_gmm_fp4_gather(const uint16_t *lhs, int64_t lhs_rows, const int32_t *row_idx, int64_t M,
@@ -421,6 +457,18 @@ extern "C" int dwm_gmm_fp4_gather(const uint16_t *lhs, int64_t lhs_rows, const i
   DWM_CHECK_ARG(lhs_rows >= 0 && M >= 0, "gmm_fp4_gather: bad sizes lhs_rows=%lld M=%lld", (long long)lhs_rows,
                 (long long)M);
   DWM_CHECK_ARG(M == 0 || (row_idx && lhs_rows > 0), "gmm_fp4_gather: null row_idx or empty lhs with rows to gather");
-  return gmm_fp4_impl(lhs, row_idx, lhs_rows, M, K, weight, scale, group_sizes, num_groups, group_offset, E_local, N,
-                      out, out_dtype, zero_init, fuse_act, stream);
+  const dwm_gmm_lhs L{lhs, nullptr, lhs_rows, row_idx};
+  return gmm_run(L, M, K, weight, scale, nullptr, 0, group_sizes, num_groups, group_offset, E_local, N, out,
+                 out_dtype, zero_init, fuse_act, stream);
+}
+
+extern "C" int dwm_gmm_fp4_mx(const uint8_t *lhs, const uint8_t *lhs_scale, int64_t lhs_rows, const int32_t *row_idx,
+                              int64_t M, int64_t K, const uint8_t *weight, const uint8_t *scale,
+                              const int32_t *group_sizes, int num_groups, const int32_t *group_offset, int64_t E_local,
+                              int64_t N, void *out, int out_dtype, int zero_init, int fuse_act, void *stream) {
+  clear_error();
+  DWM_CHECK_ARG(lhs_scale || M == 0, "gmm_fp4_mx: null lhs_scale");
+  const dwm_gmm_lhs L{lhs, lhs_scale ? lhs_scale : (const uint8_t *)lhs, lhs_rows, row_idx};
+  return gmm_run(L, M, K, weight, scale, nullptr, 0, group_sizes, num_groups, group_offset, E_local, N, out,
+                 out_dtype, zero_init, fuse_act, stream);
 }

@@ -233,7 +233,8 @@ __device__ __forceinline__ void mx_producer(const uint8_t *__restrict__ lhs, con
 
 template <class C, int AM, bool ACT>
 __device__ __forceinline__ void mx_consumer(int T, uint8_t *s_lds, int cw, int64_t row0, int rows, int64_t col0,
-                                            int N, void *__restrict__ out, int out_f32) {
+                                            int N, void *__restrict__ out, int out_f32, const void *bias,
+                                            const GmmEpilogue &ep) {
   constexpr int NS = C::STAGES;
   const int lane = threadIdx.x & 63, c32 = lane & 31, h = lane >> 5;
   f32x16_t acc[AM][2];
@@ -323,7 +324,7 @@ __device__ __forceinline__ void mx_consumer(int T, uint8_t *s_lds, int cw, int64
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
   store_tile<AM, ACT, C::EP_STRIDE>(acc, (float *)(s_lds + cw * 32 * C::EP_STRIDE * 4), row0, rows, col0, N, out,
-                                    out_f32);
+                                    out_f32, bias, ep.bias_bf16, ep.act);
 }
 
 template <class C, int MB, bool ACT>
@@ -331,7 +332,7 @@ __global__ __launch_bounds__(C::THREADS) void gmm_mx_kernel(
     const uint8_t *__restrict__ lhs, const uint8_t *__restrict__ lsc, const int32_t *__restrict__ row_idx,
     int64_t lhs_rows, int64_t M, int K, const uint8_t *__restrict__ wpk, const uint8_t *__restrict__ spk,
     const int32_t *__restrict__ group_sizes, int num_groups, const int32_t *__restrict__ group_offset,
-    int64_t e_local, int N, void *__restrict__ out, int out_f32) {
+    int64_t e_local, int N, void *__restrict__ out, int out_f32, GmmEpilogue ep) {
   constexpr int CW = C::CONS, NP = C::NPROD;
   static_assert(C::STAGES * C::STAGE >= (kMaxGroups + MB * kClsStride) * 4, "tile classes alias the stages");
   __shared__ __attribute__((aligned(1024))) uint8_t s_lds[C::STAGES * C::STAGE];
@@ -377,9 +378,10 @@ __global__ __launch_bounds__(C::THREADS) void gmm_mx_kernel(
   }
   const int act_mb = (rows + 31) >> 5;
   const int64_t col0 = (int64_t)(g0 + wave) * 64;
-  if (act_mb <= 1 || MB == 1) mx_consumer<C, 1, ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32);
-  else if (act_mb == 2 || MB == 2) mx_consumer<C, (MB >= 2 ? 2 : 1), ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32);
-  else mx_consumer<C, MB, ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32);
+  const void *const bias = expert_bias(ep, e, N);
+  if (act_mb <= 1 || MB == 1) mx_consumer<C, 1, ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32, bias, ep);
+  else if (act_mb == 2 || MB == 2) mx_consumer<C, (MB >= 2 ? 2 : 1), ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32, bias, ep);
+  else mx_consumer<C, MB, ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32, bias, ep);
 }
 
 // ---------------------------------------------------------------------------
@@ -489,7 +491,8 @@ __device__ __forceinline__ void mx128_producer(const uint8_t *__restrict__ lhs, 
 
 template <class C, int AM, bool ACT>
 __device__ __forceinline__ void mx128_consumer(int T, uint8_t *s_lds, int cw, int64_t row0, int rows, int64_t col0,
-                                               int N, void *__restrict__ out, int out_f32) {
+                                               int N, void *__restrict__ out, int out_f32, const void *bias,
+                                            const GmmEpilogue &ep) {
   constexpr int NS = C::STAGES;
   const int lane = threadIdx.x & 63, c32 = lane & 31, h = lane >> 5;
   f32x16_t acc[AM][2];
@@ -553,7 +556,7 @@ __device__ __forceinline__ void mx128_consumer(int T, uint8_t *s_lds, int cw, in
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
   store_tile<AM, ACT, C::EP_STRIDE>(acc, (float *)(s_lds + cw * 32 * C::EP_STRIDE * 4), row0, rows, col0, N, out,
-                                    out_f32);
+                                    out_f32, bias, ep.bias_bf16, ep.act);
 }
 
 template <class C, int MB, bool ACT>
@@ -561,7 +564,7 @@ __global__ __launch_bounds__(C::THREADS) void gmm_mx128_kernel(
     const uint8_t *__restrict__ lhs, const uint8_t *__restrict__ lsc, const int32_t *__restrict__ row_idx,
     int64_t lhs_rows, int64_t M, int K, const uint8_t *__restrict__ wpk, const uint8_t *__restrict__ spk,
     const int32_t *__restrict__ group_sizes, int num_groups, const int32_t *__restrict__ group_offset,
-    int64_t e_local, int N, void *__restrict__ out, int out_f32) {
+    int64_t e_local, int N, void *__restrict__ out, int out_f32, GmmEpilogue ep) {
   constexpr int CW = C::CONS, NP = C::NPROD;
   static_assert(C::STAGES * C::STAGE >= (kMaxGroups + MB * kClsStride) * 4, "tile classes alias the stages");
   __shared__ __attribute__((aligned(1024))) uint8_t s_lds[C::STAGES * C::STAGE];
@@ -605,15 +608,16 @@ __global__ __launch_bounds__(C::THREADS) void gmm_mx128_kernel(
   }
   const int act_mb = (rows + 31) >> 5;
   const int64_t col0 = (int64_t)(g0 + wave) * 64;
-  if (act_mb <= 1 || MB == 1) mx128_consumer<C, 1, ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32);
-  else if (act_mb == 2 || MB == 2) mx128_consumer<C, (MB >= 2 ? 2 : 1), ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32);
-  else mx128_consumer<C, MB, ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32);
+  const void *const bias = expert_bias(ep, e, N);
+  if (act_mb <= 1 || MB == 1) mx128_consumer<C, 1, ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32, bias, ep);
+  else if (act_mb == 2 || MB == 2) mx128_consumer<C, (MB >= 2 ? 2 : 1), ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32, bias, ep);
+  else mx128_consumer<C, MB, ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32, bias, ep);
 }
 
 template <class C, int MB, bool ACT, bool STEP128>
-static int launch_gmm_mx(const uint8_t *lhs, const uint8_t *lsc, const int32_t *row_idx, int64_t lhs_rows, int64_t M,
-                         int64_t K, const uint8_t *w, const uint8_t *s, const int32_t *gs, int ng, const int32_t *go,
-                         int64_t e_local, int64_t N, void *out, int out_f32, hipStream_t st) {
+static int launch_mx(const uint8_t *lhs, const uint8_t *lsc, const int32_t *row_idx, int64_t lhs_rows, int64_t M,
+                     int64_t K, const uint8_t *w, const uint8_t *s, const int32_t *gs, int ng, const int32_t *go,
+                     int64_t e_local, int64_t N, void *out, int out_f32, const GmmEpilogue &ep, hipStream_t st) {
   constexpr int MT = 32 * MB, NT = C::NT;
   const int64_t n_tiles = (N + NT - 1) / NT;
   const int64_t max_tiles = ((M + MT - 1) / MT + e_local) * n_tiles;
@@ -621,11 +625,33 @@ static int launch_gmm_mx(const uint8_t *lhs, const uint8_t *lsc, const int32_t *
   DWM_UNSUPPORTED_IF(grid > (1ll << 31) - 1, "gmm_fp4_mx: too many tiles (%lld)", (long long)grid);
   if constexpr (STEP128)
     hipLaunchKernelGGL((gmm_mx128_kernel<C, MB, ACT>), dim3((unsigned)grid), dim3(C::THREADS), 0, st, lhs, lsc,
-                       row_idx, lhs_rows, M, (int)K, w, s, gs, ng, go, e_local, (int)N, out, out_f32);
+                       row_idx, lhs_rows, M, (int)K, w, s, gs, ng, go, e_local, (int)N, out, out_f32, ep);
   else
     hipLaunchKernelGGL((gmm_mx_kernel<C, MB, ACT>), dim3((unsigned)grid), dim3(C::THREADS), 0, st, lhs, lsc, row_idx,
-                       lhs_rows, M, (int)K, w, s, gs, ng, go, e_local, (int)N, out, out_f32);
+                       lhs_rows, M, (int)K, w, s, gs, ng, go, e_local, (int)N, out, out_f32, ep);
   return launch_status("gmm_fp4_mx");
+}
+
+// The MX grouped matmul (arguments checked by the caller).
+int launch_gmm_mx(const uint8_t *lhs, const uint8_t *lhs_scale, const int32_t *row_idx, int64_t lhs_rows, int64_t M,
+                  int64_t K, const uint8_t *weight, const uint8_t *scale, const int32_t *group_sizes, int num_groups,
+                  const int32_t *group_offset, int64_t E_local, int64_t N, void *out, int out_f32, bool gated,
+                  const GmmEpilogue &ep, hipStream_t st) {
+  // 96-row x 512-column tiles, 8 consumer + 4 producer waves.  64-deep K
+  // steps in a five-stage ring (two published per barrier, two in flight),
+  // or 128-deep steps in a three-stage ring (one published, one in flight).
+  using C64 = MxCfg<3, 8, 4, 5>;
+  using C128 = Mx128Cfg<3, 8, 4, 3>;
+  const bool deep = K >= kMx128MinK;
+  if (gated)
+    return deep ? launch_mx<C128, 3, true, true>(lhs, lhs_scale, row_idx, lhs_rows, M, K, weight, scale, group_sizes,
+                                                 num_groups, group_offset, E_local, N, out, out_f32, ep, st)
+                : launch_mx<C64, 3, true, false>(lhs, lhs_scale, row_idx, lhs_rows, M, K, weight, scale, group_sizes,
+                                                 num_groups, group_offset, E_local, N, out, out_f32, ep, st);
+  return deep ? launch_mx<C128, 3, false, true>(lhs, lhs_scale, row_idx, lhs_rows, M, K, weight, scale, group_sizes,
+                                                num_groups, group_offset, E_local, N, out, out_f32, ep, st)
+              : launch_mx<C64, 3, false, false>(lhs, lhs_scale, row_idx, lhs_rows, M, K, weight, scale, group_sizes,
+                                                num_groups, group_offset, E_local, N, out, out_f32, ep, st);
 }
 
 }  // namespace dwm
@@ -649,61 +675,3 @@ extern "C" int dwm_mx_quant_e4m3(const uint16_t *x, int64_t rows, int64_t K, uin
   return launch_status("mx_quant_e4m3");
 }
 
-extern "C" int dwm_gmm_fp4_mx(const uint8_t *lhs, const uint8_t *lhs_scale, int64_t lhs_rows, const int32_t *row_idx,
-                              int64_t M, int64_t K, const uint8_t *weight, const uint8_t *scale,
-                              const int32_t *group_sizes, int num_groups, const int32_t *group_offset, int64_t E_local,
-                              int64_t N, void *out, int out_dtype, int zero_init, int fuse_act, void *stream) {
-  clear_error();
-  DWM_CHECK_ARG(M >= 0 && K > 0 && N > 0 && E_local >= 0 && num_groups >= 0 && lhs_rows >= 0,
-                "gmm_fp4_mx: bad sizes M=%lld K=%lld N=%lld E_local=%lld groups=%d lhs_rows=%lld", (long long)M,
-                (long long)K, (long long)N, (long long)E_local, num_groups, (long long)lhs_rows);
-  DWM_CHECK_ARG(out_dtype == DWM_BF16 || out_dtype == DWM_F32, "gmm_fp4_mx: bad out dtype %d", out_dtype);
-  DWM_CHECK_ARG(fuse_act == DWM_ACT_NONE || fuse_act == DWM_ACT_SILU_MUL_CLAMP, "gmm_fp4_mx: bad fuse_act %d",
-                fuse_act);
-  DWM_CHECK_ARG(row_idx || lhs_rows == M, "gmm_fp4_mx: without row_idx lhs must have M rows (%lld != %lld)",
-                (long long)lhs_rows, (long long)M);
-  DWM_UNSUPPORTED_IF(fuse_act != DWM_ACT_NONE && N % 64 != 0, "gmm_fp4_mx: fuse_act needs N %% 64 == 0 (N=%lld)",
-                     (long long)N);
-  DWM_UNSUPPORTED_IF(K % 128 != 0 || N % 16 != 0, "gmm_fp4_mx: K %% 128 == 0 and N %% 16 == 0 required");
-  DWM_UNSUPPORTED_IF(num_groups > kMaxGroups, "gmm_fp4_mx: at most %d groups (got %d)", kMaxGroups, num_groups);
-  DWM_UNSUPPORTED_IF(K > (1 << 24) || N > (1 << 30), "gmm_fp4_mx: K <= 2^24, N < 2^30 required");
-  if (M == 0) return DWM_OK;
-  DWM_CHECK_ARG(lhs && lhs_scale && out && (num_groups == 0 || group_sizes) && (!row_idx || lhs_rows > 0),
-                "gmm_fp4_mx: null pointer or empty lhs");
-  // lhs rows are addressed with 32-bit byte offsets.
-  DWM_UNSUPPORTED_IF(lhs_rows * K >= (1ll << 32), "gmm_fp4_mx: lhs of %lld rows is too large", (long long)lhs_rows);
-  DWM_CHECK_ARG(E_local == 0 || (weight && scale), "gmm_fp4_mx: null weight pointer");
-  DWM_CHECK_ARG((uintptr_t)lhs % 16 == 0 && (uintptr_t)weight % 16 == 0 && (uintptr_t)out % 16 == 0 &&
-                    (uintptr_t)scale % 4 == 0 && (uintptr_t)lhs_scale % 4 == 0,
-                "gmm_fp4_mx: lhs, weight and out must be 16-byte aligned, the scales 4-byte aligned");
-  hipStream_t st = as_stream(stream);
-  const int elem = out_dtype == DWM_F32 ? 4 : 2;
-  if (zero_init) {
-    const int64_t n_out = fuse_act != DWM_ACT_NONE ? N / 2 : N;
-    int rc = launch_gmm_zero_rows(group_sizes, num_groups, group_offset, E_local, M, n_out, out, elem, st);
-    if (rc != DWM_OK) return rc;
-  }
-  if (E_local == 0 || num_groups == 0) return DWM_OK;
-  const int out_f32 = out_dtype == DWM_F32;
-  // 96-row x 512-column tiles, 8 consumer + 4 producer waves, a ring of
-  // 64-deep K stages (two published per barrier, the rest in flight).
-  // 96-row x 512-column tiles, 8 consumer + 4 producer waves.  64-deep K
-  // steps in a five-stage ring (two published per barrier, two in flight),
-  // or 128-deep steps in a three-stage ring (one published, one in flight).
-  using C64 = MxCfg<3, 8, 4, 5>;
-  using C128 = Mx128Cfg<3, 8, 4, 3>;
-  const bool deep = K >= kMx128MinK;
-  if (fuse_act == DWM_ACT_SILU_MUL_CLAMP)
-    return deep ? launch_gmm_mx<C128, 3, true, true>(lhs, lhs_scale, row_idx, lhs_rows, M, K, weight, scale,
-                                                      group_sizes, num_groups, group_offset, E_local, N, out,
-                                                      out_f32, st)
-                : launch_gmm_mx<C64, 3, true, false>(lhs, lhs_scale, row_idx, lhs_rows, M, K, weight, scale,
-                                                      group_sizes, num_groups, group_offset, E_local, N, out,
-                                                      out_f32, st);
-  return deep ? launch_gmm_mx<C128, 3, false, true>(lhs, lhs_scale, row_idx, lhs_rows, M, K, weight, scale,
-                                                     group_sizes, num_groups, group_offset, E_local, N, out, out_f32,
-                                                     st)
-              : launch_gmm_mx<C64, 3, false, false>(lhs, lhs_scale, row_idx, lhs_rows, M, K, weight, scale,
-                                                     group_sizes, num_groups, group_offset, E_local, N, out, out_f32,
-                                                     st);
-}

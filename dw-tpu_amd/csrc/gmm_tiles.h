@@ -122,11 +122,34 @@ __device__ __forceinline__ bool find_tile(const int32_t *__restrict__ group_size
   return true;
 }
 
-// silu_and_mul_with_clamp on one (gate, up) accumulator pair, in f32.
-__device__ __forceinline__ float silu_mul_clamp(float gate, float up) {
-  const float g = fminf(gate, kSwigluLimit);
-  const float u = fminf(fmaxf(up, -kSwigluLimit), kSwigluLimit);
-  return g / (1.0f + expf(-g)) * u;
+// The fused activation of one (gate, up) accumulator pair, in f32 (the
+// activations of apply_act_fn, patches/tpu-inference-experimental/
+// fused-moe-fp4/0901-...:57-66).
+__device__ __forceinline__ float act_pair(int act, float gate, float up) {
+  switch (act) {
+    case DWM_ACT_SILU_MUL_CLAMP: {  // DeepSeek V4, swiglu_limit 10
+      const float g = fminf(gate, kSwigluLimit);
+      const float u = fminf(fmaxf(up, -kSwigluLimit), kSwigluLimit);
+      return g / (1.0f + expf(-g)) * u;
+    }
+    case DWM_ACT_SILU_MUL:
+      return gate / (1.0f + expf(-gate)) * up;
+    case DWM_ACT_GELU_TANH_MUL: {  // jax.nn.gelu's default (tanh) form
+      const float inner = 0.7978845608028654f * (gate + 0.044715f * (gate * gate * gate));
+      return gate * (0.5f * (1.0f + tanhf(inner))) * up;
+    }
+    case DWM_ACT_SWIGLUOAI: {  // GPT-OSS: alpha 1.702, limit 7
+      const float g = fminf(gate, 7.0f);
+      const float u = fminf(fmaxf(up, -7.0f), 7.0f);
+      return g / (1.0f + expf(-1.702f * g)) * (u + 1.0f);
+    }
+    default:
+      return 0.0f;
+  }
+}
+
+__device__ __forceinline__ float bias_at(const void *bias, int bias_bf16, int64_t i) {
+  return bias_bf16 ? bf16_bits_to_f32(((const uint16_t *)bias)[i]) : ((const float *)bias)[i];
 }
 
 // Stores 8 consecutive output values of one row (16-byte bf16 or 2 x 16-byte f32
@@ -153,31 +176,41 @@ __device__ __forceinline__ void store8(void *__restrict__ out, int64_t o, const 
 
 // Writes one consumer wave's accumulators acc[mb][j] (the 32 x 32 MFMA
 // layout: register r of lane (c32, h) is row 8 (r / 4) + 4 h + r % 4, column
-// c32 of 32-column block j) for its 64 columns col0 .. col0 + 63 through a
-// private LDS region `ep` of 32 rows x ES floats, 32 rows at a time, as whole
-// 8-column runs of a row.  With ACT, block 0 is the gate and block 1 the up
-// projection of the same 32 output columns (gate_up prepack).
+// c32 of 32-column block j) for its 64 packed columns col0 .. col0 + 63
+// through a private LDS region `ep` of 32 rows x ES floats, 32 rows at a
+// time, as whole 8-column runs of a row.  `bias` (NULL, or this expert's
+// [N] row, f32 or bf16) is added to the f32 accumulators first.  With ACT,
+// block 0 holds the gate and block 1 the up projection of the same 32 output
+// columns (gate_up prepack: packed column 64 g + 32 j + c is source column
+// j N/2 + 32 g + c) and `act` (DWM_ACT_*) combines them.
 template <int AM, bool ACT, int ES>
 __device__ __forceinline__ void store_tile(const f32x16_t (&acc)[AM][2], float *ep, int64_t row0, int rows,
-                                           int64_t col0, int N, void *__restrict__ out, int out_f32) {
+                                           int64_t col0, int N, void *__restrict__ out, int out_f32,
+                                           const void *__restrict__ bias, int bias_bf16, int act) {
   const int lane = threadIdx.x & 63, c32 = lane & 31, h = lane >> 5;
   constexpr int CO = ACT ? 32 : 64;  // output columns of this wave
   const int64_t n_out = ACT ? N / 2 : N;
   const int64_t ocol0 = ACT ? col0 / 2 : col0;
+  // The bias of this lane's two accumulator columns (source column order).
+  float b0 = 0.0f, b1 = 0.0f;
+  if (bias) {
+    const int64_t s0 = ACT ? col0 / 2 + c32 : col0 + c32;
+    const int64_t s1 = ACT ? N / 2 + col0 / 2 + c32 : col0 + 32 + c32;
+    if (s0 < N) b0 = bias_at(bias, bias_bf16, s0);
+    if (s1 < N) b1 = bias_at(bias, bias_bf16, s1);
+  }
 #pragma unroll
   for (int mb = 0; mb < AM; ++mb) {
-    // The 32x32 accumulator layout: register r of lane (c32, h) is row
-    // 8 (r / 4) + 4 h + r % 4, column c32.
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int lr = 8 * (r >> 2) + 4 * h + (r & 3);
+      const float v0 = bias ? acc[mb][0][r] + b0 : acc[mb][0][r];
+      const float v1 = bias ? acc[mb][1][r] + b1 : acc[mb][1][r];
       if constexpr (ACT) {
-        // Half 0 of the group is the gate, half 1 the up projection of the
-        // same 32 output columns (gate_up prepack).
-        ep[lr * ES + c32] = silu_mul_clamp(acc[mb][0][r], acc[mb][1][r]);
+        ep[lr * ES + c32] = act_pair(act, v0, v1);
       } else {
-        ep[lr * ES + c32] = acc[mb][0][r];
-        ep[lr * ES + 32 + c32] = acc[mb][1][r];
+        ep[lr * ES + c32] = v0;
+        ep[lr * ES + 32 + c32] = v1;
       }
     }
     // Lane q of chunk i covers row q / (CO / 8), columns 8 (q % (CO / 8)) .. + 7.
@@ -200,8 +233,32 @@ __device__ __forceinline__ void store_tile(const f32x16_t (&acc)[AM][2], float *
   }
 }
 
+// Epilogue inputs every gmm kernel passes through to store_tile.
+struct GmmEpilogue {
+  const void *bias;  // [E_local, N] (f32 or bf16) or NULL
+  int bias_bf16;
+  int act;           // DWM_ACT_*
+};
+
+// The bias row of local expert e (NULL when there is no bias).
+__device__ __forceinline__ const void *expert_bias(const GmmEpilogue &ep, int64_t e, int N) {
+  return ep.bias ? (const void *)((const uint8_t *)ep.bias + e * (int64_t)N * (ep.bias_bf16 ? 2 : 4)) : nullptr;
+}
+
 // Zeroes the rows outside the local groups (zero_initialize); host side.
 int launch_gmm_zero_rows(const int32_t *group_sizes, int num_groups, const int32_t *group_offset, int64_t e_local,
                          int64_t M, int64_t n_out, void *out, int elem_bytes, hipStream_t st);
+
+// The grouped matmuls behind the C ABI (host side): bf16 lhs (gmm_fp4.hip)
+// and MX lhs (gmm_mx.hip).  Arguments as dwm_gmm_fp4_ex, checked by the
+// caller; `gated` = the activation reads gate/up pairs.
+int launch_gmm_bf16(const uint16_t *lhs, const int32_t *row_idx, int64_t lhs_rows, int64_t M, int64_t K,
+                    const uint8_t *weight, const uint8_t *scale, const int32_t *group_sizes, int num_groups,
+                    const int32_t *group_offset, int64_t E_local, int64_t N, void *out, int out_f32, bool gated,
+                    const GmmEpilogue &ep, hipStream_t st);
+int launch_gmm_mx(const uint8_t *lhs, const uint8_t *lhs_scale, const int32_t *row_idx, int64_t lhs_rows, int64_t M,
+                  int64_t K, const uint8_t *weight, const uint8_t *scale, const int32_t *group_sizes, int num_groups,
+                  const int32_t *group_offset, int64_t E_local, int64_t N, void *out, int out_f32, bool gated,
+                  const GmmEpilogue &ep, hipStream_t st);
 
 }  // namespace dwm

@@ -17,7 +17,10 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_HIP = 0, 1, 2, 3
 BF16, F32, U8 = 0, 1, 2
 FP4_E2M1, FP4_CODES = 0, 1
-ACT_NONE, ACT_SILU_MUL_CLAMP = 0, 1
+ACT_NONE, ACT_SILU_MUL_CLAMP, ACT_SILU_MUL, ACT_GELU_TANH_MUL, ACT_SWIGLUOAI = 0, 1, 2, 3, 4
+# gmm_v2 fuse_act names (apply_act_fn) -> enum dwm_act
+FUSE_ACTS = {None: ACT_NONE, "silu_and_mul_with_clamp": ACT_SILU_MUL_CLAMP, "silu": ACT_SILU_MUL,
+             "gelu": ACT_GELU_TANH_MUL, "swigluoai": ACT_SWIGLUOAI}
 SCORE_FNS = {"softmax": 0, "sigmoid": 1, "sqrtsoftplus": 2}
 
 _i64 = ctypes.c_int64
@@ -35,6 +38,7 @@ SIGNATURES = {
     "dwm_gmm_fp4_prepack_gate_up": [_p, _i32, _p, _i32, _i64, _i64, _i64, _p, _p, _p, _p],
     "dwm_gmm_fp4": [_p, _i64, _i64, _p, _p, _p, _i32, _p, _i64, _i64, _p, _i32, _i32, _i32, _p],
     "dwm_gmm_fp4_gather": [_p, _i64, _p, _i64, _i64, _p, _p, _p, _i32, _p, _i64, _i64, _p, _i32, _i32, _i32, _p],
+    "dwm_gmm_fp4_ex": [_p, _i64, _i64, _p, _p, _p, _i32, _p, _i32, _p, _i64, _i64, _p, _i32, _i32, _i32, _p],
     "dwm_mx_quant_e4m3": [_p, _i64, _i64, _p, _p, _p],
     "dwm_gmm_fp4_mx": [_p, _p, _i64, _p, _i64, _i64, _p, _p, _p, _i32, _p, _i64, _i64, _p, _i32, _i32, _i32, _p],
     "dwm_moe_dispatch_workspace_size": [_i64, _i32, _p],
@@ -61,6 +65,12 @@ _RESTYPES = {"dwm_last_error": ctypes.c_char_p}
 
 # enum dwm_dense_kernel
 DENSE_SKINNY, DENSE_MFMA, DENSE_TILED = 1, 2, 3
+
+
+class GmmLhs(ctypes.Structure):
+    """struct dwm_gmm_lhs: the grouped lhs of dwm_gmm_fp4_ex."""
+    _fields_ = [("data", ctypes.c_void_p), ("scale", ctypes.c_void_p), ("rows", ctypes.c_int64),
+                ("row_idx", ctypes.c_void_p)]
 
 
 class DensePlan(ctypes.Structure):

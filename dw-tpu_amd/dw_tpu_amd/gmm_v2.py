@@ -239,11 +239,18 @@ def gmm_v2(lhs: torch.Tensor,
     device tensor (first local group).  Returns [M, N] in
     ``preferred_element_type`` (bf16 default, or float32).  Rows outside the
     local groups are zero when ``zero_initialize`` and unspecified otherwise.
-    ``fuse_act="silu_and_mul_with_clamp"``: rhs is a [w1 | w3] gate/up
-    weight (an ``Fp4Weight`` prepacked with ``gate_up=True``, or raw bytes
-    prepacked so per call) and the result is [M, N/2] =
-    silu(min(gate, 10)) * clip(up, -10, 10) of the f32 accumulators, rounded
-    once.  Tiling / VMEM arguments of the TPU kernel are accepted and ignored.
+    ``fuse_act``: one of apply_act_fn's gated activations
+    (patches/tpu-inference-experimental/fused-moe-fp4/0901-...:57-66) --
+    "silu_and_mul_with_clamp" (silu(min(gate, 10)) * clip(up, -10, 10)),
+    "silu", "gelu" (tanh form, jax.nn.gelu's default) or "swigluoai"
+    (GPT-OSS: g = min(gate, 7), (clip(up, -7, 7) + 1) * g * sigmoid(1.702 g))
+    -- with rhs a [w1 | w3] gate/up weight (an ``Fp4Weight`` prepacked with
+    ``gate_up=True``, or raw bytes prepacked so per call); the result is
+    [M, N/2], the activation of the f32 accumulators rounded once.
+    ``rhs_bias`` ([E, N] or [E, 1, N], f32 or bf16, in the weight's column
+    order) is added to the f32 accumulators of each expert's rows before the
+    activation and the rounding.  Tiling / VMEM arguments of the TPU kernel
+    are accepted and ignored.
 
     ``lhs_row_indices`` (an addition; int32 [M] device tensor): row r of the
     grouped operand is ``lhs[lhs_row_indices[r]]`` (JAX gather index
@@ -257,9 +264,7 @@ def gmm_v2(lhs: torch.Tensor,
     on the scaled MFMA.  ``rhs_quant_dtype`` is accepted and ignored (the rhs
     is fp4 either way).
     """
-    if rhs_bias is not None:
-        raise NotImplementedError("gmm_v2: rhs_bias is not supported by the fp4 kernel")
-    if fuse_act not in (None, "silu_and_mul_with_clamp"):
+    if fuse_act not in _lib.FUSE_ACTS:
         raise NotImplementedError(f"gmm_v2: fused activation {fuse_act!r} is not supported")
     fused = fuse_act is not None
     if transpose_rhs:
@@ -307,7 +312,6 @@ def gmm_v2(lhs: torch.Tensor,
         go = torch.tensor([group_offset], dtype=torch.int32, device=dev)
     else:
         go = group_offset.reshape(-1)[:1].to(device=dev, dtype=torch.int32).contiguous()
-    act = _lib.ACT_SILU_MUL_CLAMP if fused else _lib.ACT_NONE
     idx = lhs_row_indices
     if idx is not None:
         if idx.dtype != torch.int32 or idx.dim() != 1:
@@ -315,15 +319,24 @@ def gmm_v2(lhs: torch.Tensor,
         _lib.require_cuda(idx)
         idx = idx.contiguous()
     m = lhs.shape[0] if idx is None else idx.numel()
+    bias = None
+    if rhs_bias is not None:
+        bias = rhs_bias.reshape(rhs_bias.shape[0], -1) if rhs_bias.dim() == 3 else rhs_bias
+        if tuple(bias.shape) != (w.num_experts, w.n) or (rhs_bias.dim() == 3 and rhs_bias.shape[1] != 1):
+            raise ValueError(f"gmm_v2: rhs_bias must be [E, N] or [E, 1, N] = [{w.num_experts}, {w.n}], "
+                             f"got {tuple(rhs_bias.shape)}")
+        if bias.dtype not in (torch.float32, torch.bfloat16):
+            bias = bias.to(torch.float32)
+        bias = bias.contiguous()
+        _lib.require_cuda(bias)
     out = torch.empty((m, w.n // 2 if fused else w.n), dtype=out_dtype, device=dev)
-    tail = (_lib.ptr(w.weight), _lib.ptr(w.scale), _lib.ptr(gs), gs.numel(), _lib.ptr(go), w.num_experts, w.n,
-            _lib.ptr(out), _lib.dtype_code(out_dtype), 1 if zero_initialize else 0, act, _lib.stream_handle(dev))
     if mx:
-        codes = lhs.codes.contiguous()
-        scales = lhs.scales.contiguous()
-        _lib.call("dwm_gmm_fp4_mx", _lib.ptr(codes), _lib.ptr(scales), codes.shape[0], _lib.ptr(idx), m, w.k, *tail)
-    elif idx is None:
-        _lib.call("dwm_gmm_fp4", _lib.ptr(lhs), m, w.k, *tail)
+        codes, scales = lhs.codes.contiguous(), lhs.scales.contiguous()
+        desc = _lib.GmmLhs(codes.data_ptr(), scales.data_ptr(), codes.shape[0], None if idx is None else idx.data_ptr())
     else:
-        _lib.call("dwm_gmm_fp4_gather", _lib.ptr(lhs), lhs.shape[0], _lib.ptr(idx), m, w.k, *tail)
+        desc = _lib.GmmLhs(lhs.data_ptr(), None, lhs.shape[0], None if idx is None else idx.data_ptr())
+    _lib.call("dwm_gmm_fp4_ex", ctypes.byref(desc), m, w.k, _lib.ptr(w.weight), _lib.ptr(w.scale), _lib.ptr(bias),
+              _lib.dtype_code(bias.dtype) if bias is not None else 0, _lib.ptr(gs), gs.numel(), _lib.ptr(go),
+              w.num_experts, w.n, _lib.ptr(out), _lib.dtype_code(out_dtype), 1 if zero_initialize else 0,
+              _lib.FUSE_ACTS[fuse_act], _lib.stream_handle(dev))
     return out

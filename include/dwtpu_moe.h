@@ -38,13 +38,23 @@ enum dwm_dtype {
   DWM_U8 = 2 /* e8m0 exponent codes for scales */
 };
 
-/* Activation fused into the grouped matmul's epilogue (gmm_v2 fuse_act). */
+/* Activation fused into the grouped matmul's epilogue (gmm_v2 fuse_act):
+ * the activations of apply_act_fn
+ * (patches/tpu-inference-experimental/fused-moe-fp4/0901-...:57-66) on the
+ * f32 accumulators (plus rhs_bias), gate = columns [0, N/2) and up =
+ * [N/2, N) of a [w1 | w3] weight; the output has N/2 columns. */
 enum dwm_act {
   DWM_ACT_NONE = 0,
-  /* silu(min(gate, 10)) * clip(up, -10, 10) on the f32 accumulators, gate =
-   * columns [0, N/2) and up = [N/2, N) of a [w1 | w3] weight
-   * (patches/tpu-inference-experimental/fused-moe-fp4/0901-...:60-64). */
-  DWM_ACT_SILU_MUL_CLAMP = 1
+  /* silu(min(gate, 10)) * clip(up, -10, 10) (0901-...:60-64). */
+  DWM_ACT_SILU_MUL_CLAMP = 1,
+  /* silu(gate) * up ("silu"). */
+  DWM_ACT_SILU_MUL = 2,
+  /* gelu(gate) * up with gelu's tanh form, jax.nn.gelu's default
+   * (0.5 g (1 + tanh(sqrt(2/pi) (g + 0.044715 g^3)))) ("gelu"). */
+  DWM_ACT_GELU_TANH_MUL = 3,
+  /* GPT-OSS swiglu: g = min(gate, 7), u = clip(up, -7, 7),
+   * g * sigmoid(1.702 g) * (u + 1) ("swigluoai"). */
+  DWM_ACT_SWIGLUOAI = 4
 };
 
 /* Router score functions (apply_scoring_fn, called at
@@ -167,6 +177,31 @@ int dwm_gmm_fp4_gather(const uint16_t *lhs, int64_t lhs_rows, const int32_t *row
                        const uint8_t *weight, const uint8_t *scale, const int32_t *group_sizes, int num_groups,
                        const int32_t *group_offset, int64_t E_local, int64_t N, void *out, int out_dtype,
                        int zero_init, int fuse_act, void *stream);
+
+/* The grouped lhs of dwm_gmm_fp4_ex. */
+typedef struct dwm_gmm_lhs {
+  const void *data;        /* bf16 [rows, K]; e4m3 codes [rows, K] when scale != NULL */
+  const uint8_t *scale;    /* NULL, or e8m0 codes [rows, K/32]: the MX mode (dwm_gmm_fp4_mx) */
+  int64_t rows;            /* rows of data */
+  const int32_t *row_idx;  /* NULL (row r is row r of data; rows == M), or int32 [M]: row r is
+                              data[row_idx[r]] (the fused gather, JAX gather semantics) */
+} dwm_gmm_lhs;
+
+/* Every form of the grouped matmul in one entry point: the lhs of
+ * dwm_gmm_fp4 / dwm_gmm_fp4_gather / dwm_gmm_fp4_mx (by `lhs`), plus
+ * rhs_bias: NULL or [E_local, N] of bias_dtype (DWM_F32 or DWM_BF16), in the
+ * weight's source column order ([w1 | w3] for gate/up weights), added in f32
+ * to every accumulator of the expert's rows before the activation and the
+ * output rounding -- gmm_v2's rhs_bias (passed by gmm_wrapper,
+ * patches/tpu-inference/0001-dsv4-v6e-enablement.patch:214-233; the
+ * reference's MXFP4 MoE carries w13_bias / w2_bias,
+ * patches/tpu-inference-ext/0103-...:311-312).  fuse_act: any DWM_ACT_*
+ * (the gated ones need weights from dwm_gmm_fp4_prepack_gate_up).  Other
+ * arguments and limits as dwm_gmm_fp4. */
+int dwm_gmm_fp4_ex(const dwm_gmm_lhs *lhs, int64_t M, int64_t K, const uint8_t *weight, const uint8_t *scale,
+                   const void *rhs_bias, int bias_dtype, const int32_t *group_sizes, int num_groups,
+                   const int32_t *group_offset, int64_t E_local, int64_t N, void *out, int out_dtype, int zero_init,
+                   int fuse_act, void *stream);
 
 /* ---------------------------------------------------------------------- */
 /* MX mode: e4m3 activations with e8m0 block-32 scales (scaled MFMA).      */

@@ -38,12 +38,14 @@ def dequant_rhs(codes: np.ndarray, scale: np.ndarray, block: int = 32) -> np.nda
 
 
 def gmm(lhs, codes, scale, group_sizes, group_offset: int = 0, out_dtype: str = "bfloat16",
-        accumulate: str = "f64", zero_initialize: bool = True, w=None):
+        accumulate: str = "f64", zero_initialize: bool = True, w=None, bias=None):
     """Returns (out [M, N] float32 or float64 values, written-row mask [M]).
 
     lhs: [M, K] float32 holding bf16-exact values.  codes: [E_local, K, N]
     uint4 code values (0..15).  scale: [E_local, K/32, 1, N] f32.
-    ``w`` may pass a precomputed ``dequant_rhs`` result.
+    ``w`` may pass a precomputed ``dequant_rhs`` result.  ``bias``
+    ([E_local, N]) is gmm_v2's rhs_bias: added to each local group's rows
+    (in the accumulation dtype) before the output rounding.
     With out_dtype 'bfloat16' the result is rounded to bf16 (RNE); with
     'float32' to f32; with 'float64' it is returned unrounded.
     accumulate: 'f64' (exact up to float64 rounding), 'f32' (BLAS) or
@@ -78,6 +80,9 @@ def gmm(lhs, codes, scale, group_sizes, group_offset: int = 0, out_dtype: str = 
             y = acc.astype(np.float64)
         else:
             y = (a @ w[g - group_offset].astype(np.float32)).astype(np.float64)
+        if bias is not None:
+            b = np.asarray(bias[g - group_offset], np.float64)
+            y = y + b if accumulate == "f64" else (y.astype(np.float32) + b.astype(np.float32)).astype(np.float64)
         out[r0:r1] = y
         written[r0:r1] = True
     if out_dtype == "bfloat16":
