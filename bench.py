@@ -22,12 +22,14 @@ experts on this host's cores (and one expert on one thread), the same for
 prefill and a dense GEMM, and reports the max abs and relative Frobenius
 error of one expert's GPU output rows against the oracle's float64 product.
 
-The headline is timed last, after the `extra` workloads, so that the GPU
-runs at its sustained clock: the power manager ramps the clock up over the
-first tens of milliseconds of load, and a few warmup launches on an idle GPU
-time part of that ramp (decode_gate_up: 0.179 ms/step after 5 warmup
-launches on an idle GPU, 0.153 ms after 200).  With `--extra none` it runs
-first, on whatever clock the GPU has.
+The headline is timed last, right after the `extra` workloads (its inputs
+are in HBM beforehand), so that the GPU runs at the clock it holds under
+continuous load: after about a second without GPU work the power manager
+lowers the clock and ramps it back up over tens of milliseconds of load, so
+a few warmup launches after a host-side pause time part of that ramp
+(decode_gate_up: 170-185 us/step after an idle second, 142-155 us/step
+right after GPU load).  With `--extra none` it runs after the input upload
+alone.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--extra all|none]
 """
@@ -166,23 +168,43 @@ def bench_gmm(name, dev, steps, warmup, mode="bf16"):
     return wl, b, ms
 
 
-def bench_gmm_mx(name, dev, steps, warmup):
+def prep_gmm(name, dev, steps, warmup):
+    """The bf16 gmm of one workload: inputs now, timing in the returned run()."""
+    from dw_tpu_amd.workloads import make_gmm_workload
+    wl = make_gmm_workload(name)
+    b = GmmBench(wl, dev, copies_for(wl))
+
+    def run():
+        return {name: gmm_result(wl, time_steps(b.step, steps, warmup))}
+    return run
+
+
+def prep_gmm_mx(name, dev, steps, warmup):
     """The MX mode of one gmm workload: the gmm on the quantized lhs, the
     lhs quantization (bf16 [M, K] -> e4m3 + scales), and the two back to back
     (what gmm_v2(lhs_quant_dtype=float8_e4m3fn) runs on a bf16 lhs)."""
-    wl, b, ms = bench_gmm(name, dev, steps, warmup, "mx")
-    r = gmm_result(wl, ms, "mx")
-    q_ms = time_steps(b.quant_step, steps, min(warmup, 20))
-    qb = wl.M * wl.K * 2 + wl.M * wl.K + wl.M * wl.K // 32
-    r["quant"] = {"ms": round(q_ms, 5), "GB_s": round(qb / (q_ms * 1e-3) / 1e9, 1),
-                  "hbm_frac": round(qb / (q_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "bytes": qb}
-    both = time_steps(b.quant_and_step, steps, min(warmup, 20))
-    r["ms_with_quant"] = round(both, 5)
-    r["TFLOP_s_with_quant"] = round(wl.flops() / (both * 1e-3) / 1e12, 1)
-    return r, b
+    from dw_tpu_amd.workloads import make_gmm_workload
+    wl = make_gmm_workload(name)
+    b = GmmBench(wl, dev, copies_for(wl), "mx")
+
+    def run():
+        r = gmm_result(wl, time_steps(b.step, steps, warmup), "mx")
+        q_ms = time_steps(b.quant_step, steps, warmup)
+        qb = wl.M * wl.K * 2 + wl.M * wl.K + wl.M * wl.K // 32
+        r["quant"] = {"ms": round(q_ms, 5), "GB_s": round(qb / (q_ms * 1e-3) / 1e9, 1),
+                      "hbm_frac": round(qb / (q_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "bytes": qb}
+        both = time_steps(b.quant_and_step, steps, warmup)
+        r["ms_with_quant"] = round(both, 5)
+        r["TFLOP_s_with_quant"] = round(wl.flops() / (both * 1e-3) / 1e12, 1)
+        return {f"{name}_mx": r}
+    return run
 
 
-def bench_dispatch_combine(dev, steps, warmup):
+def bench_gmm_mx(name, dev, steps, warmup):
+    return prep_gmm_mx(name, dev, steps, warmup)()[f"{name}_mx"]
+
+
+def prep_dispatch_combine(dev, steps, warmup):
     """decode_down routing through the C ABI with preallocated outputs:
     dispatch indices for 512 tokens x top-8 over 32 experts, the row gather
     of hidden [512, 2048] into [4096, 2048], and the combine of the
@@ -216,40 +238,46 @@ def bench_dispatch_combine(dev, steps, warmup):
     y0 = torch.from_numpy(rng.standard_normal((n, wl.N), dtype=np.float32)).to(torch.bfloat16).to(dev)
     w = torch.from_numpy(wl.topk_weights).to(dev)
 
-    def run(fn, args):
+    def call(fn, args):
         rc = fn(*args)
         if rc:
             raise RuntimeError(lib.dwm_last_error().decode())
 
-    res = {}
-    ms = time_steps(lambda i: run(lib.dwm_moe_dispatch, disp_args), steps, warmup)
-    res["dispatch"] = {"ms": round(ms, 5), "ids": n, "experts": wl.E, "kernels": 1 if n <= 8192 else 3,
-                       "note": "launch-latency bound (one 1024-thread block)"}
-    run(lib.dwm_moe_dispatch, disp_args)
+    call(lib.dwm_moe_dispatch, disp_args)  # the gather and combine read its indices
     set_bytes = (wl.T + n) * wl.K * 2
     gc = -(-2 * MALL_BYTES // set_bytes)
     hiddens = [hidden0.clone() for _ in range(gc)]
     xs = [torch.empty((n, wl.K), dtype=torch.bfloat16, device=dev) for _ in range(gc)]
     gargs = [(P(hiddens[c]), wl.T, wl.K * 2, P(tok), n, P(xs[c]), st) for c in range(gc)]
-    ms = time_steps(lambda i: run(lib.dwm_row_gather, gargs[i % gc]), steps, warmup)
-    gb = wl.T * wl.K * 2 + n * wl.K * 2 + n * 4
-    res["row_gather"] = {"ms": round(ms, 5), "GB_s": round(gb / (ms * 1e-3) / 1e9, 1), "rows": n, "H": wl.K,
-                         "hbm_frac": round(gb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "bytes": gb,
-                         "rotated_sets": gc}
-    del hiddens, xs
     set_bytes = (n + wl.T) * wl.N * 2
     cc = -(-2 * MALL_BYTES // set_bytes)
     ys = [y0.clone() for _ in range(cc)]
     outs = [torch.empty((wl.T, wl.N), dtype=torch.bfloat16, device=dev) for _ in range(cc)]
     cargs = [(P(ys[c]), _lib.BF16, n, wl.N, P(rev), P(w), _lib.F32, wl.T, wl.topk, P(outs[c]), _lib.BF16, st)
              for c in range(cc)]
-    ms = time_steps(lambda i: run(lib.dwm_moe_combine, cargs[i % cc]), steps, warmup)
-    gb = n * wl.N * 2 + wl.T * wl.N * 2 + n * 8
-    res["combine"] = {"ms": round(ms, 5), "GB_s": round(gb / (ms * 1e-3) / 1e9, 1), "T": wl.T, "topk": wl.topk,
-                      "H": wl.N, "hbm_frac": round(gb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "bytes": gb,
-                      "rotated_sets": cc}
-    del ys, outs
-    return res
+
+    # The argument tuples hold raw device addresses: the closure keeps the
+    # tensors behind them alive (freed, their memory would go to later inputs).
+    keep = (ids, perm, tok, rev, gs, goff, flags, ws, hidden0, y0, w, hiddens, xs, ys, outs)
+
+    def run():
+        assert keep
+        res = {}
+        ms = time_steps(lambda i: call(lib.dwm_moe_dispatch, disp_args), steps, warmup)
+        res["dispatch"] = {"ms": round(ms, 5), "ids": n, "experts": wl.E, "kernels": 1 if n <= 8192 else 3,
+                           "note": "launch-latency bound (one 1024-thread block)"}
+        ms = time_steps(lambda i: call(lib.dwm_row_gather, gargs[i % gc]), steps, warmup)
+        gb = wl.T * wl.K * 2 + n * wl.K * 2 + n * 4
+        res["row_gather"] = {"ms": round(ms, 5), "GB_s": round(gb / (ms * 1e-3) / 1e9, 1), "rows": n, "H": wl.K,
+                             "hbm_frac": round(gb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "bytes": gb,
+                             "rotated_sets": gc}
+        ms = time_steps(lambda i: call(lib.dwm_moe_combine, cargs[i % cc]), steps, warmup)
+        gb = n * wl.N * 2 + wl.T * wl.N * 2 + n * 8
+        res["combine"] = {"ms": round(ms, 5), "GB_s": round(gb / (ms * 1e-3) / 1e9, 1), "T": wl.T, "topk": wl.topk,
+                          "H": wl.N, "hbm_frac": round(gb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "bytes": gb,
+                          "rotated_sets": cc}
+        return res
+    return run
 
 
 def _block_weights(dev, E, H, I, copies):
@@ -285,7 +313,7 @@ def _block_result(wl, ms, H, I):
             "nonempty_groups": nonempty}
 
 
-def bench_moe_block(dev, steps, warmup):
+def prep_moe_block(dev, steps, warmup):
     """The expert block through ``moe_block``: dispatch + gmm1 over the routed
     rows of hidden [T, 7168] (gathered inside the gmm) x [7168, 2x2048] with
     the fused silu_and_mul_with_clamp + gmm2 [., 2048] x [2048, 7168] +
@@ -297,8 +325,8 @@ def bench_moe_block(dev, steps, warmup):
     import torch
     from dw_tpu_amd import MoeBlockGraph, moe_block
     from dw_tpu_amd.workloads import make_gmm_workload
-    res = {}
     copies = 2
+    cases = []
     for name, key in (("decode_gate_up", "moe_block_decode"), ("prefill", "moe_block_prefill")):
         wl = make_gmm_workload(name, with_data=False)
         H, I, E = wl.K, wl.N // 2, wl.E
@@ -307,24 +335,28 @@ def bench_moe_block(dev, steps, warmup):
         hidden = torch.from_numpy(rng.standard_normal((wl.T, H), dtype=np.float32)).to(torch.bfloat16).to(dev)
         ids = torch.from_numpy(wl.topk_ids).to(dev)
         wts = torch.from_numpy(wl.topk_weights).to(dev)
-        big = name == "prefill"
-        n_steps, n_warm = (min(steps, 5), min(warmup, 3)) if big else (steps, warmup)
-        ms = time_steps(lambda i: moe_block(hidden, ids, wts, w13s[i % copies], w2s[i % copies], E), n_steps, n_warm)
-        res[key] = _block_result(wl, ms, H, I)
-        if not big:
+        graphs = None
+        if name == "decode_gate_up":
             # the same block captured once per weight copy (MoeBlockGraph) and replayed
             graphs = [MoeBlockGraph(hidden, ids, wts, w13s[c], w2s[c], E) for c in range(copies)]
-            ms_graph = time_steps(lambda i: graphs[i % copies](), steps, warmup)
-            g = _block_result(wl, ms_graph, H, I)
-            res["moe_block_decode_graph"] = {"ms": g["ms"], "GB_s": g["GB_s"], "TFLOP_s": g["TFLOP_s"],
-                                             "note": "the same block replayed from a captured HIP graph"}
-            del graphs
-        del w13s, w2s, hidden
-        torch.cuda.empty_cache()
-    return res
+        cases.append((name, key, wl, H, I, E, w13s, w2s, hidden, ids, wts, graphs))
+
+    def run():
+        res = {}
+        for name, key, wl, H, I, E, w13s, w2s, hidden, ids, wts, graphs in cases:
+            ms = time_steps(lambda i: moe_block(hidden, ids, wts, w13s[i % copies], w2s[i % copies], E), steps,
+                            warmup)
+            res[key] = _block_result(wl, ms, H, I)
+            if graphs is not None:
+                ms_graph = time_steps(lambda i: graphs[i % copies](), steps, warmup)
+                g = _block_result(wl, ms_graph, H, I)
+                res["moe_block_decode_graph"] = {"ms": g["ms"], "GB_s": g["GB_s"], "TFLOP_s": g["TFLOP_s"],
+                                                 "note": "the same block replayed from a captured HIP graph"}
+        return res
+    return run
 
 
-def bench_routing(dev, steps, warmup):
+def prep_routing(dev, steps, warmup):
     """The router (dwm_route_topk) at the decode workload's routing (256
     tokens, 32 experts, top-8 softmax) and at a DeepSeek-V4-like prefill
     (8192 tokens, 256 experts, top-8 sqrtsoftplus + correction bias +
@@ -333,7 +365,7 @@ def bench_routing(dev, steps, warmup):
     from dw_tpu_amd import _lib
     lib = _lib.load()
     st = _lib.stream_handle(dev)
-    res = {}
+    cases = []
     for name, T, E, k, fn, biased in (("route_decode", 256, 32, 8, 0, False),
                                       ("route_prefill_dsv4", 8192, 256, 8, 2, True)):
         g = torch.Generator(device="cpu").manual_seed(T + E)
@@ -344,17 +376,24 @@ def bench_routing(dev, steps, warmup):
         args = (_lib.ptr(logits), _lib.F32, T, E, k, fn, _lib.ptr(bias), None, 1 if biased else 0, None,
                 _lib.ptr(w), _lib.BF16, _lib.ptr(ids), st)
 
-        def run(i, args=args):
-            if lib.dwm_route_topk(*args):
-                raise RuntimeError(lib.dwm_last_error().decode())
-        ms = time_steps(run, steps, warmup)
-        b = T * E * 4 + T * k * 6 + (E * 4 if biased else 0)
-        res[name] = {"ms": round(ms, 5), "GB_s": round(b / (ms * 1e-3) / 1e9, 1), "bytes": b, "T": T, "E": E,
-                     "topk": k}
-    return res
+        cases.append((name, T, E, k, biased, args, (logits, bias, w, ids)))
+
+    def step(args):
+        if lib.dwm_route_topk(*args):
+            raise RuntimeError(lib.dwm_last_error().decode())
+
+    def run():
+        res = {}
+        for name, T, E, k, biased, args, _ in cases:
+            ms = time_steps(lambda i: step(args), steps, warmup)
+            b = T * E * 4 + T * k * 6 + (E * 4 if biased else 0)
+            res[name] = {"ms": round(ms, 5), "GB_s": round(b / (ms * 1e-3) / 1e9, 1), "bytes": b, "T": T, "E": E,
+                         "topk": k}
+        return res
+    return run
 
 
-def bench_formats(dev, steps, warmup):
+def prep_formats(dev, steps, warmup):
     """Checkpoint weight formats (load-time kernels) at the decode shapes:
     an MXFP4 expert checkpoint of the gate/up weight (32 experts, N = 4096,
     K = 7168: [E, N, K/2] codes + [E, N, K/32] scales -> [E, K, N/2] +
@@ -365,7 +404,6 @@ def bench_formats(dev, steps, warmup):
     from dw_tpu_amd import _lib
     lib = _lib.load()
     st = _lib.stream_handle(dev)
-    res = {}
     E, N, K = 32, 4096, 7168
     blocks = torch.randint(0, 256, (E, N, K // 2), dtype=torch.uint8, device=dev)
     scales = torch.randint(110, 135, (E, N, K // 32), dtype=torch.uint8, device=dev)
@@ -377,12 +415,7 @@ def bench_formats(dev, steps, warmup):
     def run_mx(i):
         if lib.dwm_mxfp4_requant(*args):
             raise RuntimeError(lib.dwm_last_error().decode())
-    ms = time_steps(run_mx, steps, min(warmup, 20))
-    b = 2 * (blocks.numel() + scales.numel())
-    res["mxfp4_requant"] = {"ms": round(ms, 5), "GB_s": round(b / (ms * 1e-3) / 1e9, 1),
-                            "hbm_frac": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "bytes": b,
-                            "E": E, "N": N, "K": K}
-    del blocks, scales, codes, scode
+    b_mx = 2 * (blocks.numel() + scales.numel())
     w = torch.randint(0, 0x7E, (N, K), dtype=torch.uint8, device=dev)
     wsc = torch.full((N // 128, K // 128), 2.0 ** -8, dtype=torch.float32, device=dev)
     w_out = torch.empty((K, N), dtype=torch.uint8, device=dev)
@@ -392,15 +425,27 @@ def bench_formats(dev, steps, warmup):
     def run_f8(i):
         if lib.dwm_fp8_block_requant(*args8):
             raise RuntimeError(lib.dwm_last_error().decode())
-    ms = time_steps(run_f8, steps, warmup)
-    b = 2 * w.numel() + 4 * (wsc.numel() + s_out.numel())
-    res["fp8_block_requant"] = {"ms": round(ms, 5), "GB_s": round(b / (ms * 1e-3) / 1e9, 1),
-                                "hbm_frac": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "bytes": b,
-                                "N": N, "K": K}
-    return res
+    b_f8 = 2 * w.numel() + 4 * (wsc.numel() + s_out.numel())
+    # The argument tuples hold raw device addresses: the closure keeps the
+    # tensors behind them alive.
+    keep = (blocks, scales, codes, scode, status, w, wsc, w_out, s_out)
+
+    def run():
+        assert keep
+        res = {}
+        ms = time_steps(run_mx, steps, warmup)
+        res["mxfp4_requant"] = {"ms": round(ms, 5), "GB_s": round(b_mx / (ms * 1e-3) / 1e9, 1),
+                                "hbm_frac": round(b_mx / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "bytes": b_mx,
+                                "E": E, "N": N, "K": K}
+        ms = time_steps(run_f8, steps, warmup)
+        res["fp8_block_requant"] = {"ms": round(ms, 5), "GB_s": round(b_f8 / (ms * 1e-3) / 1e9, 1),
+                                    "hbm_frac": round(b_f8 / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "bytes": b_f8,
+                                    "N": N, "K": K}
+        return res
+    return run
 
 
-def bench_dense(dev, steps, warmup, ms_list=(1, 16, 128, 1024, 4096)):
+def prep_dense(dev, steps, warmup, ms_list=(1, 16, 128, 1024, 4096)):
     """Dense FP8 GEMM (K=7168, N=4096) at each M, W8A16 and W8A8, through
     the C ABI with prepacked weights; 10 rotated weight copies (~290 MB) keep
     the small-M weight stream out of the Infinity Cache."""
@@ -411,13 +456,14 @@ def bench_dense(dev, steps, warmup, ms_list=(1, 16, 128, 1024, 4096)):
     lib = _lib.load()
     st = _lib.stream_handle(dev)
     P = _lib.ptr
-    res = {}
+    cases = []
     for m in ms_list:
         wl = make_dense_workload(m)
         k, n = wl.K, wl.N
         copies = 10 if m <= 128 else 1
         w = torch.from_numpy(wl.wq).to(dev)
         pws = [prepack_fp8(w) for _ in range(copies)]
+        del w
         x = _to_dev_bf16(wl.x_bits, dev)
         xq = torch.from_numpy(wl.xq).to(dev)
         sx = torch.from_numpy(wl.sx).to(dev)
@@ -427,34 +473,37 @@ def bench_dense(dev, steps, warmup, ms_list=(1, 16, 128, 1024, 4096)):
         wsb = ctypes.c_int64()
         _lib.call("dwm_dense_fp8_workspace_size", m, k, n, ctypes.byref(wsb))
         ws = torch.empty(max(1, wsb.value), dtype=torch.uint8, device=dev)
+        cases.append((m, k, n, copies, pws, x, xq, sx, s16, sw, out, ws, wsb.value))
 
-        def run16(i):
-            rc = lib.dwm_dense_fp8_w8a16(P(x), m, k, n, P(pws[i % copies].weight), P(s16), P(out), P(ws),
-                                         wsb.value, st)
-            if rc:
-                raise RuntimeError(lib.dwm_last_error().decode())
+    def run():
+        res = {}
+        for m, k, n, copies, pws, x, xq, sx, s16, sw, out, ws, wsb in cases:
+            def run16(i):
+                rc = lib.dwm_dense_fp8_w8a16(P(x), m, k, n, P(pws[i % copies].weight), P(s16), P(out), P(ws), wsb,
+                                             st)
+                if rc:
+                    raise RuntimeError(lib.dwm_last_error().decode())
 
-        def run8(i):
-            rc = lib.dwm_dense_fp8_w8a8(P(xq), P(sx), m, k, n, P(pws[i % copies].weight), P(sw), P(out), P(ws),
-                                        wsb.value, st)
-            if rc:
-                raise RuntimeError(lib.dwm_last_error().decode())
+            def run8(i):
+                rc = lib.dwm_dense_fp8_w8a8(P(xq), P(sx), m, k, n, P(pws[i % copies].weight), P(sw), P(out), P(ws),
+                                            wsb, st)
+                if rc:
+                    raise RuntimeError(lib.dwm_last_error().decode())
 
-        fl = 2 * m * k * n
-        for tag, fn, xbytes in (("w8a16", run16, m * k * 2 + (k // 128) * n * 4),
-                                ("w8a8", run8, m * k + m * (k // 128) * 4 + (k // 128) * (n // 128) * 4)):
-            ms = time_steps(fn, steps, warmup)
-            bts = k * n + xbytes + m * n * 2
-            gbs = bts / (ms * 1e-3) / 1e9
-            tf = fl / (ms * 1e-3) / 1e12
-            peak_key, peak = ("mfma_fp8_frac", FP8_PEAK_TFLOPS) if tag == "w8a8" else ("mfma_bf16_frac",
-                                                                                    BF16_PEAK_TFLOPS)
-            res[f"dense_{tag}_M{m}"] = {"ms": round(ms, 5), "GB_s": round(gbs, 1), "TFLOP_s": round(tf, 2),
-                                        "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), peak_key: round(tf / peak, 4),
-                                        "bytes": bts, "flops": fl}
-        del pws, w
-        torch.cuda.empty_cache()
-    return res
+            fl = 2 * m * k * n
+            for tag, fn, xbytes in (("w8a16", run16, m * k * 2 + (k // 128) * n * 4),
+                                    ("w8a8", run8, m * k + m * (k // 128) * 4 + (k // 128) * (n // 128) * 4)):
+                ms = time_steps(fn, steps, warmup)
+                bts = k * n + xbytes + m * n * 2
+                gbs = bts / (ms * 1e-3) / 1e9
+                tf = fl / (ms * 1e-3) / 1e12
+                peak_key, peak = ("mfma_fp8_frac", FP8_PEAK_TFLOPS) if tag == "w8a8" else ("mfma_bf16_frac",
+                                                                                        BF16_PEAK_TFLOPS)
+                res[f"dense_{tag}_M{m}"] = {"ms": round(ms, 5), "GB_s": round(gbs, 1), "TFLOP_s": round(tf, 2),
+                                            "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), peak_key: round(tf / peak, 4),
+                                            "bytes": bts, "flops": fl}
+        return res
+    return run
 
 
 def profiled_traffic(name="gmm_fp4_decode_gate_up.md"):
@@ -620,40 +669,38 @@ def main():
             r = gmm_result(wl1, ms1)
         print(json.dumps({"only": args.only, "result": r}), flush=True)
         return
+    # The headline's inputs go to HBM first, so that its timed steps can
+    # follow the other workloads with no host-side gap: after about a second
+    # without GPU work the power manager lowers the clock, and a few warmup
+    # launches (under 1 ms of work) run on the way back up.  Measured on this
+    # workload: 170-185 us/step after an idle second, 142-155 us/step right
+    # after GPU load.
+    log("bench: decode_gate_up inputs")
+    from dw_tpu_amd.workloads import make_gmm_workload
+    wl = make_gmm_workload("decode_gate_up")
+    b = GmmBench(wl, dev, copies_for(wl))
     extra = {}
     if args.extra == "all":
-        # The other workloads run first: by the time the headline is timed the
-        # GPU has been under load for seconds and runs at its sustained clock
-        # (the power manager ramps the clock over the first tens of
-        # milliseconds of load, which a 5-step warmup on an idle GPU would
-        # time instead).  Each measurement does its own W warmup steps.
-        for name in ("decode_down", "prefill"):
-            log(f"bench: {name} gmm")
-            wl2, b2, ms2 = bench_gmm(name, dev, args.steps, args.warmup)
-            extra[name] = gmm_result(wl2, ms2)
-            del b2
-            torch.cuda.empty_cache()
+        # Inputs of every workload first, then every timed region back to
+        # back (the GPU never waits on host-side input generation between
+        # them), the headline last.
+        runs = []
+        for label, prep in (("dispatch / gather / combine", prep_dispatch_combine), ("moe block", prep_moe_block),
+                            ("dense fp8", prep_dense), ("router", prep_routing), ("checkpoint formats", prep_formats)):
+            log(f"bench: inputs of {label}")
+            runs.append(prep(dev, args.steps, args.warmup))
         for name in ("decode_gate_up", "decode_down", "prefill"):
-            log(f"bench: {name} gmm, MX mode")
-            r, bmx = bench_gmm_mx(name, dev, args.steps, args.warmup)
-            extra[f"{name}_mx"] = r
-            del bmx
-            torch.cuda.empty_cache()
-        log("bench: dispatch / gather / combine")
-        extra.update(bench_dispatch_combine(dev, args.steps, args.warmup))
-        log("bench: moe block (decode)")
-        extra.update(bench_moe_block(dev, args.steps, args.warmup))
-        torch.cuda.empty_cache()
-        log("bench: dense fp8")
-        extra.update(bench_dense(dev, args.steps, args.warmup))
-        torch.cuda.empty_cache()
-        log("bench: router")
-        extra.update(bench_routing(dev, args.steps, args.warmup))
-        log("bench: checkpoint formats")
-        extra.update(bench_formats(dev, args.steps, args.warmup))
-        torch.cuda.empty_cache()
+            log(f"bench: inputs of {name} gmm, MX mode")
+            runs.append(prep_gmm_mx(name, dev, args.steps, args.warmup))
+        for name in ("decode_down", "prefill"):
+            log(f"bench: inputs of {name} gmm")
+            runs.append(prep_gmm(name, dev, args.steps, args.warmup))
+        log("bench: timed regions")
+        for run in runs:
+            extra.update(run())
+        del runs
     log("bench: decode_gate_up gmm (headline)")
-    wl, b, ms = bench_gmm("decode_gate_up", dev, args.steps, args.warmup)
+    ms = time_steps(b.step, args.steps, args.warmup)
     main_res = gmm_result(wl, ms)
     # Spread: 7 more samples of the same K steps, right after the timed ones.
     samples = sorted(time_steps(b.step, args.steps, 0) for _ in range(7))

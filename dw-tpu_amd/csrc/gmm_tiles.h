@@ -117,9 +117,12 @@ __device__ __forceinline__ bool find_tile(const int32_t *__restrict__ group_size
   if (cls < 0 || ref.g < 0) return false;
   ref.nt = (int)(entry % n_tiles);
   ref.row0 = s_info[1];
-  if (ref.row0 >= M) return false;
+  // group_sizes lives on the device and is not checked by the host: sizes
+  // whose sum leaves int32 would give row starts outside [0, M).  Such tiles
+  // are skipped, so no tile reads or writes a row outside [0, M).
+  if (ref.row0 < 0 || ref.row0 >= M) return false;
   ref.rows = (int)min((int64_t)s_info[2], M - ref.row0);
-  return true;
+  return ref.rows > 0;
 }
 
 // The fused activation of one (gate, up) accumulator pair, in f32 (the
