@@ -663,7 +663,7 @@ def main():
     if args.only:
         name = args.only[:-3] if args.only.endswith("_mx") else args.only
         if args.only.endswith("_mx"):
-            r, _ = bench_gmm_mx(name, dev, args.steps, args.warmup)
+            r = bench_gmm_mx(name, dev, args.steps, args.warmup)
         else:
             wl1, _, ms1 = bench_gmm(name, dev, args.steps, args.warmup)
             r = gmm_result(wl1, ms1)

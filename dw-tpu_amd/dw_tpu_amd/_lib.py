@@ -11,7 +11,9 @@ import threading
 import torch
 
 LIB_NAME = "libdwtpu_moe.so"
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+# DWTPU_MOE_LIB names another build of the same library (the host-sanitizer
+# build that the argument-check tests load); by default the in-tree one.
+LIB_PATH = os.environ.get("DWTPU_MOE_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
 # enum dwm_status / dwm_dtype / dwm_fp4_format / dwm_act / dwm_score
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_HIP = 0, 1, 2, 3

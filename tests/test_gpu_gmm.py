@@ -293,3 +293,37 @@ def test_gmm_full_size_row_permutation_and_group_independence(dev, rng):
     o = torch.from_numpy(np.flatnonzero(other)).to(dev)
     assert torch.equal(y2[o].view(torch.int16), y[o].view(torch.int16))
     assert not torch.equal(y2[starts[g]:starts[g + 1]].view(torch.int16), y[starts[g]:starts[g + 1]].view(torch.int16))
+
+
+@pytest.mark.parametrize("mx", [False, True])
+@pytest.mark.parametrize("name", ["decode_gate_up", "prefill"])
+def test_gmm_acceptance_policy_full_size(dev, rng, name, mx):
+    """The reference's kernel-acceptance rule
+    (results/dsv4-dense-gemm-kernel-1/NOTES.md:26-27) at the real K = 7168:
+    f32 output on sampled rows (first, last and a random row of every
+    non-empty expert) and columns, against float64, with the sequential f32
+    accumulation over all 7168 products as the current kernel.  In the MX
+    mode both sides take the e4m3-quantized lhs (the rule judges the
+    accumulation, the quantization is the mode's own stated error)."""
+    from dw_tpu_amd import fp4_weight_to_codes, gmm_v2
+    from dw_tpu_amd.workloads import make_gmm_workload
+    from oracle import quant
+    wl = make_gmm_workload(name)
+    pw = fp4_weight_to_codes(torch.from_numpy(wl.rhs_e2m1).to(dev), torch.from_numpy(wl.scale_codes).to(dev))
+    out = gmm_v2(bf16_tensor(wl.lhs_bits, dev), pw, torch.from_numpy(wl.group_sizes).to(dev),
+                 preferred_element_type=torch.float32, lhs_quant_dtype=torch.float8_e4m3fn if mx else None)
+    rows = _sample_rows(wl.group_sizes, rng)
+    cols = np.unique(np.r_[0, wl.N - 1, rng.integers(0, wl.N, 46)])
+    starts = np.concatenate([[0], np.cumsum(wl.group_sizes)])
+    grp = np.searchsorted(starts, rows, side="right") - 1
+    sub_gs = np.bincount(grp, minlength=wl.E).astype(np.int32)
+    w = gmm.dequant_rhs(fp4.e2m1_to_codes(_nibbles_at(wl.rhs_e2m1, cols)), fp4.e8m0_decode(wl.scale_codes[..., cols]))
+    lhs = bf16_to_f32(wl.lhs_bits[rows])
+    if mx:
+        lhs = quant.mx_dequantize(*quant.mx_quantize_e4m3(lhs)).astype(np.float32)
+    y64, _ = gmm.gmm(lhs, None, None, sub_gs, out_dtype="float64", w=w)
+    ys, _ = gmm.gmm(lhs, None, None, sub_gs, out_dtype="float32", accumulate="seq32", w=w)
+    y = out[torch.from_numpy(rows).to(dev)][:, torch.from_numpy(cols).to(dev)].cpu().numpy()
+    ok, st = gmm.acceptance_policy(y, ys, y64)
+    print(name, "mx" if mx else "bf16", st, flush=True)
+    assert ok, st
