@@ -97,7 +97,6 @@ __global__ __launch_bounds__(256) void mx_quant_e4m3_kernel(const uint16_t *__re
       w0 = f32x4_e4m3(q);
       w1 = f32x4_e4m3(q + 4);
     }
-    typedef __attribute__((ext_vector_type(2))) uint32_t u32x2_t;
     *(u32x2_t *)(codes + 8 * i) = u32x2_t{w0, w1};
     if ((i & 3) == 0) scales[i >> 2] = (uint8_t)(bad ? 255 : e + 127);
   }
