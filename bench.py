@@ -49,7 +49,8 @@ METRIC = "FP4 MoE gmm TFLOP/s + HBM GB/s (% of peak) at decode & prefill sizes"
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 FP8_PEAK_TFLOPS = 5000.0
-ONLY_CHOICES = ("decode_gate_up", "decode_down", "prefill", "decode_gate_up_mx", "decode_down_mx", "prefill_mx")
+ONLY_CHOICES = ("decode_gate_up", "decode_down", "prefill", "decode_gate_up_mx", "decode_down_mx", "prefill_mx",
+                "dense_M1", "dense_M16", "dense_M128", "dense_M1024", "dense_M4096")
 MALL_BYTES = 256 * 2 ** 20
 
 
@@ -639,8 +640,9 @@ def main():
     ap.add_argument("--calib-copy", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy (byte-counter calibration)")
     ap.add_argument("--only", choices=ONLY_CHOICES, default=None,
-                    help="profiling aid: time one gmm workload line (name, or name_mx for the MX mode) and print "
-                         "it as {\"only\": name, ...}; not the benchmark line")
+                    help="profiling aid: time one gmm workload line (name, or name_mx for the MX mode) or the "
+                         "dense FP8 GEMM at one M (W8A16 then W8A8) and print it as {\"only\": name, ...}; not the "
+                         "benchmark line")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -662,7 +664,9 @@ def main():
         return
     if args.only:
         name = args.only[:-3] if args.only.endswith("_mx") else args.only
-        if args.only.endswith("_mx"):
+        if args.only.startswith("dense_M"):
+            r = prep_dense(dev, args.steps, args.warmup, ms_list=(int(args.only[len("dense_M"):]),))()
+        elif args.only.endswith("_mx"):
             r = bench_gmm_mx(name, dev, args.steps, args.warmup)
         else:
             wl1, _, ms1 = bench_gmm(name, dev, args.steps, args.warmup)

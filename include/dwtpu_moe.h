@@ -152,11 +152,13 @@ int dwm_gmm_fp4_prepack_gate_up(const uint8_t *rhs, int format, const void *scal
  *   group_offset: device int32[1] or NULL (= 0).
  *   out_dtype:    DWM_BF16 or DWM_F32 (the MOE_F32_REDUCE variant,
  *                 patches/tpu-inference-ext/0106-...:243-250).
- *   fuse_act:     DWM_ACT_NONE, or DWM_ACT_SILU_MUL_CLAMP with weights from
+ *   fuse_act:     DWM_ACT_NONE, or a gated DWM_ACT_* with weights from
  *                 dwm_gmm_fp4_prepack_gate_up: out is then [M, N/2], the
  *                 activation of the f32 accumulators rounded once (gmm_v2's
  *                 fuse_act as gmm1 of moe_gmm_local uses it,
- *                 patches/tpu-inference-ext/0103-...:77-78).
+ *                 patches/tpu-inference-ext/0103-...:77-78; the
+ *                 activations of apply_act_fn, patches/tpu-inference-
+ *                 experimental/fused-moe-fp4/0901-...:57-66).
  * Requires K % 128 == 0, N % 16 == 0 (N % 64 == 0 with fuse_act),
  * num_groups <= 1024. */
 int dwm_gmm_fp4(const uint16_t *lhs, int64_t M, int64_t K, const uint8_t *weight,
