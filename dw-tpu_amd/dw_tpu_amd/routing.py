@@ -4,34 +4,56 @@
   (_fused_moe_fp4_routing,
   patches/tpu-inference-experimental/fused-moe-fp4/0901-...:656-687): score
   function (softmax, sigmoid or DeepSeek V4's sqrtsoftplus), hash routing or
-  top-k on score + e_score_correction_bias (weights stay the unbiased scores)
-  or plain top-k, optional renormalization, invalid tokens to expert 0 with
-  weight 0, cast to ``dtype``.
+  lax.approx_max_k on the scores (MOE_APPROX_TOPK: no bias), top-k on score
+  + e_score_correction_bias (weights stay the unbiased scores) or plain
+  top-k, optional renormalization, invalid tokens to expert 0 with weight 0,
+  cast to ``dtype``.
 * ``dedupe_topk`` (0901-...:98-121): makes each token's expert ids distinct
   for precomputed routing.
 
 Both are one kernel each (dwm_route_topk / dwm_dedupe_topk).
 """
+import os
+
 import torch
 
 from . import _lib
 
 
+def _env_flag(name):
+    return os.environ.get(name, "").strip().lower() in ("1", "true", "yes", "on")
+
+
 def fused_moe_fp4_routing(gating_output: torch.Tensor, top_k: int, renormalize: bool, scoring_fn: str,
-                          dtype: torch.dtype, extra: dict = None):
+                          dtype: torch.dtype, extra: dict = None, approx_topk: bool = None,
+                          recall_target: float = None):
     """gating_output [T, E] (bf16 or f32) -> (topk_weights [T, top_k] of
     ``dtype``, topk_ids [T, top_k] int32).
 
     ``extra`` may hold ``hash_based_topk_indices`` (int [T, top_k]),
     ``e_score_correction_bias`` ([E]) and ``num_valid_tokens`` (int or a
     one-element device tensor); they are popped from it, as the reference
-    does.  lax.approx_max_k (MOE_APPROX_TOPK) is not provided: the exact
-    top-k is always used.
+    does.
+
+    ``approx_topk`` (default: the MOE_APPROX_TOPK environment variable, off
+    when unset) takes the reference's lax.approx_max_k branch
+    (0901-...:671-675): it comes after hash routing and before the
+    correction bias, so a bias in ``extra`` is popped but not applied.  The
+    exact top-k of the scores is returned; it meets every ``recall_target``
+    (default MOE_APPROX_TOPK_RECALL_TARGET, else 0.95; accepted in (0, 1]).
     """
     extra = {} if extra is None else extra
     hash_ids = extra.pop("hash_based_topk_indices", None)
     bias = extra.pop("e_score_correction_bias", None)
     num_valid = extra.pop("num_valid_tokens", None)
+    if approx_topk is None:
+        approx_topk = _env_flag("MOE_APPROX_TOPK")
+    if recall_target is None:
+        recall_target = float(os.environ.get("MOE_APPROX_TOPK_RECALL_TARGET", "0.95"))
+    if not 0.0 < recall_target <= 1.0:
+        raise ValueError(f"recall_target must be in (0, 1], got {recall_target}")
+    if approx_topk and hash_ids is None:
+        bias = None  # the approx_max_k branch ranks the unbiased scores
     _lib.require_cuda(gating_output)
     if gating_output.dim() != 2:
         raise ValueError(f"gating_output must be [T, E], got {tuple(gating_output.shape)}")

@@ -71,6 +71,33 @@ def test_route_topk_ties_go_to_the_lower_expert(dev):
     _check(dev, logits, 4, "softmax")  # 7, 40, then 0, 1 among the equal rest
 
 
+@pytest.mark.parametrize("score", ["softmax", "sqrtsoftplus"])
+def test_route_topk_approx_branch(dev, rng, score):
+    """MOE_APPROX_TOPK (0901-...:671-675): after hash routing, before the
+    bias, so a correction bias is popped but not applied; the exact top-k of
+    the unbiased scores (a valid approx_max_k result for any recall target).
+    Hash routing still takes precedence."""
+    from dw_tpu_amd import fused_moe_fp4_routing
+    E, k, T = 256, 8, 300
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    bias = (rng.standard_normal(E) * 0.5).astype(np.float32)
+    lt = torch.from_numpy(logits).to(dev)
+    bt = torch.from_numpy(bias).to(dev)
+    extra = {"e_score_correction_bias": bt}
+    w, ids = fused_moe_fp4_routing(lt, k, True, score, torch.float32, extra, approx_topk=True, recall_target=0.9)
+    assert not extra
+    w0, ids0 = fused_moe_fp4_routing(lt, k, True, score, torch.float32, {})
+    assert torch.equal(ids, ids0) and torch.equal(w, w0)
+    ww, wid = moe.route_topk(logits, k, renormalize=True, scoring_fn=score)
+    assert np.array_equal(ids.cpu().numpy(), wid)
+    wb, idb = fused_moe_fp4_routing(lt, k, True, score, torch.float32, {"e_score_correction_bias": bt})
+    assert not torch.equal(idb, ids)  # the bias does change the exact branch's choice here
+    hid = torch.from_numpy(rng.integers(0, E, (T, k)).astype(np.int32)).to(dev)
+    wh, idh = fused_moe_fp4_routing(lt, k, True, score, torch.float32, {"hash_based_topk_indices": hid},
+                                    approx_topk=True)
+    assert torch.equal(idh, hid)
+
+
 @pytest.mark.parametrize("k,E", [(8, 256), (8, 12), (6, 6), (3, 2), (64, 300)])
 def test_dedupe_topk_bit_exact(dev, rng, k, E):
     from dw_tpu_amd import dedupe_topk
