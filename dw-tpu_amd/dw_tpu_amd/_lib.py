@@ -10,6 +10,8 @@ import threading
 
 import torch
 
+from . import _trace
+
 LIB_NAME = "libdwtpu_moe.so"
 # DWTPU_MOE_LIB names another build of the same library (the host-sanitizer
 # build that the argument-check tests load); by default the in-tree one.
@@ -117,9 +119,14 @@ def load():
 
 
 def call(name, *args):
-    """Calls an entry point and maps its status to an exception."""
+    """Calls an entry point and maps its status to an exception (inside a
+    roctx range named by the entry point when ranges are on)."""
     lib = load()
-    rc = getattr(lib, name)(*args)
+    if _trace.enabled():
+        with _trace.op_range(name):
+            rc = getattr(lib, name)(*args)
+    else:
+        rc = getattr(lib, name)(*args)
     if rc == OK:
         return
     msg = lib.dwm_last_error().decode(errors="replace")

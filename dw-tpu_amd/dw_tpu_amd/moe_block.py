@@ -17,6 +17,7 @@ from dataclasses import dataclass
 
 import torch
 
+from . import _trace
 from .gmm_v2 import Fp4Weight, gmm_v2
 from .moe_fast_combine import fast_combine
 from .moe_fast_dispatch import moe_dispatch, row_gather
@@ -32,6 +33,7 @@ class MoeBlockOutputs:
     y: torch.Tensor         # [T * topk, H] gmm2 output (bf16 or f32)
 
 
+@_trace.traced("moe_block")
 def moe_block(hidden: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.Tensor, w13: Fp4Weight,
               w2: Fp4Weight, num_experts: int, group_offset=None, f32_reduce: bool = False,
               return_intermediates: bool = False):
@@ -97,6 +99,7 @@ class MoeBlockGraph:
         with torch.cuda.graph(self.graph):
             self.out = moe_block(self.hidden, self.topk_ids, self.topk_weights, *args, **kw)
 
+    @_trace.traced("moe_block_graph")
     def __call__(self, hidden: torch.Tensor = None, topk_ids: torch.Tensor = None,
                  topk_weights: torch.Tensor = None) -> torch.Tensor:
         """Copies the given inputs (same shapes and dtypes as at construction)
