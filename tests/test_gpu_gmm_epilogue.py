@@ -115,3 +115,42 @@ def test_bias_with_fused_gather(dev, rng, mx):
         want = _run(dev, x_bits, rhs, sc, gs, bias, act, mx)
         got = _run(dev, hidden_bits, rhs, sc, gs, bias, act, mx, idx=idx)
         assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
+@pytest.mark.parametrize("mx", [False, True])
+@pytest.mark.parametrize("act", [None, "gelu"])
+def test_bias_with_group_offset_window(dev, rng, mx, act):
+    """An expert-parallel window (group_offset, E_local < num_groups): the
+    bias row of local expert g - group_offset is added to group g's rows only,
+    and rows outside the window are zero (zero_initialize)."""
+    from dw_tpu_amd import fp4_weight_to_codes, gmm_v2
+    K, N = 256, 128
+    sizes = [20, 33, 0, 41, 7, 50]
+    go, e_local = 2, 3
+    lhs_bits = to_bf16_bits(rng.standard_normal((sum(sizes), K)).astype(np.float32))
+    rhs = rng.integers(0, 256, (e_local, K, N // 2), dtype=np.uint8)
+    sc = rng.integers(122, 128, (e_local, K // 32, 1, N), dtype=np.uint8)
+    bias = (rng.standard_normal((e_local, N)) * 4).astype(np.float32)
+    gs = np.array(sizes, np.int32)
+    pw = fp4_weight_to_codes(torch.from_numpy(rhs).to(dev), torch.from_numpy(sc).to(dev), gate_up=act is not None)
+    out = gmm_v2(bf16_tensor(lhs_bits, dev), pw, torch.from_numpy(gs).to(dev),
+                 rhs_bias=torch.from_numpy(bias).to(dev), group_offset=go, fuse_act=act,
+                 preferred_element_type=torch.float32, lhs_quant_dtype=torch.float8_e4m3fn if mx else None)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().astype(np.float64)
+    a = bf16_to_f32(lhs_bits)
+    if mx:
+        a = quant.mx_dequantize(*quant.mx_quantize_e4m3(a))
+    w = _w(rhs, sc)
+    y64, written = gmm.gmm(a, None, None, gs, group_offset=go, out_dtype="float64", w=w, bias=bias)
+    ap = gmm.abs_product(a, w, gs, group_offset=go)
+    acc_err = K * 2.0 ** -24 * ap + 2.0 ** -24 * np.abs(y64)
+    if mx:
+        acc_err += gmm.MX_BLOCK_TERM * gmm.block_max_product(a, w, gs, group_offset=go)
+    if act is None:
+        want, bound = y64, 2.0 ** -24 * np.abs(y64) + acc_err
+    else:
+        want, bound = omb.apply_act(y64, act), omb.act_bound(y64, acc_err, act)
+    assert np.all(got[~written] == 0)
+    err = np.abs(got[written] - want[written])
+    assert np.all(err <= bound[written]), float((err / bound[written]).max())
