@@ -348,6 +348,15 @@ def prep_moe_block(dev, steps, warmup):
             ms = time_steps(lambda i: moe_block(hidden, ids, wts, w13s[i % copies], w2s[i % copies], E), steps,
                             warmup)
             res[key] = _block_result(wl, ms, H, I)
+            # The same block in the MX mode (e4m3 activations with e8m0
+            # block-32 scales into both gmm: a lossier computation).
+            ms_mx = time_steps(lambda i: moe_block(hidden, ids, wts, w13s[i % copies], w2s[i % copies], E,
+                                                   lhs_quant_dtype=torch.float8_e4m3fn), steps, warmup)
+            mx = _block_result(wl, ms_mx, H, I)
+            res[key + "_mx"] = {"ms": mx["ms"], "TFLOP_s": mx["TFLOP_s"],
+                                "mfma_fp8_frac": round(mx["TFLOP_s"] / FP8_PEAK_TFLOPS, 4),
+                                "note": "the same block with lhs_quant_dtype=float8_e4m3fn (hidden and the "
+                                        "activation quantized in the step)"}
             if graphs is not None:
                 ms_graph = time_steps(lambda i: graphs[i % copies](), steps, warmup)
                 g = _block_result(wl, ms_graph, H, I)

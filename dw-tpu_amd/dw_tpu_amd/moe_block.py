@@ -12,13 +12,18 @@ activation of the accumulators is rounded once to bf16 (fused-moe-fp4
 0901-...:420-423); gmm2 accumulates in f32 and rounds once (0901-...:446-449)
 or stays f32 (``f32_reduce``, 0106-...:243-250); the combine sums in f32 in
 top-k order and rounds once (moe_fast_combine.py:44-54).
+
+With ``lhs_quant_dtype=torch.float8_e4m3fn`` both gmm run in the MX mode
+(gmm_v2.py): ``hidden`` is quantized once, [T, H] before the gather (the
+blocks run along each row, so gmm1 reads exactly the quantized rows of the
+gathered copy), and gmm2 quantizes the activation.
 """
 from dataclasses import dataclass
 
 import torch
 
 from . import _trace
-from .gmm_v2 import Fp4Weight, gmm_v2
+from .gmm_v2 import Fp4Weight, gmm_v2, mx_quantize
 from .moe_fast_combine import fast_combine
 from .moe_fast_dispatch import moe_dispatch, row_gather
 
@@ -36,11 +41,13 @@ class MoeBlockOutputs:
 @_trace.traced("moe_block")
 def moe_block(hidden: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.Tensor, w13: Fp4Weight,
               w2: Fp4Weight, num_experts: int, group_offset=None, f32_reduce: bool = False,
-              return_intermediates: bool = False):
+              return_intermediates: bool = False, lhs_quant_dtype=None):
     """hidden [T, H] bf16; topk_ids [T, topk] int32; topk_weights [T, topk]
     f32 or bf16; w13: gate/up weights [E, H, 2I] prepacked with
     ``gate_up=True``; w2: down weights [E, I, H].  Returns [T, H] bf16 (or
-    ``MoeBlockOutputs`` with ``return_intermediates``)."""
+    ``MoeBlockOutputs`` with ``return_intermediates``).  ``lhs_quant_dtype``:
+    None (the reference's bf16 activations) or torch.float8_e4m3fn (the MX
+    mode for both gmm)."""
     if not w13.gate_up:
         raise ValueError("moe_block: w13 must be prepacked with gate_up=True")
     if w13.k != hidden.shape[1] or w2.k != w13.n // 2 or w2.n != hidden.shape[1]:
@@ -49,13 +56,15 @@ def moe_block(hidden: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.
     d = moe_dispatch(topk_ids, num_experts)
     # gmm1 reads hidden[token_indices_sorted] itself (the row gather fused
     # into its loads), the same rows the separate gather would write.
-    h = gmm_v2(hidden, w13, d.group_sizes, group_offset=group_offset, zero_initialize=False,
-               fuse_act="silu_and_mul_with_clamp", lhs_row_indices=d.token_indices_sorted)
+    src = hidden if lhs_quant_dtype is None else mx_quantize(hidden)
+    h = gmm_v2(src, w13, d.group_sizes, group_offset=group_offset, zero_initialize=False,
+               fuse_act="silu_and_mul_with_clamp", lhs_row_indices=d.token_indices_sorted,
+               lhs_quant_dtype=lhs_quant_dtype)
     # With a group_offset (an expert-parallel shard) rows of other shards'
     # experts are zeroed before the combine, as the reference does
     # (patches/tpu-inference-ext/0103-...:94-97: 0 * NaN would poison it).
     y = gmm_v2(h, w2, d.group_sizes, group_offset=group_offset, zero_initialize=group_offset is not None,
-               preferred_element_type=torch.float32 if f32_reduce else None)
+               preferred_element_type=torch.float32 if f32_reduce else None, lhs_quant_dtype=lhs_quant_dtype)
     out = fast_combine(y, d.topk_argsort_revert_indices, topk_weights, topk, out_dtype=hidden.dtype)
     if return_intermediates:
         return MoeBlockOutputs(out, d, row_gather(hidden, d.token_indices_sorted), h, y)
@@ -77,7 +86,8 @@ class MoeBlockGraph:
     """
 
     def __init__(self, hidden: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.Tensor, w13: Fp4Weight,
-                 w2: Fp4Weight, num_experts: int, group_offset=None, f32_reduce: bool = False):
+                 w2: Fp4Weight, num_experts: int, group_offset=None, f32_reduce: bool = False,
+                 lhs_quant_dtype=None):
         self.hidden = hidden.clone()
         self.topk_ids = topk_ids.to(torch.int32).clone()
         self.topk_weights = topk_weights.clone()
@@ -87,7 +97,7 @@ class MoeBlockGraph:
             # an int would become a host-to-device copy inside the capture
             group_offset = torch.tensor([int(group_offset)], dtype=torch.int32, device=hidden.device)
         args = (w13, w2, num_experts)
-        kw = dict(group_offset=group_offset, f32_reduce=f32_reduce)
+        kw = dict(group_offset=group_offset, f32_reduce=f32_reduce, lhs_quant_dtype=lhs_quant_dtype)
         self._keep = (w13, w2, group_offset)
         # One eager run on a side stream first (as torch's capture recipe asks).
         side = torch.cuda.Stream(device=hidden.device)
