@@ -697,17 +697,26 @@ def main():
         # Inputs of every workload first, then every timed region back to
         # back (the GPU never waits on host-side input generation between
         # them), the headline last.
+        # Compute-heavy regions first (they pull the clock down to their own
+        # power-limited level), then memory-bound ones, the decode lines
+        # last: the headline starts from decode-type load, not from the
+        # recovery after a prefill.
         runs = []
-        for label, prep in (("dispatch / gather / combine", prep_dispatch_combine), ("moe block", prep_moe_block),
-                            ("dense fp8", prep_dense), ("router", prep_routing), ("checkpoint formats", prep_formats)):
-            log(f"bench: inputs of {label}")
-            runs.append(prep(dev, args.steps, args.warmup))
-        for name in ("decode_gate_up", "decode_down", "prefill"):
+        for name in ("prefill",):
             log(f"bench: inputs of {name} gmm, MX mode")
             runs.append(prep_gmm_mx(name, dev, args.steps, args.warmup))
-        for name in ("decode_down", "prefill"):
             log(f"bench: inputs of {name} gmm")
             runs.append(prep_gmm(name, dev, args.steps, args.warmup))
+        for label, prep in (("moe block", prep_moe_block), ("dense fp8", prep_dense),
+                            ("checkpoint formats", prep_formats), ("router", prep_routing),
+                            ("dispatch / gather / combine", prep_dispatch_combine)):
+            log(f"bench: inputs of {label}")
+            runs.append(prep(dev, args.steps, args.warmup))
+        for name in ("decode_down", "decode_gate_up"):
+            log(f"bench: inputs of {name} gmm, MX mode")
+            runs.append(prep_gmm_mx(name, dev, args.steps, args.warmup))
+        log("bench: inputs of decode_down gmm")
+        runs.append(prep_gmm("decode_down", dev, args.steps, args.warmup))
         log("bench: timed regions")
         for run in runs:
             extra.update(run())
