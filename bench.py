@@ -656,7 +656,7 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures one GPU only: the MoE hot path is built and measured on one MI355X's share of "
-              "the experts; runs on more than one GPU are not part of this build.", file=sys.stderr)
+              "the experts; runs on more than one GPU are not measured here.", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np

@@ -79,7 +79,7 @@ def matmul(x, w, s, *, tn=None, tk=None, tm=None, mode="native", stages=0):
     With tm, tk and tn left unset the library launches its own plan.  Given,
     they name a launch (``dense_fp8_tiles``: mode "native" = the skinny or
     MFMA kernel, "megablox" = the general tiled kernel; tk = the K depth per
-    block; ``stages`` = ring depth) and a tile this build has no kernel for
+    block; ``stages`` = ring depth) and a tile the library has no kernel for
     raises ValueError.  The reference's "pre" mode (weights scaled in bf16
     before the dot) is a different rounding and is not provided."""
     if mode not in ("native", "megablox"):

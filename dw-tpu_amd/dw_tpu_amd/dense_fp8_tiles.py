@@ -118,7 +118,7 @@ def parse_table(data):
     if data.get("version") != FORMAT_VERSION or type(data.get("version")) is not int:
         raise ValueError(f"dense tile file: version must be {FORMAT_VERSION}")
     if data.get("device") != DEVICE:
-        raise ValueError(f"dense tile file: written for {data.get('device')!r}, this build runs on {DEVICE!r}")
+        raise ValueError(f"dense tile file: written for {data.get('device')!r}, this library runs on {DEVICE!r}")
     rows = data.get("entries")
     if not isinstance(rows, list):
         raise ValueError("dense tile file: 'entries' must be a list")

@@ -18,7 +18,7 @@ def fp4_weight_to_codes(weight: torch.Tensor, weight_scale: torch.Tensor,
                         rhs_fp4_codes: bool = False, gate_up: bool = False) -> Fp4Weight:
     """Stored fp4 expert weight [E, K, N/2] (+ block scales) -> ``Fp4Weight``.
 
-    The reference re-encodes e2m1 to uint4 codes here (exact); this build
+    The reference re-encodes e2m1 to uint4 codes here (exact); this package
     also relayouts into the kernel's K-major tiles (exact, same bytes).
     ``gate_up``: a [w1 | w3] weight that gmm1 runs with the fused activation.
     """
