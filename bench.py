@@ -516,6 +516,58 @@ def prep_dense(dev, steps, warmup, ms_list=(1, 16, 128, 1024, 4096)):
     return run
 
 
+def probe_equal_experts(dev, kind):
+    """Profiling aid (``--probe``): the grouped matmul on synthetic equal
+    experts (K = 7168, N = 4096, random prepacked weights, two copies
+    rotated), bf16 and MX modes, 5 rounds of 30 steps, median us per launch.
+
+    kind "rows": 28 experts with 16 .. 96 rows each (the MFMA row blocks a
+    decode tile carries); kind "cus": 28 experts x 73 rows at K = 7168 (224
+    tiles, like decode_gate_up), 32 x 73 rows at K = 6272 (256 tiles holding
+    the same total work: every CU busy) and 32 x 73 at K = 7168."""
+    import statistics
+    import torch
+    from dw_tpu_amd import _lib, fp4_weight_to_codes, mx_quantize
+    lib = _lib.load()
+    P = ctypes.c_void_p
+    st = _lib.stream_handle(dev)
+    N = 4096
+    shapes = ([(28, r, 7168) for r in (16, 32, 48, 64, 73, 80, 96)] if kind == "rows"
+              else [(28, 73, 7168), (32, 73, 6272), (32, 73, 7168)])
+    weights = {}
+    cases = []
+    for E, rows, K in shapes:
+        if (E, K) not in weights:
+            ws = []
+            for _ in range(2):
+                r = torch.randint(0, 256, (E, K, N // 2), dtype=torch.uint8, device=dev)
+                s = torch.randint(122, 128, (E, K // 32, 1, N), dtype=torch.uint8, device=dev)
+                ws.append(fp4_weight_to_codes(r, s))
+                del r, s
+            weights[(E, K)] = ws
+        ws = weights[(E, K)]
+        M = E * rows
+        x = torch.randn(M, K, device=dev).to(torch.bfloat16)
+        q = mx_quantize(x)
+        gs = torch.full((E,), rows, dtype=torch.int32, device=dev)
+        out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+        for mx in (False, True):
+            def step(i, ws=ws, x=x, q=q, gs=gs, out=out, E=E, K=K, M=M, mx=mx):
+                w = ws[i % 2]
+                tail = (P(w.weight.data_ptr()), P(w.scale.data_ptr()), P(gs.data_ptr()), E, None, E, N,
+                        P(out.data_ptr()), _lib.BF16, 0, 0, st)
+                rc = (lib.dwm_gmm_fp4_mx(P(q.codes.data_ptr()), P(q.scales.data_ptr()), M, None, M, K, *tail) if mx
+                      else lib.dwm_gmm_fp4(P(x.data_ptr()), M, K, *tail))
+                if rc:
+                    raise RuntimeError(lib.dwm_last_error().decode())
+            cases.append((f"E{E}_rows{rows}_K{K}_{'mx' if mx else 'bf16'}", step, (x, q, gs, out)))
+    res = {}
+    for _ in range(5):
+        for name, step, _keep in cases:
+            res.setdefault(name, []).append(time_steps(step, 30, 10))
+    return {name: round(1e3 * statistics.median(v), 2) for name, v in res.items()}
+
+
 def profiled_traffic(name="gmm_fp4_decode_gate_up.md"):
     """HBM bytes per launch of the main kernel from the committed rocprofv3
     counter summary (FETCH_SIZE + WRITE_SIZE, copy-calibrated), or None."""
@@ -646,6 +698,9 @@ def main():
     ap.add_argument("--extra", choices=["all", "none"], default="all")
     ap.add_argument("--cpu-budget", type=float, default=15.0,
                     help="seconds of CPU-baseline work (0 skips it)")
+    ap.add_argument("--probe", choices=("rows", "cus"), default=None,
+                    help="profiling aid: the grouped matmul on synthetic equal experts (rows per expert, or all "
+                         "CUs busy); prints {\"probe\": kind, \"us\": {...}}; not the benchmark line")
     ap.add_argument("--calib-copy", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy (byte-counter calibration)")
     ap.add_argument("--only", choices=ONLY_CHOICES, default=None,
@@ -662,6 +717,9 @@ def main():
     import numpy as np
     import torch
     dev = torch.device("cuda:0")
+    if args.probe:
+        print(json.dumps({"probe": args.probe, "us": probe_equal_experts(dev, args.probe)}), flush=True)
+        return
     if args.calib_copy:
         src = torch.empty(2 ** 30, dtype=torch.uint8, device=dev).fill_(1)
         dst = torch.empty_like(src)
