@@ -339,3 +339,40 @@ def test_gmm_acceptance_policy_full_size(dev, rng, name, mx):
                                wl.K, "float32")
     err = np.abs(y.astype(np.float64) - y64)
     assert np.all(err <= bound), float((err / bound).max())
+
+
+@pytest.mark.parametrize("mx", [False, True])
+@pytest.mark.parametrize("num_groups,go,e_local", [(256, 96, 32), (1024, 1016, 8), (130, 0, 130)])
+def test_gmm_many_groups_window(dev, rng, mx, num_groups, go, e_local):
+    """Many global groups (DeepSeek's 256 experts, the 1024 maximum, and 130
+    local ones): the device tile list's group scans run over several 64-group
+    chunks.  Sizes are ragged with empty groups; the window's rows match the
+    oracle (bf16 bound, or the MX bound) and every other row is zero."""
+    from dw_tpu_amd import fp4_weight_to_codes, gmm_v2
+    from oracle import quant
+    K, N = 128, 64
+    sizes = rng.integers(0, 6, num_groups).astype(np.int32)
+    sizes[rng.random(num_groups) < 0.3] = 0
+    sizes[go] = 97  # a multi-tile local group
+    M = int(sizes.sum())
+    lhs_bits = bf16_bits_np(rng.standard_normal((M, K)).astype(np.float32))
+    rhs = rng.integers(0, 256, (e_local, K, N // 2), dtype=np.uint8)
+    sc = rng.integers(123, 130, (e_local, K // 32, 1, N), dtype=np.uint8)
+    pw = fp4_weight_to_codes(torch.from_numpy(rhs).to(dev), torch.from_numpy(sc).to(dev))
+    out = gmm_v2(bf16_tensor(lhs_bits, dev), pw, torch.from_numpy(sizes).to(dev), group_offset=go,
+                 preferred_element_type=torch.float32, lhs_quant_dtype=torch.float8_e4m3fn if mx else None)
+    torch.cuda.synchronize()
+    a = bf16_to_f32(lhs_bits)
+    if mx:
+        a = quant.mx_dequantize(*quant.mx_quantize_e4m3(a)).astype(np.float32)
+    w = gmm.dequant_rhs(fp4.e2m1_to_codes(_nibbles_at(rhs, np.arange(N))), fp4.e8m0_decode(sc))
+    y64, written = gmm.gmm(a, None, None, sizes, group_offset=go, out_dtype="float64", w=w)
+    ap = gmm.abs_product(a, w, sizes, group_offset=go)
+    if mx:
+        bound = gmm.mx_error_bound(y64, ap, gmm.block_max_product(a, w, sizes, group_offset=go), K, "float32")
+    else:
+        bound = gmm.error_bound(y64, ap, K, "float32")
+    y = out.cpu().numpy().astype(np.float64)
+    assert written.sum() == sizes[go:go + e_local].sum()
+    assert np.all(y[~written] == 0)
+    assert np.all(np.abs(y - y64)[written] <= bound[written])
