@@ -6,21 +6,26 @@
 // (512-column tile).  Tiles are enumerated on the device from group_sizes (no
 // host sync): the tile total is (row tiles of every local group) x (column
 // tiles); empty groups own no tile and cost no weight traffic.  Tiles are
-// listed by cost class (32-row MFMA blocks holding rows, largest first) so
+// listed by cost class (16-row MFMA blocks holding rows, largest first) so
 // the dispatcher, which hands blocks to free CUs in index order, balances
 // multi-round launches.  Blocks whose index is equal mod 8 run on one XCD
 // (the dispatcher's round robin); each class is cut into one contiguous run
 // per XCD -- consecutive column tiles of the same row tile -- so the group's
-// lhs rows are shared in that XCD's L2.
+// lhs rows are shared in that XCD's L2.  When the tiles leave CUs idle (a
+// one-round decode launch), the costliest classes run as 256-column tiles.
 //
 // The block is warp-specialised (see the WsCfg comment): producer waves move
 // the lhs tile and the prepacked weights and scales (fp4.hip) from memory to
 // a ring of LDS stages with direct global -> LDS loads; consumer waves decode
 // the weights in registers with the gfx950 fp4 -> bf16 converter (which
-// applies the e8m0 scale exactly) and run bf16 MFMA 32x32x16 for every 32-row
+// applies the e8m0 scale exactly) and run bf16 MFMA 16x16x32 for every 16-row
 // block that holds rows.  The dequantised weights are exact (e2m1 x power of
 // two fits bf16), so the products equal the reference's
-// bf16(decode(q)) * bf16(scale) operands; only the f32 summation order differs.
+// bf16(decode(q)) * bf16(scale) operands; only the f32 summation order differs,
+// and it is the same for every row.
+#include <algorithm>
+#include <atomic>
+
 #include "gmm_tiles.h"
 
 namespace dwm {
@@ -33,9 +38,10 @@ __device__ __forceinline__ int lhs_swizzle(int r) { return (r >> 1) & 7; }
 // ---------------------------------------------------------------------------
 // Warp-specialised tiles.
 //
-// A block of 12 waves owns (group, 32*MB rows) x 512 columns.  Waves 0..7
-// (consumers, two per SIMD) each own 64 columns: they read the lhs tile and
-// their weight codes and scales from LDS, decode, and run the 32x32x16 MFMAs.
+// A block of 12 waves owns (group, 32*MB rows) x 512 columns (256 in a narrow
+// tile, whose last four consumers idle).  Waves 0..7 (consumers, two per
+// SIMD) each own 64 columns: they read the lhs tile and their weight codes
+// and scales from LDS, decode, and run the MFMAs.
 // Waves 8..11 (producers, one per SIMD) only move data: global -> LDS loads
 // (global_load_lds) of the lhs tile, weights and scales through a ring of LDS
 // stages.  One workgroup barrier per 64-deep K step publishes two steps
@@ -52,8 +58,9 @@ __device__ __forceinline__ int lhs_swizzle(int r) { return (r >> 1) & 7; }
 // 64 g + 32 j + c at k = 64 t + 32 h .. + 31, two per byte, low nibble first.
 // Scale layout: for (e, g, 128-deep step kb) 256 bytes; byte 2 f + j of lane
 // l = c + 32 h is the e8m0 code of column 64 g + 32 j + c, K-block
-// 4 kb + 2 f + h.  MFMA step s of K step t takes lane (c, h)'s codes
-// k = 64 t + 32 h + 8 s .. + 7 and the lhs chunk with the same k.
+// 4 kb + 2 f + h.  Decoded, lane (c, h)'s codes k = 64 t + 32 h + 8 s .. + 7
+// are the B operand of a 32x32x16 MFMA step s; the consumer turns pairs of
+// such steps into 16x16x32 operands (ws_consumer).
 // Block shape: CW consumer waves owning JW 32-column blocks each (a tile of
 // 32 JW CW columns = GT 64-column groups), NP producer waves, NS LDS stages.
 template <int MB, int CW, int JW, int NP, int NS>
@@ -77,15 +84,16 @@ struct WsCfg {
 };
 
 // Producer wave pw: NA of its A_LOADS lhs row groups hold rows of the tile;
-// the others are zero in every stage and never loaded.
-template <class C, int NA>
+// the others are zero in every stage and never loaded.  It loads GL of the
+// tile's 64-column weight groups (G_LOADS in a wide tile, half in a narrow one).
+template <class C, int NA, int GL>
 __device__ __forceinline__ void ws_producer(const uint16_t *__restrict__ lhs, const int32_t *__restrict__ row_idx,
                                             int64_t lhs_rows, int64_t row0, int rows, int K, int T,
                                             int KB, const uint8_t *__restrict__ wexp,
                                             const uint8_t *__restrict__ sexp, int g0, int G, uint8_t *s_lds,
                                             int pw) {
   constexpr int NP = C::NPROD, NS = C::STAGES;
-  constexpr int LOADS = NA + 3 * C::G_LOADS;
+  constexpr int LOADS = NA + 3 * GL;
   constexpr int PENDING = LOADS * (NS - 1 - C::AHEAD);
   static_assert(PENDING < 64, "vmcnt range");
   const int lane = threadIdx.x & 63;
@@ -109,10 +117,10 @@ __device__ __forceinline__ void ws_producer(const uint16_t *__restrict__ lhs, co
     const int64_t src = row_idx ? gather_index(row_idx[row0 + rs], lhs_rows) : rs;
     aoff[i] = (uint32_t)(src * K * 2) + ((((lane & 7) ^ lhs_swizzle(r))) << 4);
   }
-  const uint8_t *wsrc[C::G_LOADS];
-  const uint8_t *ssrc[C::G_LOADS];
+  const uint8_t *wsrc[GL];
+  const uint8_t *ssrc[GL];
 #pragma unroll
-  for (int c = 0; c < C::G_LOADS; ++c) {
+  for (int c = 0; c < GL; ++c) {
     const int g = min(g0 + pw + NP * c, G - 1);  // groups past N feed unstored columns
     wsrc[c] = wexp + (int64_t)g * T * 2048 + lane * 16;
     ssrc[c] = sexp + (int64_t)g * KB * 256 + lane * 4;
@@ -125,7 +133,7 @@ __device__ __forceinline__ void ws_producer(const uint16_t *__restrict__ lhs, co
       __builtin_amdgcn_global_load_lds((const void *)(a + aoff[i]),
                                        (lds_void_t *)(st + C::A + (pw + NP * i) * 1024), 16, 0, 0);
 #pragma unroll
-    for (int c = 0; c < C::G_LOADS; ++c) {
+    for (int c = 0; c < GL; ++c) {
       const int gi = pw + NP * c;
       const uint8_t *const w = wsrc[c] + (int64_t)t * 2048;
       __builtin_amdgcn_global_load_lds((const void *)w, (lds_void_t *)(st + C::W + gi * 2048), 16, 0, 0);
@@ -156,35 +164,51 @@ __device__ __forceinline__ void ws_producer(const uint16_t *__restrict__ lhs, co
   __builtin_amdgcn_s_barrier();
 }
 
-template <class C, int AM, bool ACT>
+// A consumer wave runs its 64 columns for NH 16-row blocks of the tile with
+// 16x16x32 MFMAs: every row of every tile sums K in the same grouping, so a
+// row's result depends on its own lhs row only (not on its place in the
+// tile), and MFMA work follows the rows in steps of 16.  The weights are
+// decoded in the 32x32x16 lane layout the prepack writes (lane (c, h) holds
+// column 32 j + c at k = 32 h + 8 s .. + 7 of the K step, s = 0 .. 3);
+// v_permlane16_swap of the decoded steps 2v and 2v + 1 turns them into the
+// 16x16x32 B operands of column blocks 2j (first result) and 2j + 1
+// (second): lane row q = lane / 16 then holds K chunk (h = q / 2, s = 2v +
+// q % 2) of column 16 u + lane % 16, and the lhs fragment of MFMA step v
+// reads the same K chunk.  Each K step runs 2 x NH x 4 MFMAs in groups of at
+// most 3 row blocks; a group's lhs fragments are read during the previous
+// group.
+template <class C, int NH, bool ACT>
 __device__ __forceinline__ void ws_consumer(int T, uint8_t *s_lds, int cw, int64_t row0, int rows,
                                             int64_t col0, int N, void *__restrict__ out, int out_f32,
                                             const void *bias, const GmmEpilogue &ep) {
-  constexpr int JW = C::JWAVE, NS = C::STAGES;
-  const int lane = threadIdx.x & 63, c32 = lane & 31, h = lane >> 5;
-  f32x16_t acc[AM][JW];
+  constexpr int NS = C::STAGES;
+  constexpr int RG = NH > 3 ? 2 : 1;      // row groups of at most three 16-row blocks
+  constexpr int H0 = NH > 3 ? 3 : NH;     // blocks of row group 0 (row group 1: NH - H0)
+  static_assert(C::JWAVE == 2 && NH >= 1 && NH <= 6, "64 columns and 16 .. 96 rows per consumer");
+  const int lane = threadIdx.x & 63, q = lane >> 4;
+  f32x4_t acc[NH][4];
 #pragma unroll
-  for (int mb = 0; mb < AM; ++mb)
+  for (int hb = 0; hb < NH; ++hb)
 #pragma unroll
-    for (int j = 0; j < JW; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[mb][j][r] = 0.0f;
-  const int arow = C::A + c32 * 128;
-  const int x = lhs_swizzle(c32);  // rows mb * 32 + c32 share it
+    for (int u = 0; u < 4; ++u) acc[hb][u] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  const int arow = C::A + (lane & 15) * 128;  // row 16 hb + lane % 16: + 2048 hb
+  const int x = lhs_swizzle(lane & 15);       // every row 16 hb + lane % 16 shares it
+  const int qk = 4 * (q >> 1) + (q & 1);      // K chunk of MFMA step v: qk + 2 v
   const int woff = C::W + cw * 2048 + lane * 16;
   const int soff = C::S + cw * 256 + lane * 4;
   // Next step's weights and scales, and the lhs fragments of the next MFMA group.
-  u32x4_t wn[JW], an[AM];
+  u32x4_t wn[2], an[3];
   uint32_t sn;
   auto read_w = [&](const uint8_t *st) {
     wn[0] = *(const u32x4_t *)(st + woff);
     wn[1] = *(const u32x4_t *)(st + woff + 1024);
     sn = *(const uint32_t *)(st + soff);
   };
-  auto read_a = [&](const uint8_t *st, int s) {
-    const int ach = (((4 * h + s) ^ x) << 4);
+  auto read_a = [&](const uint8_t *st, int v, int rg) {
+    const int ach = ((qk + 2 * v) ^ x) << 4;
+    const int nb = rg ? NH - H0 : H0;
 #pragma unroll
-    for (int mb = 0; mb < AM; ++mb) an[mb] = *(const u32x4_t *)(st + arow + mb * 32 * 128 + ach);
+    for (int i = 0; i < nb; ++i) an[i] = *(const u32x4_t *)(st + arow + (3 * rg + i) * 2048 + ach);
   };
   int cur = 0;  // stage of step t
   for (int t = 0; t < T; ++t) {
@@ -200,10 +224,10 @@ __device__ __forceinline__ void ws_consumer(int T, uint8_t *s_lds, int cw, int64
     const uint8_t *const sx = s_lds + nxt * C::STAGE;
     if (t == 0) {
       read_w(st);
-      read_a(st, 0);
+      read_a(st, 0, 0);
     }
-    u32x4_t w[JW];
-    float sc[JW];
+    u32x4_t w[2];
+    float sc[2];
     w[0] = wn[0];
     w[1] = wn[1];
     {
@@ -212,29 +236,48 @@ __device__ __forceinline__ void ws_consumer(int T, uint8_t *s_lds, int cw, int64
       sc[1] = e8m0_to_f32((sd >> 8) & 0xFFu);
     }
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      u32x4_t a[AM];
+    for (int v = 0; v < 2; ++v) {
+      u32x4_t bop[4];  // B operands of column blocks u = 0 .. 3
 #pragma unroll
-      for (int mb = 0; mb < AM; ++mb) a[mb] = an[mb];
-      __builtin_amdgcn_sched_barrier(0);
-      if (s < 3) read_a(st, s + 1);
-      else read_a(sx, 0);
-      if (s == 0) read_w(sx);
-      u32x4_t b[JW];
+      for (int rg = 0; rg < RG; ++rg) {
+        const int nb = rg ? NH - H0 : H0;
+        u32x4_t a[3];
 #pragma unroll
-      for (int j = 0; j < JW; ++j) {
-        b[j][0] = cvt_fp4x2_bf16<0>(w[j][s], sc[j]);
-        b[j][1] = cvt_fp4x2_bf16<1>(w[j][s], sc[j]);
-        b[j][2] = cvt_fp4x2_bf16<2>(w[j][s], sc[j]);
-        b[j][3] = cvt_fp4x2_bf16<3>(w[j][s], sc[j]);
+        for (int i = 0; i < nb; ++i) a[i] = an[i];
+        __builtin_amdgcn_sched_barrier(0);
+        if (rg + 1 < RG) read_a(st, v, rg + 1);
+        else if (v == 0) read_a(st, 1, 0);
+        else read_a(sx, 0, 0);
+        if (rg == 0) {
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            u32x4_t e, o;
+            e[0] = cvt_fp4x2_bf16<0>(w[j][2 * v], sc[j]);
+            e[1] = cvt_fp4x2_bf16<1>(w[j][2 * v], sc[j]);
+            e[2] = cvt_fp4x2_bf16<2>(w[j][2 * v], sc[j]);
+            e[3] = cvt_fp4x2_bf16<3>(w[j][2 * v], sc[j]);
+            o[0] = cvt_fp4x2_bf16<0>(w[j][2 * v + 1], sc[j]);
+            o[1] = cvt_fp4x2_bf16<1>(w[j][2 * v + 1], sc[j]);
+            o[2] = cvt_fp4x2_bf16<2>(w[j][2 * v + 1], sc[j]);
+            o[3] = cvt_fp4x2_bf16<3>(w[j][2 * v + 1], sc[j]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const auto p = __builtin_amdgcn_permlane16_swap(e[i], o[i], false, false);
+              bop[2 * j][i] = p[0];
+              bop[2 * j + 1][i] = p[1];
+            }
+          }
+          // the next step's weights, once steps 0 and 1's words are decoded
+          if (v == 0) read_w(sx);
+        }
+#pragma unroll
+        for (int i = 0; i < nb; ++i)
+#pragma unroll
+          for (int u = 0; u < 4; ++u)
+            acc[3 * rg + i][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                __builtin_bit_cast(bf16x8_t, a[i]), __builtin_bit_cast(bf16x8_t, bop[u]), acc[3 * rg + i][u], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
       }
-#pragma unroll
-      for (int mb = 0; mb < AM; ++mb)
-#pragma unroll
-        for (int j = 0; j < JW; ++j)
-          acc[mb][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a[mb]),
-                                                               __builtin_bit_cast(bf16x8_t, b[j]), acc[mb][j], 0, 0, 0);
-      __builtin_amdgcn_sched_barrier(0);
     }
     cur = nxt;
   }
@@ -245,20 +288,46 @@ __device__ __forceinline__ void ws_consumer(int T, uint8_t *s_lds, int cw, int64
   __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
-  store_tile<AM, ACT, C::EP_STRIDE>(acc, (float *)(s_lds + cw * 32 * C::EP_STRIDE * 4), row0, rows, col0, N, out,
-                                     out_f32, bias, ep.bias_bf16, ep.act);
+  store_halves<NH, ACT, C::EP_STRIDE>(acc, (float *)(s_lds + cw * 32 * C::EP_STRIDE * 4), row0, rows, col0, N, out,
+                                      out_f32, bias, ep.bias_bf16, ep.act);
 }
 
-template <class C, int MB, bool ACT>
+// A consumer wave with no columns in a narrow tile: it only keeps the
+// barrier count (T + 1) of the others.
+__device__ __forceinline__ void ws_idle_consumer(int T) {
+  for (int t = 0; t <= T; ++t) {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  }
+}
+
+// Producer dispatch on the number of lhs row groups that hold rows.
+template <class C, int GL>
+__device__ __forceinline__ void ws_produce(int na, const uint16_t *lhs, const int32_t *row_idx, int64_t lhs_rows,
+                                           int64_t row0, int rows, int K, int T, int KB, const uint8_t *wexp,
+                                           const uint8_t *sexp, int g0, int G, uint8_t *s_lds, int pw) {
+  constexpr int AL = C::A_LOADS;
+  if (na >= AL) ws_producer<C, AL, GL>(lhs, row_idx, lhs_rows, row0, rows, K, T, KB, wexp, sexp, g0, G, s_lds, pw);
+  else if (na == 2) ws_producer<C, (AL > 2 ? 2 : AL), GL>(lhs, row_idx, lhs_rows, row0, rows, K, T, KB, wexp, sexp, g0, G, s_lds, pw);
+  else if (na == 1) ws_producer<C, (AL > 1 ? 1 : AL), GL>(lhs, row_idx, lhs_rows, row0, rows, K, T, KB, wexp, sexp, g0, G, s_lds, pw);
+  else ws_producer<C, 0, GL>(lhs, row_idx, lhs_rows, row0, rows, K, T, KB, wexp, sexp, g0, G, s_lds, pw);
+}
+
+// NARROW: the tile list may cut its costliest classes into 256-column tiles
+// (find_tile) when the 512-column tiles leave some of the ncu CUs idle.
+template <class C, int MB, bool ACT, bool NARROW>
 __global__ __launch_bounds__(C::THREADS) void gmm_fp4_ws_kernel(
     const uint16_t *__restrict__ lhs, const int32_t *__restrict__ row_idx, int64_t lhs_rows, int64_t M, int K,
     const uint8_t *__restrict__ wpk,
     const uint8_t *__restrict__ spk, const int32_t *__restrict__ group_sizes, int num_groups,
     const int32_t *__restrict__ group_offset, int64_t e_local, int N, void *__restrict__ out,
-    int out_f32, GmmEpilogue ep) {
-  constexpr int NT = C::NT;
+    int out_f32, GmmEpilogue ep, int ncu) {
   constexpr int CW = C::CONS;
-  static_assert(C::STAGES * C::STAGE >= (kMaxGroups + MB * kClsStride) * 4, "tile classes alias the stages");
+  constexpr int NC = 2 * MB;  // tile classes: 16-row blocks holding rows
+  static_assert(MB == 3, "consumer variants are written for 96-row tiles");
+  static_assert(C::STAGES * C::STAGE >= (kMaxGroups + NC * kClsStride) * 4, "tile classes alias the stages");
+  static_assert(C::GT % (2 * C::NPROD) == 0, "a narrow tile's groups split evenly over the producers");
   __shared__ __attribute__((aligned(1024))) uint8_t s_lds[C::STAGES * C::STAGE];
   __shared__ int s_info[3];
   int *s_rowstart = (int *)s_lds;
@@ -266,38 +335,48 @@ __global__ __launch_bounds__(C::THREADS) void gmm_fp4_ws_kernel(
 
   const int tid = threadIdx.x, wave = tid >> 6;
   const int go = group_offset ? group_offset[0] : 0;
+  const int G = (N + 63) >> 6;
+  const int n_tiles = (G + C::GT - 1) / C::GT;
+  const int n_tiles_n = NARROW ? (G + C::GT / 2 - 1) / (C::GT / 2) : 0;
   TileRef ref;
-  if (!find_tile<MB, C::THREADS>(group_sizes, num_groups, go, e_local, M, (N + NT - 1) / NT, s_rowstart, s_cls,
-                                 s_info, ref))
+  if (!find_tile<MB, 16, C::THREADS>(group_sizes, num_groups, go, e_local, M, n_tiles, n_tiles_n, ncu, s_rowstart,
+                                     s_cls, s_info, ref))
     return;
   const int g = ref.g, nt = ref.nt, rows = ref.rows;
+  const bool narrow = NARROW && ref.narrow;
   const int64_t row0 = ref.row0;
   const int64_t e = g - go;
-  const int T = K >> 6, KB = K >> 7, G = (N + 63) >> 6;
-  const int g0 = nt * C::GT;  // first 64-column group of the tile
+  const int T = K >> 6, KB = K >> 7;
+  const int g0 = nt * (narrow ? C::GT / 2 : C::GT);  // first 64-column group of the tile
   if (wave >= CW) {
     const int pw = wave - CW;
     const uint8_t *const wexp = wpk + e * G * T * 2048;
     const uint8_t *const sexp = spk + e * G * KB * 256;
     // Row groups pw + NP i with 8 (pw + NP i) < rows are loaded.
     const int na = min(C::A_LOADS, (rows + 8 * C::NPROD - 1 - 8 * pw) / (8 * C::NPROD));
-    if (na >= C::A_LOADS) ws_producer<C, C::A_LOADS>(lhs, row_idx, lhs_rows, row0, rows, K, T, KB, wexp, sexp, g0, G, s_lds, pw);
-    else if (na == 2) ws_producer<C, (C::A_LOADS > 2 ? 2 : C::A_LOADS)>(lhs, row_idx, lhs_rows, row0, rows, K, T, KB, wexp, sexp, g0, G, s_lds, pw);
-    else if (na == 1) ws_producer<C, (C::A_LOADS > 1 ? 1 : C::A_LOADS)>(lhs, row_idx, lhs_rows, row0, rows, K, T, KB, wexp, sexp, g0, G, s_lds, pw);
-    else ws_producer<C, 0>(lhs, row_idx, lhs_rows, row0, rows, K, T, KB, wexp, sexp, g0, G, s_lds, pw);
+    if (NARROW && narrow)
+      ws_produce<C, C::G_LOADS / 2>(na, lhs, row_idx, lhs_rows, row0, rows, K, T, KB, wexp, sexp, g0, G, s_lds, pw);
+    else
+      ws_produce<C, C::G_LOADS>(na, lhs, row_idx, lhs_rows, row0, rows, K, T, KB, wexp, sexp, g0, G, s_lds, pw);
     return;
   }
-  const int act_mb = (rows + 31) >> 5;
-  const int64_t col0 = (int64_t)(g0 + wave) * 64;
   // Every consumer runs exactly T + 1 barriers (the producers' count),
   // whatever its row-block count.
+  if (narrow && wave >= C::GT / 2) {
+    ws_idle_consumer(T);
+    return;
+  }
+  const int nh = (rows + 15) >> 4;  // 16-row blocks holding rows
+  const int64_t col0 = (int64_t)(g0 + wave) * 64;
   const void *const bias = expert_bias(ep, e, N);
-  if (act_mb <= 1 || MB == 1) ws_consumer<C, 1, ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32, bias, ep);
-  else if (act_mb == 2 || MB == 2)
-    ws_consumer<C, (MB >= 2 ? 2 : 1), ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32, bias, ep);
-  else if (act_mb == 3 || MB == 3)
-    ws_consumer<C, (MB >= 3 ? 3 : 1), ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32, bias, ep);
-  else ws_consumer<C, MB, ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32, bias, ep);
+  switch (nh) {
+    case 1: ws_consumer<C, 1, ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32, bias, ep); break;
+    case 2: ws_consumer<C, 2, ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32, bias, ep); break;
+    case 3: ws_consumer<C, 3, ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32, bias, ep); break;
+    case 4: ws_consumer<C, 4, ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32, bias, ep); break;
+    case 5: ws_consumer<C, 5, ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32, bias, ep); break;
+    default: ws_consumer<C, 6, ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32, bias, ep); break;
+  }
 }
 
 // zero_initialize: zero rows outside [start(go), start(go + E_local)).
@@ -340,22 +419,43 @@ int launch_gmm_zero_rows(const int32_t *group_sizes, int num_groups, const int32
   return launch_status("gmm zero rows");
 }
 
-template <int MB, int CW, int JW, int NP, int NS, bool ACT = false>
+// Compute units of the current device (looked up once per device).  It only
+// sizes the narrow split; any positive value gives correct results.
+static int device_cu_count() {
+  constexpr int kMaxDev = 64;
+  static std::atomic<int> cache[kMaxDev];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) {
+    (void)hipGetLastError();
+    return 256;
+  }
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n > 0) return n;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) {
+    (void)hipGetLastError();
+    n = 256;
+  }
+  cache[dev].store(n, std::memory_order_relaxed);
+  return n;
+}
+
+template <int MB, int CW, int JW, int NP, int NS, bool ACT, bool NARROW>
 static int launch_gmm_ws(const uint16_t *lhs, const int32_t *row_idx, int64_t lhs_rows, int64_t M, int64_t K,
                          const uint8_t *w, const uint8_t *s,
                          const int32_t *gs, int ng, const int32_t *go, int64_t e_local, int64_t N, void *out,
-                         int out_f32, const GmmEpilogue &ep, hipStream_t st) {
+                         int out_f32, const GmmEpilogue &ep, int ncu, hipStream_t st) {
   using C = WsCfg<MB, CW, JW, NP, NS>;
-  constexpr int MT = 32 * MB, NT = C::NT;
+  constexpr int MT = 32 * MB, NT = C::NT, NC = 2 * MB;
   const int64_t n_tiles = (N + NT - 1) / NT;
   const int64_t max_tiles = ((M + MT - 1) / MT + e_local) * n_tiles;
-  // Per XCD at most ceil(n_a / 8) tiles of each class: <= max_tiles / 8 + MB.
-  const int64_t grid = ((max_tiles + 7) / 8 + MB) * 8;
+  // Per XCD at most ceil(n_a / 8) tiles of each class: <= entries / 8 + NC,
+  // where a narrow split keeps the entry count within ncu.
+  const int64_t entries = NARROW ? std::max<int64_t>(max_tiles, ncu) : max_tiles;
+  const int64_t grid = ((entries + 7) / 8 + NC) * 8;
   DWM_UNSUPPORTED_IF(grid > (1ll << 31) - 1, "gmm_fp4: too many tiles (%lld)", (long long)grid);
   DWM_UNSUPPORTED_IF(K > (1 << 24), "gmm_fp4: K <= 2^24 required");
-  hipLaunchKernelGGL((gmm_fp4_ws_kernel<C, MB, ACT>), dim3((unsigned)grid), dim3(C::THREADS), 0, st, lhs, row_idx,
-                     lhs_rows, M, (int)K, w,
-                     s, gs, ng, go, e_local, (int)N, out, out_f32, ep);
+  hipLaunchKernelGGL((gmm_fp4_ws_kernel<C, MB, ACT, NARROW>), dim3((unsigned)grid), dim3(C::THREADS), 0, st, lhs,
+                     row_idx, lhs_rows, M, (int)K, w, s, gs, ng, go, e_local, (int)N, out, out_f32, ep, ncu);
   return launch_status("gmm_fp4");
 }
 
@@ -367,12 +467,18 @@ int launch_gmm_bf16(const uint16_t *lhs, const int32_t *row_idx, int64_t lhs_row
   // 96-row x 512-column tiles, 8 consumer + 4 producer waves, four 64-deep
   // K stages (120 KB of LDS, under 168 VGPRs: one block of 12 waves per CU).
   // Measured fastest on the decode and prefill workloads among the tile,
-  // wave-split and pipeline-depth variants tried.
-  if (gated)
-    return launch_gmm_ws<3, 8, 2, 4, 4, true>(lhs, row_idx, lhs_rows, M, K, weight, scale, group_sizes, num_groups,
-                                              group_offset, E_local, N, out, out_f32, ep, st);
-  return launch_gmm_ws<3, 8, 2, 4, 4>(lhs, row_idx, lhs_rows, M, K, weight, scale, group_sizes, num_groups,
-                                      group_offset, E_local, N, out, out_f32, ep, st);
+  // wave-split and pipeline-depth variants tried.  The narrow-split kernel
+  // is launched when even the fewest tiles M rows can make (every group
+  // local and full) leave CUs idle; larger launches never split, and run the
+  // kernel without the narrow producers.
+  const int ncu = device_cu_count();
+  const bool narrow = ((M + 95) / 96) * ((N + 511) / 512) < ncu;
+#define DWM_GMM_WS(ACT, NARROW)                                                                                   \
+  launch_gmm_ws<3, 8, 2, 4, 4, ACT, NARROW>(lhs, row_idx, lhs_rows, M, K, weight, scale, group_sizes, num_groups, \
+                                             group_offset, E_local, N, out, out_f32, ep, ncu, st)
+  if (gated) return narrow ? DWM_GMM_WS(true, true) : DWM_GMM_WS(true, false);
+  return narrow ? DWM_GMM_WS(false, true) : DWM_GMM_WS(false, false);
+#undef DWM_GMM_WS
 }
 
 // Checks shared by every form of the grouped matmul, then the launch.

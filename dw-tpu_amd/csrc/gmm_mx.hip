@@ -342,7 +342,7 @@ __global__ __launch_bounds__(C::THREADS) void gmm_mx_kernel(
   const int tid = threadIdx.x, wave = tid >> 6;
   const int go = group_offset ? group_offset[0] : 0;
   TileRef ref;
-  if (!find_tile<MB, C::THREADS>(group_sizes, num_groups, go, e_local, M, (N + C::NT - 1) / C::NT, s_rowstart,
+  if (!find_tile<MB, 32, C::THREADS>(group_sizes, num_groups, go, e_local, M, (N + C::NT - 1) / C::NT, 0, 0, s_rowstart,
                                  s_cls, s_info, ref))
     return;
   const int g = ref.g, nt = ref.nt, rows = ref.rows;
@@ -573,7 +573,7 @@ __global__ __launch_bounds__(C::THREADS) void gmm_mx128_kernel(
   const int tid = threadIdx.x, wave = tid >> 6;
   const int go = group_offset ? group_offset[0] : 0;
   TileRef ref;
-  if (!find_tile<MB, C::THREADS>(group_sizes, num_groups, go, e_local, M, (N + C::NT - 1) / C::NT, s_rowstart,
+  if (!find_tile<MB, 32, C::THREADS>(group_sizes, num_groups, go, e_local, M, (N + C::NT - 1) / C::NT, 0, 0, s_rowstart,
                                  s_cls, s_info, ref))
     return;
   const int g = ref.g, nt = ref.nt, rows = ref.rows;

@@ -1,7 +1,8 @@
 // Shared parts of the ragged grouped matmul kernels (gmm_fp4.hip: bf16
 // MFMA on decoded weights; gmm_mx.hip: scaled MFMA on e4m3 activations):
 // the device-side tile list over ragged group_sizes, the fused activation
-// and the LDS-staged epilogue of a consumer wave's 32 x 64 accumulators.
+// and the LDS-staged epilogue of a consumer wave's accumulators (32x32 or
+// 16x16 MFMA layouts) for its 64 columns.
 #pragma once
 
 #include "common.h"
@@ -13,23 +14,24 @@ constexpr float kSwigluLimit = 10.0f;  // DeepSeek V4 swiglu_limit of silu_and_m
 
 // Row tiles are ordered by cost.  A local group of sz rows has sz / MT full
 // row tiles and, when sz % MT != 0, one partial tile; a row tile's class is
-// its count of 32-row MFMA blocks (1 .. MB), the full tiles' class being MB.
-// Wave 0 computes the exclusive row starts of every group and, per class
-// (index 0 = MB blocks, largest first), the exclusive prefix over groups of
-// that class's row tiles; s_cls[a * kClsStride + num_groups] is the class
+// its count of CG-row MFMA blocks (1 .. NC = MT / CG), the full tiles' class
+// being NC.  Wave 0 computes the exclusive row starts of every group and, per
+// class (index 0 = NC blocks, largest first), the exclusive prefix over groups
+// of that class's row tiles; s_cls[a * kClsStride + num_groups] is the class
 // total.
 constexpr int kClsStride = kMaxGroups + 1;
 
-template <int MB>
+template <int MB, int CG>
 __device__ __forceinline__ void tile_classes(const int32_t *group_sizes, int num_groups, int go, int64_t e_local,
                                              int *s_rowstart, int *s_cls) {
-  constexpr int MT = 32 * MB;
+  constexpr int MT = 32 * MB, NC = MT / CG;
+  static_assert(NC * CG == MT, "class granularity divides the tile");
   const int lane = threadIdx.x & 63;
   if ((threadIdx.x >> 6) == 0) {
     int row_carry = 0;
-    int carry[MB];
+    int carry[NC];
 #pragma unroll
-    for (int a = 0; a < MB; ++a) carry[a] = 0;
+    for (int a = 0; a < NC; ++a) carry[a] = 0;
     for (int base = 0; base < num_groups; base += 64) {
       const int g = base + lane;
       int sz = g < num_groups ? group_sizes[g] : 0;
@@ -37,13 +39,13 @@ __device__ __forceinline__ void tile_classes(const int32_t *group_sizes, int num
       const bool local = g >= go && (int64_t)g < (int64_t)go + e_local;
       const int n_full = local ? sz / MT : 0;
       const int rem = local ? sz % MT : 0;
-      const int rem_cls = (rem + 31) >> 5;  // 0 when there is no partial tile
+      const int rem_cls = (rem + CG - 1) / CG;  // 0 when there is no partial tile
       const int ri = wave_inclusive_scan(sz);
       if (g < num_groups) s_rowstart[g] = row_carry + ri - sz;
       row_carry += __shfl(ri, 63, 64);
 #pragma unroll
-      for (int a = 0; a < MB; ++a) {
-        const int cnt = (a == 0 ? n_full : 0) + (rem_cls == MB - a ? 1 : 0);
+      for (int a = 0; a < NC; ++a) {
+        const int cnt = (a == 0 ? n_full : 0) + (rem_cls == NC - a ? 1 : 0);
         const int ci = wave_inclusive_scan(cnt);
         if (g < num_groups) s_cls[a * kClsStride + g] = carry[a] + ci - cnt;
         carry[a] += __shfl(ci, 63, 64);
@@ -51,59 +53,84 @@ __device__ __forceinline__ void tile_classes(const int32_t *group_sizes, int num
     }
     if (lane == 0) {
 #pragma unroll
-      for (int a = 0; a < MB; ++a) s_cls[a * kClsStride + num_groups] = carry[a];
+      for (int a = 0; a < NC; ++a) s_cls[a * kClsStride + num_groups] = carry[a];
     }
   }
 }
 
 // The block's tile: (local group g, rows row0 .. row0 + rows - 1) x column
-// tile nt.
+// tile nt, of the wide tile width, or of half of it when `narrow`.
 struct TileRef {
-  int g, rows, nt;
+  int g, rows, nt, narrow;
   int64_t row0;
 };
 
 // Every thread of the block calls this (it holds two block barriers).  Work
-// list: the (row tile, column tile) pairs of class 0 (MB blocks), then class
+// list: the (row tile, column tile) pairs of class 0 (NC blocks), then class
 // 1, ... (longest first, so the dispatcher's in-order refill of free CUs
 // balances them).  Each class is cut into 8 contiguous runs, one per XCD
 // (blocks equal mod 8 run on one XCD), so a row tile's column tiles share
-// that XCD's L2.  Returns false when the block has no tile.
-template <int MB, int THREADS>
+// that XCD's L2.
+//
+// Narrow split (n_tiles_n > 0): when the wide tiles leave some of the ncu CUs
+// idle, the costliest classes are cut into column tiles of half the width
+// (n_tiles_n per row tile), whole classes at a time and only while the tile
+// count stays within ncu, so the longest tiles of a one-round launch get the
+// idle CUs.  Returns false when the block has no tile.
+template <int MB, int CG, int THREADS>
 __device__ __forceinline__ bool find_tile(const int32_t *__restrict__ group_sizes, int num_groups, int go,
-                                          int64_t e_local, int64_t M, int n_tiles, int *s_rowstart, int *s_cls,
-                                          int *s_info, TileRef &ref) {
-  constexpr int MT = 32 * MB;
+                                          int64_t e_local, int64_t M, int n_tiles, int n_tiles_n, int ncu,
+                                          int *s_rowstart, int *s_cls, int *s_info, TileRef &ref) {
+  constexpr int MT = 32 * MB, NC = MT / CG;
   const int tid = threadIdx.x;
-  tile_classes<MB>(group_sizes, num_groups, go, e_local, s_rowstart, s_cls);
+  tile_classes<MB, CG>(group_sizes, num_groups, go, e_local, s_rowstart, s_cls);
   if (tid == 0) s_info[0] = -1;
   __syncthreads();
+  int nsplit = 0;
+  if (n_tiles_n > 0) {
+    int64_t spare = (int64_t)ncu;
+#pragma unroll
+    for (int a = 0; a < NC; ++a) spare -= (int64_t)s_cls[a * kClsStride + num_groups] * n_tiles;
+    bool open = true;
+#pragma unroll
+    for (int a = 0; a < NC; ++a) {
+      const int64_t extra = (int64_t)s_cls[a * kClsStride + num_groups] * (n_tiles_n - n_tiles);
+      if (open && extra <= spare) {
+        spare -= extra;
+        nsplit = a + 1;
+      } else {
+        open = false;
+      }
+    }
+  }
   const int xcd = blockIdx.x & 7;
   int64_t j = blockIdx.x >> 3;
-  int cls = -1;
+  int cls = -1, per_row = n_tiles;
   int64_t entry = 0;
 #pragma unroll
-  for (int a = 0; a < MB; ++a) {
-    const int64_t n_a = (int64_t)s_cls[a * kClsStride + num_groups] * n_tiles;
+  for (int a = 0; a < NC; ++a) {
+    const int nt_a = a < nsplit ? n_tiles_n : n_tiles;
+    const int64_t n_a = (int64_t)s_cls[a * kClsStride + num_groups] * nt_a;
     const int64_t per = (n_a + 7) / 8;
     const int64_t lo = xcd * per, hi = min(lo + per, n_a);
     const int64_t len = hi > lo ? hi - lo : 0;
     if (cls < 0) {
       if (j < len) {
         cls = a;
+        per_row = nt_a;
         entry = lo + j;
       } else {
         j -= len;
       }
     }
   }
-  const int trow = cls >= 0 ? (int)(entry / n_tiles) : -1;
+  const int trow = cls >= 0 ? (int)(entry / per_row) : -1;
   if (cls >= 0) {
     const int *const cs = s_cls + cls * kClsStride;
     for (int g = tid; g < num_groups; g += THREADS) {
       if (cs[g] <= trow && trow < cs[g + 1]) {
         const int sz = group_sizes[g];
-        // Class 0 holds the full tiles (then a partial one of MB blocks);
+        // Class 0 holds the full tiles (then a partial one of NC blocks);
         // the other classes hold one partial tile per group.
         const int tt = cls == 0 ? trow - cs[g] : sz / MT;
         s_info[0] = g;
@@ -115,7 +142,8 @@ __device__ __forceinline__ bool find_tile(const int32_t *__restrict__ group_size
   __syncthreads();  // also retires the class reads before the stages overwrite them
   ref.g = s_info[0];
   if (cls < 0 || ref.g < 0) return false;
-  ref.nt = (int)(entry % n_tiles);
+  ref.nt = (int)(entry % per_row);
+  ref.narrow = cls < nsplit;
   ref.row0 = s_info[1];
   // group_sizes lives on the device and is not checked by the host: sizes
   // whose sum leaves int32 would give row starts outside [0, M).  Such tiles
@@ -222,6 +250,65 @@ __device__ __forceinline__ void store_tile(const f32x16_t (&acc)[AM][2], float *
       const int q = lane + 64 * i;
       const int lr = q / (CO / 8), c8 = q % (CO / 8);
       const int row = mb * 32 + lr;
+      const int64_t col = ocol0 + 8 * c8;
+      float v[8];
+      const f32x4_t lo = *(const f32x4_t *)(ep + lr * ES + 8 * c8);
+      const f32x4_t hi = *(const f32x4_t *)(ep + lr * ES + 8 * c8 + 4);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        v[k] = lo[k];
+        v[4 + k] = hi[k];
+      }
+      if (row < rows && col < n_out) store8(out, (row0 + row) * n_out + col, v, out_f32);
+    }
+  }
+}
+
+// Writes one consumer wave's 16x16x32 MFMA accumulators for NH 16-row
+// blocks (register r of acc[hb][u] in lane (c16, q) is tile row 16 hb + 4 q +
+// r, column 16 u + c16 of the wave's 64 packed columns col0 .. col0 + 63)
+// through `ep` like store_tile, 16 rows at a time.  With ACT, acc[hb][u] and
+// acc[hb][u + 2] are the gate and up projections of output column
+// 16 u + c16 (packed columns 32 j + c hold source column j N / 2 + col0 / 2 + c).
+template <int NH, bool ACT, int ES>
+__device__ __forceinline__ void store_halves(const f32x4_t (&acc)[NH][4], float *ep, int64_t row0, int rows,
+                                             int64_t col0, int N, void *__restrict__ out, int out_f32,
+                                             const void *__restrict__ bias, int bias_bf16, int act) {
+  const int lane = threadIdx.x & 63, c16 = lane & 15, q = lane >> 4;
+  constexpr int CO = ACT ? 32 : 64;
+  const int64_t n_out = ACT ? N / 2 : N;
+  const int64_t ocol0 = ACT ? col0 / 2 : col0;
+  float b[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (bias) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int c = 16 * (u & 1) + c16;  // column within its 32-column block
+      const int64_t s = ACT ? (u < 2 ? col0 / 2 + c : N / 2 + col0 / 2 + c) : col0 + 16 * u + c16;
+      if (s < N) b[u] = bias_at(bias, bias_bf16, s);
+    }
+  }
+#pragma unroll
+  for (int hb = 0; hb < NH; ++hb) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int lr = 4 * q + r;
+      float v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) v[u] = bias ? acc[hb][u][r] + b[u] : acc[hb][u][r];
+      if constexpr (ACT) {
+        ep[lr * ES + c16] = act_pair(act, v[0], v[2]);
+        ep[lr * ES + 16 + c16] = act_pair(act, v[1], v[3]);
+      } else {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) ep[lr * ES + 16 * u + c16] = v[u];
+      }
+    }
+    // Lane p of chunk i covers row p / (CO / 8), columns 8 (p % (CO / 8)) .. + 7.
+#pragma unroll
+    for (int i = 0; i < 16 * CO / 8 / 64; ++i) {
+      const int p = lane + 64 * i;
+      const int lr = p / (CO / 8), c8 = p % (CO / 8);
+      const int row = 16 * hb + lr;
       const int64_t col = ocol0 + 8 * c8;
       float v[8];
       const f32x4_t lo = *(const f32x4_t *)(ep + lr * ES + 8 * c8);

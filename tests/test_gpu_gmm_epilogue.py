@@ -154,3 +154,54 @@ def test_bias_with_group_offset_window(dev, rng, mx, act):
     assert np.all(got[~written] == 0)
     err = np.abs(got[written] - want[written])
     assert np.all(err <= bound[written]), float((err / bound[written]).max())
+
+
+@pytest.mark.parametrize("act", [None, "silu_and_mul_with_clamp"])
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("window", [False, True])
+def test_remainder_rows_every_count(dev, rng, act, out_dtype, window):
+    """Row tiles of every 16-row block count (1 .. 6) and fill, the first and
+    last rows of a block included, with a bias and N = 640 (a 512-column tile
+    and a part-filled one; as 256-column tiles, one of them past N by two
+    groups).  The tile list leaves most CUs idle, so every class runs as
+    narrow tiles; with `window` a 12,288-row group outside the expert-parallel
+    window (group_offset 1) comes first, so the launch sizes its grid for
+    that many rows and runs the kernel without narrow tiles on the same
+    local groups.  Against the float64 oracle under the bounds above; rows
+    outside the window are zero."""
+    from dw_tpu_amd import fp4_weight_to_codes, gmm_v2
+    K, N = 256, 640
+    local = [1, 16, 17, 32, 33, 48, 49, 64, 0, 65, 80, 81, 96, 97, 112, 113, 160, 161, 177, 192, 5]
+    sizes = ([12288] if window else []) + local
+    go = 1 if window else 0
+    e_local = len(local)
+    lhs_bits = to_bf16_bits(rng.standard_normal((sum(sizes), K)).astype(np.float32))
+    rhs = rng.integers(0, 256, (e_local, K, N // 2), dtype=np.uint8)
+    sc = rng.integers(122, 128, (e_local, K // 32, 1, N), dtype=np.uint8)
+    bias = (rng.standard_normal((e_local, N)) * 4).astype(np.float32)
+    gs = np.array(sizes, np.int32)
+    pw = fp4_weight_to_codes(torch.from_numpy(rhs).to(dev), torch.from_numpy(sc).to(dev), gate_up=act is not None)
+    out = gmm_v2(bf16_tensor(lhs_bits, dev), pw, torch.from_numpy(gs).to(dev),
+                 rhs_bias=torch.from_numpy(bias).to(dev), group_offset=go if window else None, fuse_act=act,
+                 preferred_element_type=out_dtype, zero_initialize=window)
+    torch.cuda.synchronize()
+    a = bf16_to_f32(lhs_bits)
+    w = _w(rhs, sc)
+    y64, written = gmm.gmm(a, None, None, gs, group_offset=go, out_dtype="float64", w=w, bias=bias)
+    ap = gmm.abs_product(a, w, gs, group_offset=go)
+    acc_err = K * 2.0 ** -24 * ap + 2.0 ** -24 * np.abs(y64)
+    if out_dtype == torch.float32:
+        got = out.cpu().numpy().astype(np.float64)
+        rnd = 2.0 ** -24
+    else:
+        got = bf16_to_f32(bf16_bits(out)).astype(np.float64)
+        rnd = 2.0 ** -8
+    if act is None:
+        want, bound = y64, rnd * np.abs(y64) + acc_err
+    else:
+        want, bound = omb.apply_act(y64, act), omb.act_bound(y64, acc_err, act)
+    assert int(written.sum()) == sum(local)
+    assert np.all(got[~written] == 0)
+    err = np.abs(got[written] - want[written])
+    assert np.all(np.isfinite(got))
+    assert np.all(err <= bound[written]), (float(err.max()), float((err / bound[written]).max()))
