@@ -105,13 +105,19 @@ __global__ __launch_bounds__(256) void mx_quant_e4m3_kernel(const uint16_t *__re
 // ---------------------------------------------------------------------------
 // The MX tile kernel.
 
-template <int MB, int CW, int NP, int NS>
+// RH = 2 stacks two row halves: the tile is (32 MB x 2 rows) x (64 CW / 2
+// columns), consumer cw owning column group cw % GT of row half cw / GT (the
+// two consumers of a SIMD, cw and cw + 4, then hold both halves).  A group
+// of up to 192 rows then reads its weights once, not once per 96 rows.
+template <int MB, int CW, int NP, int NS, int RH = 1>
 struct MxCfg {
-  static constexpr int CONS = CW, NPROD = NP, STAGES = NS;
-  static constexpr int GT = CW;                          // 64-column groups per tile, one per consumer
+  static constexpr int CONS = CW, NPROD = NP, STAGES = NS, HALVES = RH;
+  static constexpr int GT = CW / RH;                     // 64-column groups per tile
   static constexpr int THREADS = 64 * (CW + NP);
   static constexpr int NT = 64 * GT;
-  static constexpr int ROWS = 32 * MB;
+  static constexpr int CMB = MB;                         // 32-row blocks of one consumer
+  static constexpr int TMB = MB * RH;                    // 32-row blocks of the tile
+  static constexpr int ROWS = 32 * TMB;
   static constexpr int W = 0;                            // group i: 2 KiB at W + 2048 i
   static constexpr int A = GT * 2048;                    // ROWS x 64 bytes
   static constexpr int AS = A + ROWS * 64;               // 128-row groups x 256 bytes (dword per row)
@@ -122,7 +128,7 @@ struct MxCfg {
   static constexpr int G_LOADS = GT / NP;                // weight groups per producer
   static constexpr int AHEAD = 2;                        // steps published per barrier
   static constexpr int EP_STRIDE = 72;
-  static_assert(ROWS % 16 == 0 && G_LOADS * NP == GT, "load split");
+  static_assert(ROWS % 16 == 0 && G_LOADS * NP == GT && GT * RH == CW, "load split");
   static_assert(AS_LOADS <= NP, "one row-scale load per producer at most");
   static constexpr int INFLIGHT = NS - 1 - AHEAD;        // steps loading behind the published pair
   static_assert(INFLIGHT >= 1, "stage count");
@@ -230,10 +236,11 @@ __device__ __forceinline__ void mx_producer(const uint8_t *__restrict__ lhs, con
   __builtin_amdgcn_s_barrier();
 }
 
+// Consumer cw of column group cg, tile rows rb .. rb + rows - 1 (its row half).
 template <class C, int AM, bool ACT>
-__device__ __forceinline__ void mx_consumer(int T, uint8_t *s_lds, int cw, int64_t row0, int rows, int64_t col0,
-                                            int N, void *__restrict__ out, int out_f32, const void *bias,
-                                            const GmmEpilogue &ep) {
+__device__ __forceinline__ void mx_consumer(int T, uint8_t *s_lds, int cw, int cg, int rb, int64_t row0, int rows,
+                                            int64_t col0, int N, void *__restrict__ out, int out_f32,
+                                            const void *bias, const GmmEpilogue &ep) {
   constexpr int NS = C::STAGES;
   const int lane = threadIdx.x & 63, c32 = lane & 31, h = lane >> 5;
   f32x16_t acc[AM][2];
@@ -243,13 +250,13 @@ __device__ __forceinline__ void mx_consumer(int T, uint8_t *s_lds, int cw, int64
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[mb][j][r] = 0.0f;
-  const int woff = C::W + cw * 2048 + lane * 16;
-  const int soff = C::S + cw * 256 + lane * 4;
-  // A fragment of row block mb: row mb * 32 + c32 (same swizzle for all mb),
-  // logical chunks h and 2 + h.
+  const int woff = C::W + cg * 2048 + lane * 16;
+  const int soff = C::S + cg * 256 + lane * 4;
+  // A fragment of row block mb: row rb + mb * 32 + c32 (same swizzle for all
+  // mb, rb % 16 == 0), logical chunks h and 2 + h.
   const int sw = mx_swizzle(c32);
-  const int alo = C::A + c32 * 64 + ((h ^ sw) << 4);
-  const int ahi = C::A + c32 * 64 + (((2 + h) ^ sw) << 4);
+  const int alo = C::A + (rb + c32) * 64 + ((h ^ sw) << 4);
+  const int ahi = C::A + (rb + c32) * 64 + (((2 + h) ^ sw) << 4);
   u32x4_t wn[2];
   uint32_t sn = 0, asn[AM];
   i32x8_t an;
@@ -260,7 +267,7 @@ __device__ __forceinline__ void mx_consumer(int T, uint8_t *s_lds, int cw, int64
   auto read_s = [&](const uint8_t *st) {  // even steps: scale dwords of this and the next step
     sn = *(const uint32_t *)(st + soff);
 #pragma unroll
-    for (int mb = 0; mb < AM; ++mb) asn[mb] = *(const uint32_t *)(st + C::AS + (mb * 32 + c32) * 4);
+    for (int mb = 0; mb < AM; ++mb) asn[mb] = *(const uint32_t *)(st + C::AS + (rb + mb * 32 + c32) * 4);
   };
   auto read_a = [&](const uint8_t *st, int mb) {
     const u32x4_t lo = *(const u32x4_t *)(st + alo + mb * 32 * 64);
@@ -326,14 +333,42 @@ __device__ __forceinline__ void mx_consumer(int T, uint8_t *s_lds, int cw, int64
                                     out_f32, bias, ep.bias_bf16, ep.act);
 }
 
-template <class C, int MB, bool ACT>
+// Producer dispatch on the lhs row groups that hold rows (NA) and on whether
+// this producer also loads a part of the row scales.
+template <class C, int NA = (C::A_GROUPS + C::NPROD - 1) / C::NPROD>
+__device__ __forceinline__ void mx_produce(int na, bool asl, const uint8_t *lhs, const uint8_t *lsc,
+                                           const int32_t *row_idx, int64_t lhs_rows, int64_t row0, int rows, int K,
+                                           int T, int KB, const uint8_t *wexp, const uint8_t *sexp, int g0, int G,
+                                           uint8_t *s_lds, int pw) {
+  if constexpr (NA > 0) {
+    if (na < NA) {
+      mx_produce<C, NA - 1>(na, asl, lhs, lsc, row_idx, lhs_rows, row0, rows, K, T, KB, wexp, sexp, g0, G, s_lds, pw);
+      return;
+    }
+  }
+  if (asl)
+    mx_producer<C, NA, true>(lhs, lsc, row_idx, lhs_rows, row0, rows, K, T, KB, wexp, sexp, g0, G, s_lds, pw);
+  else
+    mx_producer<C, NA, false>(lhs, lsc, row_idx, lhs_rows, row0, rows, K, T, KB, wexp, sexp, g0, G, s_lds, pw);
+}
+
+// A consumer whose row half holds no rows keeps the barrier count (T + 1).
+__device__ __forceinline__ void mx_idle_consumer(int T) {
+  for (int t = 0; t <= T; ++t) {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  }
+}
+
+template <class C, bool ACT>
 __global__ __launch_bounds__(C::THREADS) void gmm_mx_kernel(
     const uint8_t *__restrict__ lhs, const uint8_t *__restrict__ lsc, const int32_t *__restrict__ row_idx,
     int64_t lhs_rows, int64_t M, int K, const uint8_t *__restrict__ wpk, const uint8_t *__restrict__ spk,
     const int32_t *__restrict__ group_sizes, int num_groups, const int32_t *__restrict__ group_offset,
     int64_t e_local, int N, void *__restrict__ out, int out_f32, GmmEpilogue ep) {
-  constexpr int CW = C::CONS, NP = C::NPROD;
-  static_assert(C::STAGES * C::STAGE >= (kMaxGroups + MB * kClsStride) * 4, "tile classes alias the stages");
+  constexpr int CW = C::CONS, NP = C::NPROD, TMB = C::TMB, CMB = C::CMB;
+  static_assert(C::STAGES * C::STAGE >= (kMaxGroups + TMB * kClsStride) * 4, "tile classes alias the stages");
   __shared__ __attribute__((aligned(1024))) uint8_t s_lds[C::STAGES * C::STAGE];
   __shared__ int s_info[3];
   int *s_rowstart = (int *)s_lds;
@@ -342,8 +377,8 @@ __global__ __launch_bounds__(C::THREADS) void gmm_mx_kernel(
   const int tid = threadIdx.x, wave = tid >> 6;
   const int go = group_offset ? group_offset[0] : 0;
   TileRef ref;
-  if (!find_tile<MB, 32, C::THREADS>(group_sizes, num_groups, go, e_local, M, (N + C::NT - 1) / C::NT, 0, 0, s_rowstart,
-                                 s_cls, s_info, ref))
+  if (!find_tile<TMB, 32, C::THREADS>(group_sizes, num_groups, go, e_local, M, (N + C::NT - 1) / C::NT, 0, 0,
+                                      s_rowstart, s_cls, s_info, ref))
     return;
   const int g = ref.g, nt = ref.nt, rows = ref.rows;
   const int64_t row0 = ref.row0;
@@ -354,33 +389,28 @@ __global__ __launch_bounds__(C::THREADS) void gmm_mx_kernel(
     const int pw = wave - CW;
     const uint8_t *const wexp = wpk + e * G * T * 2048;
     const uint8_t *const sexp = spk + e * G * KB * 256;
-    // Row groups pw + NP i (i < MAXA, < A_GROUPS) with 16 (pw + NP i) < rows are loaded.
+    // Row groups pw + NP i (< A_GROUPS) with 16 (pw + NP i) < rows are loaded.
     int na = 0;
     for (int ga = pw; ga < C::A_GROUPS; ga += NP) na += 16 * ga < rows ? 1 : 0;
     const bool asl = pw >= NP - C::AS_LOADS;
-    auto run = [&](auto na_c, auto asl_c) {
-      mx_producer<C, decltype(na_c)::value, decltype(asl_c)::value != 0>(lhs, lsc, row_idx, lhs_rows, row0, rows, K,
-                                                                          T, KB, wexp, sexp, g0, G, s_lds, pw);
-    };
-    // A_GROUPS = 6 over 4 producers: producers 0, 1 own two row groups, 2, 3 one.
-    static_assert(C::A_GROUPS <= 2 * NP, "at most two lhs row groups per producer");
-    if (asl) {
-      if (na >= 2) run(IntC<2>{}, IntC<1>{});
-      else if (na == 1) run(IntC<1>{}, IntC<1>{});
-      else run(IntC<0>{}, IntC<1>{});
-    } else {
-      if (na >= 2) run(IntC<2>{}, IntC<0>{});
-      else if (na == 1) run(IntC<1>{}, IntC<0>{});
-      else run(IntC<0>{}, IntC<0>{});
-    }
+    mx_produce<C>(na, asl, lhs, lsc, row_idx, lhs_rows, row0, rows, K, T, KB, wexp, sexp, g0, G, s_lds, pw);
     return;
   }
-  const int act_mb = (rows + 31) >> 5;
-  const int64_t col0 = (int64_t)(g0 + wave) * 64;
+  const int cg = wave % C::GT, rb = 32 * CMB * (wave / C::GT);
+  const int rows_h = min(rows - rb, 32 * CMB);  // rows of this consumer's half
+  if (rows_h <= 0) {
+    mx_idle_consumer(T);
+    return;
+  }
+  const int act_mb = (rows_h + 31) >> 5;
+  const int64_t col0 = (int64_t)(g0 + cg) * 64;
   const void *const bias = expert_bias(ep, e, N);
-  if (act_mb <= 1 || MB == 1) mx_consumer<C, 1, ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32, bias, ep);
-  else if (act_mb == 2 || MB == 2) mx_consumer<C, (MB >= 2 ? 2 : 1), ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32, bias, ep);
-  else mx_consumer<C, MB, ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32, bias, ep);
+  if (act_mb <= 1 || CMB == 1)
+    mx_consumer<C, 1, ACT>(T, s_lds, wave, cg, rb, row0 + rb, rows_h, col0, N, out, out_f32, bias, ep);
+  else if (act_mb == 2 || CMB == 2)
+    mx_consumer<C, (CMB >= 2 ? 2 : 1), ACT>(T, s_lds, wave, cg, rb, row0 + rb, rows_h, col0, N, out, out_f32, bias,
+                                            ep);
+  else mx_consumer<C, CMB, ACT>(T, s_lds, wave, cg, rb, row0 + rb, rows_h, col0, N, out, out_f32, bias, ep);
 }
 
 // ---------------------------------------------------------------------------
@@ -626,7 +656,7 @@ static int launch_mx(const uint8_t *lhs, const uint8_t *lsc, const int32_t *row_
     hipLaunchKernelGGL((gmm_mx128_kernel<C, MB, ACT>), dim3((unsigned)grid), dim3(C::THREADS), 0, st, lhs, lsc,
                        row_idx, lhs_rows, M, (int)K, w, s, gs, ng, go, e_local, (int)N, out, out_f32, ep);
   else
-    hipLaunchKernelGGL((gmm_mx_kernel<C, MB, ACT>), dim3((unsigned)grid), dim3(C::THREADS), 0, st, lhs, lsc, row_idx,
+    hipLaunchKernelGGL((gmm_mx_kernel<C, ACT>), dim3((unsigned)grid), dim3(C::THREADS), 0, st, lhs, lsc, row_idx,
                        lhs_rows, M, (int)K, w, s, gs, ng, go, e_local, (int)N, out, out_f32, ep);
   return launch_status("gmm_fp4_mx");
 }
@@ -639,18 +669,22 @@ int launch_gmm_mx(const uint8_t *lhs, const uint8_t *lhs_scale, const int32_t *r
   // 96-row x 512-column tiles, 8 consumer + 4 producer waves.  64-deep K
   // steps in a five-stage ring (two published per barrier, two in flight),
   // or 128-deep steps in a three-stage ring (one published, one in flight).
+  // Below K = 4096, groups of more than 96 rows on average run 192 x 256
+  // tiles (two stacked row halves), so their weights are read once:
+  // decode_down (~128 rows per group) 111 -> 106 us, measured against the
+  // 96 x 512 tiles; seven stages in place of five were slower (110 us).
   using C64 = MxCfg<3, 8, 4, 5>;
+  using C64H = MxCfg<3, 8, 4, 5, 2>;
   using C128 = Mx128Cfg<3, 8, 4, 3>;
   const bool deep = K >= kMx128MinK;
+  const bool halves = !deep && M > 96 * E_local;
+#define DWM_MX(CFG, TMB, ACT, DEEP)                                                                                \
+  launch_mx<CFG, TMB, ACT, DEEP>(lhs, lhs_scale, row_idx, lhs_rows, M, K, weight, scale, group_sizes, num_groups, \
+                                 group_offset, E_local, N, out, out_f32, ep, st)
   if (gated)
-    return deep ? launch_mx<C128, 3, true, true>(lhs, lhs_scale, row_idx, lhs_rows, M, K, weight, scale, group_sizes,
-                                                 num_groups, group_offset, E_local, N, out, out_f32, ep, st)
-                : launch_mx<C64, 3, true, false>(lhs, lhs_scale, row_idx, lhs_rows, M, K, weight, scale, group_sizes,
-                                                 num_groups, group_offset, E_local, N, out, out_f32, ep, st);
-  return deep ? launch_mx<C128, 3, false, true>(lhs, lhs_scale, row_idx, lhs_rows, M, K, weight, scale, group_sizes,
-                                                num_groups, group_offset, E_local, N, out, out_f32, ep, st)
-              : launch_mx<C64, 3, false, false>(lhs, lhs_scale, row_idx, lhs_rows, M, K, weight, scale, group_sizes,
-                                                num_groups, group_offset, E_local, N, out, out_f32, ep, st);
+    return deep ? DWM_MX(C128, 3, true, true) : halves ? DWM_MX(C64H, 6, true, false) : DWM_MX(C64, 3, true, false);
+  return deep ? DWM_MX(C128, 3, false, true) : halves ? DWM_MX(C64H, 6, false, false) : DWM_MX(C64, 3, false, false);
+#undef DWM_MX
 }
 
 }  // namespace dwm

@@ -205,3 +205,30 @@ def test_remainder_rows_every_count(dev, rng, act, out_dtype, window):
     err = np.abs(got[written] - want[written])
     assert np.all(np.isfinite(got))
     assert np.all(err <= bound[written]), (float(err.max()), float((err / bound[written]).max()))
+
+
+@pytest.mark.parametrize("act", [None, "swigluoai"])
+def test_mx_row_halves(dev, rng, act):
+    """The 64-deep MX kernel's stacked row halves (192 x 256 tiles, used
+    below K = 4096 when the groups average more than 96 rows): groups of
+    1 .. 193 rows, so a half holds 0 .. 3 row blocks and a consumer may have
+    no rows; a bias; N = 320, so the second 256-column tile holds one group
+    and three past N.  Against the float64 MX oracle under the bounds above."""
+    K, N = 256, 320
+    sizes = [1, 97, 150, 192, 193, 0, 64, 128]
+    assert sum(sizes) > 96 * len(sizes)
+    lhs_bits, rhs, sc, gs, bias = _case(rng, sizes, K, N)
+    out = _run(dev, lhs_bits, rhs, sc, gs, bias, act, True)
+    a = quant.mx_dequantize(*quant.mx_quantize_e4m3(bf16_to_f32(lhs_bits)))
+    w = _w(rhs, sc)
+    y64, _ = gmm.gmm(a, None, None, gs, out_dtype="float64", w=w, bias=bias)
+    ap = gmm.abs_product(a, w, gs)
+    acc_err = K * 2.0 ** -24 * ap + 2.0 ** -24 * np.abs(y64) + gmm.MX_BLOCK_TERM * gmm.block_max_product(a, w, gs)
+    got = bf16_to_f32(bf16_bits(out)).astype(np.float64)
+    if act is None:
+        want, bound = y64, 2.0 ** -8 * np.abs(y64) + acc_err
+    else:
+        want, bound = omb.apply_act(y64, act), omb.act_bound(y64, acc_err, act)
+    err = np.abs(got - want)
+    assert np.all(np.isfinite(got))
+    assert np.all(err <= bound), (float(err.max()), float((err / bound).max()))
