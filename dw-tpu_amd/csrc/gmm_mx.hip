@@ -669,15 +669,16 @@ int launch_gmm_mx(const uint8_t *lhs, const uint8_t *lhs_scale, const int32_t *r
   // 96-row x 512-column tiles, 8 consumer + 4 producer waves.  64-deep K
   // steps in a five-stage ring (two published per barrier, two in flight),
   // or 128-deep steps in a three-stage ring (one published, one in flight).
-  // Below K = 4096, groups of more than 96 rows on average run 192 x 256
+  // Below K = 4096, groups of 97 .. 192 rows on average run 192 x 256
   // tiles (two stacked row halves), so their weights are read once:
   // decode_down (~128 rows per group) 111 -> 106 us, measured against the
   // 96 x 512 tiles; seven stages in place of five were slower (110 us).
+  // Larger groups read their weights once per row tile either way.
   using C64 = MxCfg<3, 8, 4, 5>;
   using C64H = MxCfg<3, 8, 4, 5, 2>;
   using C128 = Mx128Cfg<3, 8, 4, 3>;
   const bool deep = K >= kMx128MinK;
-  const bool halves = !deep && M > 96 * E_local;
+  const bool halves = !deep && M > 96 * E_local && M <= 192 * E_local;
 #define DWM_MX(CFG, TMB, ACT, DEEP)                                                                                \
   launch_mx<CFG, TMB, ACT, DEEP>(lhs, lhs_scale, row_idx, lhs_rows, M, K, weight, scale, group_sizes, num_groups, \
                                  group_offset, E_local, N, out, out_f32, ep, st)

@@ -210,13 +210,13 @@ def test_remainder_rows_every_count(dev, rng, act, out_dtype, window):
 @pytest.mark.parametrize("act", [None, "swigluoai"])
 def test_mx_row_halves(dev, rng, act):
     """The 64-deep MX kernel's stacked row halves (192 x 256 tiles, used
-    below K = 4096 when the groups average more than 96 rows): groups of
+    below K = 4096 when the groups average 97 .. 192 rows): groups of
     1 .. 193 rows, so a half holds 0 .. 3 row blocks and a consumer may have
     no rows; a bias; N = 320, so the second 256-column tile holds one group
     and three past N.  Against the float64 MX oracle under the bounds above."""
     K, N = 256, 320
     sizes = [1, 97, 150, 192, 193, 0, 64, 128]
-    assert sum(sizes) > 96 * len(sizes)
+    assert 96 * len(sizes) < sum(sizes) <= 192 * len(sizes)
     lhs_bits, rhs, sc, gs, bias = _case(rng, sizes, K, N)
     out = _run(dev, lhs_bits, rhs, sc, gs, bias, act, True)
     a = quant.mx_dequantize(*quant.mx_quantize_e4m3(bf16_to_f32(lhs_bits)))
