@@ -308,6 +308,58 @@ __global__ __launch_bounds__(256) void combine_kernel(const void *x, int64_t x_r
   }
 }
 
+// The combine for bf16 rows with 16-byte aligned rows (H % 8 == 0): the
+// same arithmetic as combine_kernel, but each row's 8 values stay packed
+// (one 16-byte register quad per row, widened while accumulating), so a
+// thread holds its kCombineKG rows in 32 registers and every block of the
+// decode shapes is resident at once (8 waves per SIMD).
+template <int OF32>
+__global__ __launch_bounds__(256) void combine_bf16_kernel(const uint16_t *__restrict__ x, int64_t x_rows, int64_t H,
+                                                           const int32_t *__restrict__ idx, const void *w,
+                                                           int w_dtype, int64_t T, int topk, void *out) {
+  const int64_t c = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
+  if (c >= H) return;
+  for (int64_t t = blockIdx.y; t < T; t += gridDim.y) {
+    float acc[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+    for (int k0 = 0; k0 < topk; k0 += kCombineKG) {
+      u32x4_t raw[kCombineKG];
+      float wk[kCombineKG];
+#pragma unroll
+      for (int g = 0; g < kCombineKG; ++g) {
+        if (k0 + g < topk) {
+          const int64_t r = gather_index(idx[t * topk + k0 + g], x_rows);
+          wk[g] = load_f32(w, w_dtype, t * topk + k0 + g);
+          raw[g] = *(const u32x4_t *)(x + r * H + c);
+        }
+      }
+#pragma unroll
+      for (int g = 0; g < kCombineKG; ++g) {
+        if (k0 + g < topk) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float lo = __builtin_bit_cast(float, raw[g][i] << 16);
+            const float hi = __builtin_bit_cast(float, raw[g][i] & 0xFFFF0000u);
+            acc[2 * i] = acc[2 * i] + lo * wk[g];          // separately rounded product,
+            acc[2 * i + 1] = acc[2 * i + 1] + hi * wk[g];  // then sum, k ascending from +0.0
+          }
+        }
+      }
+    }
+    if (OF32) {
+      *(f32x4_t *)((float *)out + t * H + c) = f32x4_t{acc[0], acc[1], acc[2], acc[3]};
+      *(f32x4_t *)((float *)out + t * H + c + 4) = f32x4_t{acc[4], acc[5], acc[6], acc[7]};
+    } else {
+      u32x4_t q;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        q[i] = (uint32_t)f32_to_bf16_bits(acc[2 * i]) | ((uint32_t)f32_to_bf16_bits(acc[2 * i + 1]) << 16);
+      *(u32x4_t *)((uint16_t *)out + t * H + c) = q;
+    }
+  }
+}
+
 // The dispatch launches for n = T * topk ids with chunk counters `counts`
 // (nchunks * (E + 1) int32, fully written by the count kernel before they are
 // read, so they need no clearing).
@@ -463,6 +515,15 @@ extern "C" int dwm_moe_combine(const void *x, int x_dtype, int64_t x_rows, int64
   const dim3 grid((unsigned)((H + 2047) / 2048), (unsigned)(T < 65535 ? T : 65535));
   hipStream_t st = as_stream(stream);
   const int of32 = out_dtype == DWM_F32;
+  if (vec && !xf32) {
+    if (of32)
+      hipLaunchKernelGGL((combine_bf16_kernel<1>), grid, dim3(256), 0, st, (const uint16_t *)x, x_rows, H, idx, w,
+                         w_dtype, T, topk, out);
+    else
+      hipLaunchKernelGGL((combine_bf16_kernel<0>), grid, dim3(256), 0, st, (const uint16_t *)x, x_rows, H, idx, w,
+                         w_dtype, T, topk, out);
+    return launch_status("moe_combine");
+  }
   if (!xf32 && !of32)
     hipLaunchKernelGGL((combine_kernel<0, 0>), grid, dim3(256), 0, st, x, x_rows, H, idx, w,
                        w_dtype, T, topk, out, vec);
