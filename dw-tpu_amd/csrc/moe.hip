@@ -56,30 +56,62 @@ __global__ __launch_bounds__(1024) void dispatch_scan_kernel(int32_t *counts, in
                                                              int32_t *group_offsets) {
   __shared__ int s_tot[kMaxExperts + 1];
   __shared__ int s_off[kMaxExperts + 1];
-  for (int e = threadIdx.x; e <= E; e += blockDim.x) {
-    int t = 0;
-    for (int c = 0; c < nchunks; ++c) t += counts[(int64_t)c * (E + 1) + e];
-    s_tot[e] = t;
+  __shared__ int s_part[1024];  // [G][E + 1] sums of each chunk run
+  // counts[nchunks][E + 1]: thread (g, e) owns column e of the contiguous
+  // chunk run g, G = blockDim / (E + 1) runs (loads coalesced along e).  With
+  // more columns than threads (G = 0) each thread walks whole columns.
+  const int C = E + 1;
+  const int G = (int)blockDim.x / C;
+  const int tid = threadIdx.x;
+  const int L = G > 0 ? (nchunks + G - 1) / G : 0;
+  const int e = G > 0 ? tid % C : 0, g = G > 0 ? tid / C : 0;
+  const bool own = G > 0 && g < G;
+  const int c_lo = own ? min(nchunks, g * L) : 0, c_hi = own ? min(nchunks, c_lo + L) : 0;
+  if (own) {
+    int sum = 0;
+    for (int c = c_lo; c < c_hi; ++c) sum += counts[(int64_t)c * C + e];
+    s_part[g * C + e] = sum;
   }
   __syncthreads();
-  if (threadIdx.x < 64) {
-    const int lane = threadIdx.x;
+  for (int ee = tid; ee < C; ee += blockDim.x) {
+    int t = 0;
+    if (G > 0)
+      for (int gg = 0; gg < G; ++gg) t += s_part[gg * C + ee];
+    else
+      for (int c = 0; c < nchunks; ++c) t += counts[(int64_t)c * C + ee];
+    s_tot[ee] = t;
+  }
+  __syncthreads();
+  if (tid < 64) {
+    const int lane = tid;
     int carry = 0;
-    for (int b = 0; b <= E; b += 64) {
-      const int e = b + lane;
-      const int v = e <= E ? s_tot[e] : 0;
+    for (int b = 0; b < C; b += 64) {
+      const int ee = b + lane;
+      const int v = ee < C ? s_tot[ee] : 0;
       const int inc = wave_inclusive_scan(v);
-      if (e <= E) s_off[e] = carry + inc - v;
+      if (ee < C) s_off[ee] = carry + inc - v;
       carry += __shfl(inc, 63, 64);
     }
   }
   __syncthreads();
-  for (int e = threadIdx.x; e <= E; e += blockDim.x) {
-    if (e < E) group_sizes[e] = s_tot[e];
-    if (group_offsets) group_offsets[e] = s_off[e];  // entry E = number of valid ids
+  for (int ee = tid; ee < C; ee += blockDim.x) {
+    if (ee < E) group_sizes[ee] = s_tot[ee];
+    if (group_offsets) group_offsets[ee] = s_off[ee];  // entry E = number of valid ids
+    if (G == 0) {
+      int run = s_off[ee];
+      for (int c = 0; c < nchunks; ++c) {
+        const int64_t idx = (int64_t)c * C + ee;
+        const int v = counts[idx];
+        counts[idx] = run;
+        run += v;
+      }
+    }
+  }
+  if (own) {
     int run = s_off[e];
-    for (int c = 0; c < nchunks; ++c) {
-      const int64_t idx = (int64_t)c * (E + 1) + e;
+    for (int gg = 0; gg < g; ++gg) run += s_part[gg * C + e];
+    for (int c = c_lo; c < c_hi; ++c) {
+      const int64_t idx = (int64_t)c * C + e;
       const int v = counts[idx];
       counts[idx] = run;
       run += v;
