@@ -232,3 +232,20 @@ def test_mx_row_halves(dev, rng, act):
     err = np.abs(got - want)
     assert np.all(np.isfinite(got))
     assert np.all(err <= bound), (float(err.max()), float((err / bound).max()))
+
+
+@pytest.mark.parametrize("act", [None, "silu_and_mul_with_clamp"])
+def test_mx_row_halves_with_fused_gather(dev, rng, act):
+    """The stacked-halves MX tiles with lhs_row_indices give the bits of the
+    gathered copy through the same call (row indices read per half)."""
+    from dw_tpu_amd import row_gather
+    K, N, T = 256, 320, 300
+    sizes = [1, 97, 150, 192, 193, 0, 64, 128]
+    assert 96 * len(sizes) < sum(sizes) <= 192 * len(sizes)
+    _, rhs, sc, gs, bias = _case(rng, sizes, K, N)
+    hidden_bits = to_bf16_bits(rng.standard_normal((T, K)).astype(np.float32))
+    idx = torch.from_numpy(rng.integers(0, T, sum(sizes)).astype(np.int32)).to(dev)
+    x_bits = bf16_bits(row_gather(bf16_tensor(hidden_bits, dev), idx))
+    want = _run(dev, x_bits, rhs, sc, gs, bias, act, True)
+    got = _run(dev, hidden_bits, rhs, sc, gs, bias, act, True, idx=idx)
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
