@@ -762,7 +762,12 @@ def main():
         runs = []
         for name in ("prefill",):
             log(f"bench: inputs of {name} gmm, MX mode")
-            runs.append(prep_gmm_mx(name, dev, args.steps, args.warmup))
+            # The first timed region follows seconds of host-side input
+            # generation with the GPU idle: at least 60 warmup launches
+            # (~0.1 s of prefill load) let the clock come back up to its
+            # power-limited level first (with 5 the MX prefill measured
+            # 1.65 ms against 1.55 ms after a settled clock).
+            runs.append(prep_gmm_mx(name, dev, args.steps, max(args.warmup, 60)))
             log(f"bench: inputs of {name} gmm")
             runs.append(prep_gmm(name, dev, args.steps, args.warmup))
         for label, prep in (("moe block", prep_moe_block), ("dense fp8", prep_dense),
