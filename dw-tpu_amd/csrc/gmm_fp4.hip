@@ -59,8 +59,9 @@ __device__ __forceinline__ int lhs_swizzle(int r) { return (r >> 1) & 7; }
 // Scale layout: for (e, g, 128-deep step kb) 256 bytes; byte 2 f + j of lane
 // l = c + 32 h is the e8m0 code of column 64 g + 32 j + c, K-block
 // 4 kb + 2 f + h.  Decoded, lane (c, h)'s codes k = 64 t + 32 h + 8 s .. + 7
-// are the B operand of a 32x32x16 MFMA step s; the consumer turns pairs of
-// such steps into 16x16x32 operands (ws_consumer).
+// are the B operand of a 32x32x16 MFMA step s (the MX kernel's 32x32x64
+// operand is the lane's 16 bytes as they are); the consumers here read the
+// 4-byte pieces of the 16x16x32 operands from their slots (ws_consumer).
 // Block shape: CW consumer waves owning JW 32-column blocks each (a tile of
 // 32 JW CW columns = GT 64-column groups), NP producer waves, NS LDS stages.
 template <int MB, int CW, int JW, int NP, int NS>
@@ -167,16 +168,16 @@ __device__ __forceinline__ void ws_producer(const uint16_t *__restrict__ lhs, co
 // A consumer wave runs its 64 columns for NH 16-row blocks of the tile with
 // 16x16x32 MFMAs: every row of every tile sums K in the same grouping, so a
 // row's result depends on its own lhs row only (not on its place in the
-// tile), and MFMA work follows the rows in steps of 16.  The weights are
-// decoded in the 32x32x16 lane layout the prepack writes (lane (c, h) holds
-// column 32 j + c at k = 32 h + 8 s .. + 7 of the K step, s = 0 .. 3);
-// v_permlane16_swap of the decoded steps 2v and 2v + 1 turns them into the
-// 16x16x32 B operands of column blocks 2j (first result) and 2j + 1
-// (second): lane row q = lane / 16 then holds K chunk (h = q / 2, s = 2v +
-// q % 2) of column 16 u + lane % 16, and the lhs fragment of MFMA step v
-// reads the same K chunk.  Each K step runs 2 x NH x 4 MFMAs in groups of at
-// most 3 row blocks; a group's lhs fragments are read during the previous
-// group.
+// tile), and MFMA work follows the rows in steps of 16.  In MFMA step v
+// (32 of the K step's 64) lane row q = lane / 16 of the B operand of column
+// block u holds K chunk (h = q / 2, s = 2v + q % 2) of column 16 u + lane %
+// 16: 8 codes that the prepack stores as 4 bytes of the column's slot (slot
+// c + 32 h of half j holds k = 32 h .. + 31, chunk s at byte 4 s), read from
+// LDS and decoded in place (two such dwords per column block and K step, one
+// ds_read2).  The lhs fragment of MFMA step v reads the same K chunk, so the
+// sum over K is the same in another order.  Each K step runs 2 x NH x 4
+// MFMAs in groups of at most 3 row blocks; a group's lhs fragments are read
+// during the previous group.
 template <class C, int NH, bool ACT>
 __device__ __forceinline__ void ws_consumer(int T, uint8_t *s_lds, int cw, int64_t row0, int rows,
                                             int64_t col0, int N, void *__restrict__ out, int out_f32,
@@ -194,15 +195,25 @@ __device__ __forceinline__ void ws_consumer(int T, uint8_t *s_lds, int cw, int64
   const int arow = C::A + (lane & 15) * 128;  // row 16 hb + lane % 16: + 2048 hb
   const int x = lhs_swizzle(lane & 15);       // every row 16 hb + lane % 16 shares it
   const int qk = 4 * (q >> 1) + (q & 1);      // K chunk of MFMA step v: qk + 2 v
-  const int woff = C::W + cw * 2048 + lane * 16;
-  const int soff = C::S + cw * 256 + lane * 4;
+  // The B operand of column block u (columns 16 (u & 1) + c16 of half
+  // j = u >> 1) in lane (c16, q) of MFMA step v: the 8 codes of K chunk
+  // (h = q >> 1, s = 2 v + (q & 1)), i.e. bytes 8 v + 4 (q & 1) .. + 3 of
+  // slot c32 + 32 h of half j; its scale, byte 2 f + j of that slot's dword.
+  const int slot = (lane & 15) + 32 * (q >> 1);
+  const int woff = C::W + cw * 2048 + slot * 16 + 4 * (q & 1);  // + 1024 j + 256 (u & 1) + 8 v
+  const int soff = C::S + cw * 256 + slot * 4;                   // + 64 (u & 1)
   // Next step's weights and scales, and the lhs fragments of the next MFMA group.
-  u32x4_t wn[2], an[3];
-  uint32_t sn;
+  u32x2_t wn[4];
+  u32x4_t an[3];
+  uint32_t sn[2];
   auto read_w = [&](const uint8_t *st) {
-    wn[0] = *(const u32x4_t *)(st + woff);
-    wn[1] = *(const u32x4_t *)(st + woff + 1024);
-    sn = *(const uint32_t *)(st + soff);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const uint32_t *const p = (const uint32_t *)(st + woff + 1024 * (u >> 1) + 256 * (u & 1));
+      wn[u] = u32x2_t{p[0], p[2]};
+    }
+    sn[0] = *(const uint32_t *)(st + soff);
+    sn[1] = *(const uint32_t *)(st + soff + 64);
   };
   auto read_a = [&](const uint8_t *st, int v, int rg) {
     const int ach = ((qk + 2 * v) ^ x) << 4;
@@ -226,14 +237,12 @@ __device__ __forceinline__ void ws_consumer(int T, uint8_t *s_lds, int cw, int64
       read_w(st);
       read_a(st, 0, 0);
     }
-    u32x4_t w[2];
-    float sc[2];
-    w[0] = wn[0];
-    w[1] = wn[1];
-    {
-      const uint32_t sd = sn >> (16 * (t & 1));
-      sc[0] = e8m0_to_f32(sd & 0xFFu);
-      sc[1] = e8m0_to_f32((sd >> 8) & 0xFFu);
+    u32x2_t w[4];
+    float sc[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      w[u] = wn[u];
+      sc[u] = e8m0_to_f32(sn[u & 1] >> (16 * (t & 1) + 8 * (u >> 1)));
     }
 #pragma unroll
     for (int v = 0; v < 2; ++v) {
@@ -250,22 +259,11 @@ __device__ __forceinline__ void ws_consumer(int T, uint8_t *s_lds, int cw, int64
         else read_a(sx, 0, 0);
         if (rg == 0) {
 #pragma unroll
-          for (int j = 0; j < 2; ++j) {
-            u32x4_t e, o;
-            e[0] = cvt_fp4x2_bf16<0>(w[j][2 * v], sc[j]);
-            e[1] = cvt_fp4x2_bf16<1>(w[j][2 * v], sc[j]);
-            e[2] = cvt_fp4x2_bf16<2>(w[j][2 * v], sc[j]);
-            e[3] = cvt_fp4x2_bf16<3>(w[j][2 * v], sc[j]);
-            o[0] = cvt_fp4x2_bf16<0>(w[j][2 * v + 1], sc[j]);
-            o[1] = cvt_fp4x2_bf16<1>(w[j][2 * v + 1], sc[j]);
-            o[2] = cvt_fp4x2_bf16<2>(w[j][2 * v + 1], sc[j]);
-            o[3] = cvt_fp4x2_bf16<3>(w[j][2 * v + 1], sc[j]);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const auto p = __builtin_amdgcn_permlane16_swap(e[i], o[i], false, false);
-              bop[2 * j][i] = p[0];
-              bop[2 * j + 1][i] = p[1];
-            }
+          for (int u = 0; u < 4; ++u) {
+            bop[u][0] = cvt_fp4x2_bf16<0>(w[u][v], sc[u]);
+            bop[u][1] = cvt_fp4x2_bf16<1>(w[u][v], sc[u]);
+            bop[u][2] = cvt_fp4x2_bf16<2>(w[u][v], sc[u]);
+            bop[u][3] = cvt_fp4x2_bf16<3>(w[u][v], sc[u]);
           }
           // the next step's weights, once steps 0 and 1's words are decoded
           if (v == 0) read_w(sx);
