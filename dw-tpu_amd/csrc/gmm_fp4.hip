@@ -237,13 +237,9 @@ __device__ __forceinline__ void ws_consumer(int T, uint8_t *s_lds, int cw, int64
       read_w(st);
       read_a(st, 0, 0);
     }
-    u32x2_t w[4];
     float sc[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      w[u] = wn[u];
-      sc[u] = e8m0_to_f32(sn[u & 1] >> (16 * (t & 1) + 8 * (u >> 1)));
-    }
+    for (int u = 0; u < 4; ++u) sc[u] = e8m0_to_f32(sn[u & 1] >> (16 * (t & 1) + 8 * (u >> 1)));
 #pragma unroll
     for (int v = 0; v < 2; ++v) {
       u32x4_t bop[4];  // B operands of column blocks u = 0 .. 3
@@ -260,13 +256,14 @@ __device__ __forceinline__ void ws_consumer(int T, uint8_t *s_lds, int cw, int64
         if (rg == 0) {
 #pragma unroll
           for (int u = 0; u < 4; ++u) {
-            bop[u][0] = cvt_fp4x2_bf16<0>(w[u][v], sc[u]);
-            bop[u][1] = cvt_fp4x2_bf16<1>(w[u][v], sc[u]);
-            bop[u][2] = cvt_fp4x2_bf16<2>(w[u][v], sc[u]);
-            bop[u][3] = cvt_fp4x2_bf16<3>(w[u][v], sc[u]);
+            bop[u][0] = cvt_fp4x2_bf16<0>(wn[u][v], sc[u]);
+            bop[u][1] = cvt_fp4x2_bf16<1>(wn[u][v], sc[u]);
+            bop[u][2] = cvt_fp4x2_bf16<2>(wn[u][v], sc[u]);
+            bop[u][3] = cvt_fp4x2_bf16<3>(wn[u][v], sc[u]);
           }
-          // the next step's weights, once steps 0 and 1's words are decoded
-          if (v == 0) read_w(sx);
+          // the next step's weights and scales, once this step's are decoded
+          // (the step's remaining MFMA groups cover the reads)
+          if (v == 1) read_w(sx);
         }
 #pragma unroll
         for (int i = 0; i < nb; ++i)
