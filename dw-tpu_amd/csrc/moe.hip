@@ -166,9 +166,10 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_scatter_kernel(
   }
 }
 
-// Small batches (n <= kFusedMax ids): one block of 1024 threads runs all
-// three steps -- the LDS histogram, the scan (wave 0) and the stable scatter
-// in 1024-id steps -- in one launch, with no workspace round trip.
+// Small batches (n <= kFusedMax ids) over 64 or more experts (fewer take
+// dispatch_small_kernel below): one block of 1024 threads runs all three
+// steps -- the LDS histogram, the scan (wave 0) and the stable scatter in
+// 1024-id steps -- in one launch, with no workspace round trip.
 constexpr int kFusedThreads = 1024, kFusedMax = 8192;
 
 __global__ __launch_bounds__(kFusedThreads) void dispatch_fused_kernel(const int32_t *ids, int64_t n, int topk,
@@ -238,6 +239,106 @@ __global__ __launch_bounds__(kFusedThreads) void dispatch_fused_kernel(const int
   }
 }
 
+
+// Small batches over few experts (n <= kFusedMax ids, E + 1 <= 64 keys):
+// the scattered stores, not the ranking, set the time of a one-block
+// dispatch, so the ids are split into portions of 512 over up to 16 blocks.
+// Every block counts all n ids (cheap: 16 waves, one 64-id round each per
+// 1024 ids) by key -- in total and before its portion -- and ranks its own
+// portion; lane e of a wave counts key e from the key bits' ballots, and a
+// lane's rank within a round is the lanes below it holding its key.  An id
+// lands at key offset + ids of its key before the portion + before its round
+// in the portion + its rank in the round: the stable order of j.  Block 0
+// writes the group sizes and offsets.  No atomics and two block barriers.
+constexpr int kSmallMaxKeys = 64, kSmallPortion = 512;
+
+__global__ __launch_bounds__(kFusedThreads) void dispatch_small_kernel(const int32_t *ids, int64_t n, int topk,
+                                                                       int E, int32_t *perm, int32_t *tok_sorted,
+                                                                       int32_t *revert, int32_t *group_sizes,
+                                                                       int32_t *group_offsets, int32_t *flags) {
+  constexpr int W = kFusedThreads / 64, PR = kSmallPortion / 64;     // waves; rounds per portion
+  constexpr int RMAX = kFusedMax / kFusedThreads;                      // rounds per wave
+  static_assert(PR <= W, "a portion's rounds fall on distinct waves");
+  __shared__ int s_tot[W][kSmallMaxKeys], s_bef[W][kSmallMaxKeys];
+  __shared__ int s_rc[PR][kSmallMaxKeys];  // per round of the portion: count of each key
+  __shared__ int s_base[kSmallMaxKeys], s_rp[PR][kSmallMaxKeys];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int NR = (int)((n + 63) >> 6);  // 64-id rounds
+  const int r0 = blockIdx.x * PR;       // the portion's first round
+  int nbits = 0;
+  while ((1 << nbits) <= E) ++nbits;  // keys 0 .. E
+  const uint64_t lt = (1ull << lane) - 1ull;
+  // Round wave + W i; every round's id is loaded before the first is counted.
+  int key[RMAX];
+#pragma unroll
+  for (int i = 0; i < RMAX; ++i) {
+    const int64_t j = (int64_t)(wave + W * i) * 64 + lane;
+    key[i] = j < n ? ids[j] : 0;
+  }
+  int tot = 0, bef = 0, myrank = 0, mykey = 0, myq = -1;  // lane e: key e's counts
+  bool bad = false;
+#pragma unroll
+  for (int i = 0; i < RMAX; ++i) {
+    const int r = wave + W * i;
+    if (r < NR) {
+      const int64_t j = (int64_t)r * 64 + lane;
+      const bool active = j < n;
+      const int k = active ? dispatch_key(key[i], E, &bad) : 0;
+      uint64_t peers = __ballot(active), mine = peers;  // lanes holding my key; holding key `lane`
+      for (int b = 0; b < nbits; ++b) {
+        const uint64_t m = __ballot(active && ((k >> b) & 1));
+        peers &= ((k >> b) & 1) ? m : ~m;
+        mine &= ((lane >> b) & 1) ? m : ~m;
+      }
+      const int c = lane <= E ? __popcll(mine) : 0;
+      tot += c;
+      if (r < r0) bef += c;
+      const int q = r - r0;
+      if (q >= 0 && q < PR) {  // a round of this block's portion (one per wave)
+        if (lane <= E) s_rc[q][lane] = c;
+        myq = q;
+        mykey = k;
+        myrank = __popcll(peers & lt);
+      }
+    }
+  }
+  if (lane <= E) {
+    s_tot[wave][lane] = tot;
+    s_bef[wave][lane] = bef;
+  }
+  if (bad && flags) atomicOr(flags, 1);
+  __syncthreads();
+  if (wave == 0) {
+    int t = 0, bf = 0;
+    for (int w = 0; w < W; ++w) {
+      t += lane <= E ? s_tot[w][lane] : 0;
+      bf += lane <= E ? s_bef[w][lane] : 0;
+    }
+    const int off = wave_inclusive_scan(t) - t;
+    if (lane <= E) {
+      if (blockIdx.x == 0) {
+        if (lane < E) group_sizes[lane] = t;
+        if (group_offsets) group_offsets[lane] = off;  // entry E = number of valid ids
+      }
+      s_base[lane] = off + bf;
+      int run = 0;  // ids of key `lane` in the portion's rounds before q
+      for (int q = 0; q < PR; ++q) {
+        s_rp[q][lane] = run;
+        run += r0 + q < NR ? s_rc[q][lane] : 0;
+      }
+    }
+  }
+  __syncthreads();
+  if (myq >= 0) {
+    const int64_t j = (int64_t)(r0 + myq) * 64 + lane;
+    if (j < n) {
+      const int p = s_base[mykey] + s_rp[myq][mykey] + myrank;
+      perm[p] = (int32_t)j;
+      tok_sorted[p] = (int32_t)(j / topk);
+      revert[j] = p;
+    }
+  }
+}
 
 template <typename V>
 __global__ __launch_bounds__(256) void row_gather_kernel(const char *src, int64_t src_rows,
@@ -402,6 +503,12 @@ static int dispatch_launch(const int32_t *topk_ids, int64_t n, int topk, int num
   if (n == 0) {
     hipLaunchKernelGGL(dispatch_scan_kernel, dim3(1), dim3(1024), 0, st, counts, 0, num_experts,
                        group_sizes, group_offsets);
+    return launch_status("moe_dispatch");
+  }
+  if (n <= kFusedMax && num_experts < kSmallMaxKeys) {
+    const unsigned blocks = (unsigned)((n + kSmallPortion - 1) / kSmallPortion);
+    hipLaunchKernelGGL(dispatch_small_kernel, dim3(blocks), dim3(kFusedThreads), 0, st, topk_ids, n, topk,
+                       num_experts, perm, tok_sorted, revert, group_sizes, group_offsets, flags);
     return launch_status("moe_dispatch");
   }
   if (n <= kFusedMax) {

@@ -17,15 +17,18 @@ def _dispatch(dev, ids, E, check=False):
     return [t.cpu().numpy() for t in d]
 
 
-# Batches of up to 8192 ids take the one-block kernel, larger ones the
-# three-launch path: both sides of that boundary are covered.  In the
+# Batches of up to 8192 ids take a one-block kernel (with at most 63
+# experts the register-count kernel, E = 63 and a ragged last round here;
+# with more the LDS-histogram one, E = 64 here), larger ones the
+# three-launch path: both sides of each boundary are covered.  In the
 # three-launch path the scan splits the chunk counters into runs per expert
 # column (E + 1 <= 512 columns: 2 .. 1024 runs), or walks whole columns
 # (E = 1024: more columns than the scan's threads).
 @pytest.mark.parametrize("T,topk,E", [(1, 1, 1), (3, 2, 8), (64, 2, 8), (256, 8, 32), (512, 8, 32),
                                       (1000, 6, 256), (8192, 8, 32), (130, 8, 1024), (4096, 1, 3),
                                       (1024, 8, 1024), (8192, 1, 5), (8193, 1, 7), (2731, 3, 64),
-                                      (2048, 8, 1024), (16384, 8, 256), (65536, 8, 32), (9000, 1, 1)])
+                                      (2048, 8, 1024), (16384, 8, 256), (65536, 8, 32), (9000, 1, 1),
+                                      (1000, 5, 63), (700, 8, 64), (1, 7, 2), (8191, 1, 1)])
 def test_dispatch_bit_exact(dev, rng, T, topk, E):
     ids = rng.integers(0, E, (T, topk)).astype(np.int32)
     got = _dispatch(dev, ids, E)
