@@ -239,7 +239,8 @@ __device__ __forceinline__ void ws_consumer(int T, uint8_t *s_lds, int cw, int64
     }
     float sc[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) sc[u] = e8m0_to_f32(sn[u & 1] >> (16 * (t & 1) + 8 * (u >> 1)));
+    for (int u = 0; u < 4; ++u)
+      sc[u] = __builtin_bit_cast(float, __builtin_amdgcn_ubfe(sn[u & 1], 16 * (t & 1) + 8 * (u >> 1), 8) << 23);
 #pragma unroll
     for (int v = 0; v < 2; ++v) {
       u32x4_t bop[4];  // B operands of column blocks u = 0 .. 3
