@@ -221,8 +221,14 @@ __device__ __forceinline__ void ws_consumer(int T, uint8_t *s_lds, int cw, int64
 #pragma unroll
     for (int i = 0; i < nb; ++i) an[i] = *(const u32x4_t *)(st + arow + (3 * rg + i) * 2048 + ach);
   };
-  int cur = 0;  // stage of step t
-  for (int t = 0; t < T; ++t) {
+  // Steps in runs of NS, one per stage, so that every stage address is a
+  // constant offset (cur = t % NS is known in each copy of the body).
+  static_assert(NS % 2 == 0, "t & 1 == cur & 1");
+  for (int t0 = 0; t0 < T; t0 += NS) {
+#pragma unroll
+  for (int cur = 0; cur < NS; ++cur) {
+    const int t = t0 + cur;
+    if (t >= T) break;
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
     __builtin_amdgcn_s_barrier();
@@ -240,7 +246,7 @@ __device__ __forceinline__ void ws_consumer(int T, uint8_t *s_lds, int cw, int64
     float sc[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u)
-      sc[u] = __builtin_bit_cast(float, __builtin_amdgcn_ubfe(sn[u & 1], 16 * (t & 1) + 8 * (u >> 1), 8) << 23);
+      sc[u] = __builtin_bit_cast(float, __builtin_amdgcn_ubfe(sn[u & 1], 16 * (cur & 1) + 8 * (u >> 1), 8) << 23);
 #pragma unroll
     for (int v = 0; v < 2; ++v) {
       u32x4_t bop[4];  // B operands of column blocks u = 0 .. 3
@@ -275,7 +281,7 @@ __device__ __forceinline__ void ws_consumer(int T, uint8_t *s_lds, int cw, int64
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    cur = nxt;
+  }
   }
   // One more barrier: every wave is done with the stages and every load has
   // landed, so each consumer stages its results in a private LDS region and
