@@ -277,8 +277,13 @@ __device__ __forceinline__ void mx_consumer(int T, uint8_t *s_lds, int cw, int c
   uint32_t sw_cur = 0, sa_cur[AM];
 #pragma unroll
   for (int mb = 0; mb < AM; ++mb) sa_cur[mb] = 0;
-  int cur = 0;
-  for (int t = 0; t < T; ++t) {
+  // Steps in runs of NS, one per stage, so that every stage address is a
+  // constant offset (cur = t % NS is known in each copy of the body).
+  for (int t0 = 0; t0 < T; t0 += NS) {
+#pragma unroll
+  for (int cur = 0; cur < NS; ++cur) {
+    const int t = t0 + cur;
+    if (t >= T) break;
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
     __builtin_amdgcn_s_barrier();
@@ -323,7 +328,7 @@ __device__ __forceinline__ void mx_consumer(int T, uint8_t *s_lds, int cw, int c
       acc[mb][1] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b1, acc[mb][1], 0, 4, 0, sa, 1, sb);
       __builtin_amdgcn_sched_barrier(0);
     }
-    cur = nxt;
+  }
   }
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
@@ -542,8 +547,12 @@ __device__ __forceinline__ void mx128_consumer(int T, uint8_t *s_lds, int cw, in
     const u32x4_t hi = *(const u32x4_t *)(st + arow + mb * 32 * 128 + (((4 * f + 2 + h) ^ sw) << 4));
     an = i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
   };
-  int cur = 0;
-  for (int t = 0; t < T; ++t) {
+  // Steps in runs of NS, one per stage, so that every stage address is a
+  // constant offset (cur = t % NS is known in each copy of the body).
+  for (int t0 = 0; t0 < T; t0 += NS) {
+#pragma unroll
+  for (int cur = 0; cur < NS; ++cur) {
+    if (t0 + cur >= T) break;
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
     __builtin_amdgcn_s_barrier();
@@ -578,7 +587,7 @@ __device__ __forceinline__ void mx128_consumer(int T, uint8_t *s_lds, int cw, in
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    cur = cur == NS - 1 ? 0 : cur + 1;
+  }
   }
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
