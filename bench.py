@@ -9,9 +9,11 @@ resident in HBM before the timed region; the weight set is rotated over
 copies larger than the 256 MB Infinity Cache so the stream comes from HBM.
 
 `value` is algorithmic HBM GB/s (non-empty experts' packed weights + scales,
-lhs once, output once) divided by the average step time measured with HIP
-events on the stream the kernels run on.  The headline runs the reference's
-W4A16 arithmetic (bf16 lhs, exactly decoded fp4 weights, bf16 MFMA).
+lhs once, output once) divided by the step time measured with HIP events on
+the stream the kernels run on: the median of 9 samples of --steps
+back-to-back launches (the gmm and dense lines in `extra`: of 3).  The
+headline runs the reference's W4A16 arithmetic (bf16 lhs, exactly decoded
+fp4 weights, bf16 MFMA).
 `extra` reports the other workloads (decode down-projection with dispatch /
 combine, prefill) the same way, each gmm workload again in the MX mode
 (`<name>_mx`: e4m3 lhs with e8m0 block-32 scales on the scaled MFMA, a
@@ -52,6 +54,7 @@ FP8_PEAK_TFLOPS = 5000.0
 ONLY_CHOICES = ("decode_gate_up", "decode_down", "prefill", "decode_gate_up_mx", "decode_down_mx", "prefill_mx",
                 "dense_M1", "dense_M16", "dense_M128", "dense_M1024", "dense_M4096")
 MALL_BYTES = 256 * 2 ** 20
+HEADLINE_SAMPLES = 9  # timed samples of the headline; value is their median
 
 
 def log(*a):
@@ -136,6 +139,13 @@ def time_steps(step, steps, warmup):
     return start.elapsed_time(end) / steps
 
 
+def time_median(step, steps, warmup, n=3):
+    """Median over n samples of time_steps (the first after `warmup` untimed
+    launches, the others straight after it)."""
+    s = sorted([time_steps(step, steps, warmup)] + [time_steps(step, steps, 0) for _ in range(n - 1)])
+    return s[len(s) // 2]
+
+
 def gmm_result(wl, ms, mode="bf16"):
     """Throughput of one gmm launch.  Algorithmic bytes: the non-empty
     experts' packed weights and e8m0 scales, the lhs once (bf16, or e4m3
@@ -176,7 +186,7 @@ def prep_gmm(name, dev, steps, warmup):
     b = GmmBench(wl, dev, copies_for(wl))
 
     def run():
-        return {name: gmm_result(wl, time_steps(b.step, steps, warmup))}
+        return {name: gmm_result(wl, time_median(b.step, steps, warmup))}
     return run
 
 
@@ -189,7 +199,7 @@ def prep_gmm_mx(name, dev, steps, warmup):
     b = GmmBench(wl, dev, copies_for(wl), "mx")
 
     def run():
-        r = gmm_result(wl, time_steps(b.step, steps, warmup), "mx")
+        r = gmm_result(wl, time_median(b.step, steps, warmup), "mx")
         q_ms = time_steps(b.quant_step, steps, warmup)
         qb = wl.M * wl.K * 2 + wl.M * wl.K + wl.M * wl.K // 32
         r["quant"] = {"ms": round(q_ms, 5), "GB_s": round(qb / (q_ms * 1e-3) / 1e9, 1),
@@ -503,7 +513,7 @@ def prep_dense(dev, steps, warmup, ms_list=(1, 16, 128, 1024, 4096)):
             fl = 2 * m * k * n
             for tag, fn, xbytes in (("w8a16", run16, m * k * 2 + (k // 128) * n * 4),
                                     ("w8a8", run8, m * k + m * (k // 128) * 4 + (k // 128) * (n // 128) * 4)):
-                ms = time_steps(fn, steps, warmup)
+                ms = time_median(fn, steps, warmup)
                 bts = k * n + xbytes + m * n * 2
                 gbs = bts / (ms * 1e-3) / 1e9
                 tf = fl / (ms * 1e-3) / 1e12
@@ -792,10 +802,14 @@ def main():
     else:
         runs = []
     log("bench: decode_gate_up gmm (headline)")
-    ms = time_steps(b.step, args.steps, args.warmup)
+    # HEADLINE_SAMPLES samples of --steps back-to-back launches, the first
+    # after --warmup untimed ones; value and ms_per_step are their median (a
+    # single sample has erred by 10-15% either way against the sustained
+    # rate), the first sample and the spread are kept in config.
+    first = time_steps(b.step, args.steps, args.warmup)
+    samples = sorted([first] + [time_steps(b.step, args.steps, 0) for _ in range(HEADLINE_SAMPLES - 1)])
+    ms = samples[len(samples) // 2]
     main_res = gmm_result(wl, ms)
-    # Spread: 7 more samples of the same K steps, right after the timed ones.
-    samples = sorted(time_steps(b.step, args.steps, 0) for _ in range(7))
     e_chk = int(np.flatnonzero(wl.group_sizes > 0)[0])
     r0 = int(wl.group_sizes[:e_chk].sum())
     gpu_check = (e_chk, b.out[0][r0:r0 + int(wl.group_sizes[e_chk])].float().cpu().numpy())
@@ -828,8 +842,8 @@ def main():
                                "experts), K=7168, N=4096, fp4 e2m1 weights with e8m0 block-32 scales, bf16 out",
                    "TFLOP_s": main_res["TFLOP_s"], "mfma_bf16_frac": main_res["mfma_bf16_frac"],
                    "bytes_per_step": main_res["bytes"], "flops_per_step": main_res["flops"],
-                   "ms_per_step_7_samples": {"median": round(samples[3], 5), "min": round(samples[0], 5),
-                                             "max": round(samples[-1], 5)}},
+                   "ms_per_step_samples": {"n": len(samples), "statistic": "median", "first": round(first, 5),
+                                           "min": round(samples[0], 5), "max": round(samples[-1], 5)}},
         "roofline": {"bound": "hbm", "achieved": main_res["GB_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": main_res["hbm_frac"], "traffic": profiled_traffic()},
         "cpu_baseline": cpu,

@@ -68,8 +68,22 @@ __global__ void dense_fp8_prepack_kernel(const uint8_t *w, int64_t K, int64_t N,
   dst[1] = u32x4_t{words[4], words[5], words[6], words[7]};
 }
 
+// A packed pair of bf16 values, each multiplied by `s` (a bf16 value held
+// in f32) and rounded to bf16 (round to nearest even): the bf16 x bf16
+// product of the reference's "pre" mode (dense_fp8.py:39-43).  The f32
+// product of two bf16 values is exact, so this is the correctly rounded
+// bf16 product.
+__device__ __forceinline__ uint32_t scale_bf16x2(uint32_t v, float s) {
+  const float lo = bf16_bits_to_f32(v & 0xFFFFu) * s;
+  const float hi = __builtin_bit_cast(float, v & 0xFFFF0000u) * s;
+  return (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
+}
+
 // A8: activations are e4m3 codes with scales sx [M, K/128]; else bf16.
-template <int MB, int NBW, bool A8>
+// PRE (W8A16 only): the reference's "pre" rounding -- every weight times the
+// bf16-rounded scale of its (K block, column), rounded to bf16, feeds the
+// MFMA, and the partials are summed with no scale after the dot.
+template <int MB, int NBW, bool A8, bool PRE = false>
 __global__ __launch_bounds__(kDenseThreads) void dense_fp8_kernel(
     const void *__restrict__ xin, const float *__restrict__ sx, int64_t M, int K, int N,
     const uint8_t *__restrict__ wpk, const float *__restrict__ sw, int sw_ld, int ksplit,
@@ -171,6 +185,15 @@ __global__ __launch_bounds__(kDenseThreads) void dense_fp8_kernel(
 #pragma unroll
       for (int j = 0; j < NBW; ++j) part[mb][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     const uint16_t *abase = &s_a[buf][arow * kDLdsRow + acol];
+    // PRE: the bf16-rounded scale of each of the lane's weight columns.
+    float pscale[NBW];
+    if constexpr (PRE) {
+#pragma unroll
+      for (int j = 0; j < NBW; ++j) {
+        const int64_t col = (int64_t)(nvalid[j] ? nb0 + j : 0) * 16 + (lane & 15);
+        pscale[j] = bf16_bits_to_f32(f32_to_bf16_bits(sw[(int64_t)kb * sw_ld + col]));
+      }
+    }
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       u32x4_t bfrag[NBW];
@@ -183,6 +206,10 @@ __global__ __launch_bounds__(kDenseThreads) void dense_fp8_kernel(
         bfrag[j][1] = cvt_fp8x2_bf16<true>(w0);
         bfrag[j][2] = cvt_fp8x2_bf16<false>(w1);
         bfrag[j][3] = cvt_fp8x2_bf16<true>(w1);
+        if constexpr (PRE) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) bfrag[j][i] = scale_bf16x2(bfrag[j][i], pscale[j]);
+        }
       }
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) {
@@ -195,11 +222,11 @@ __global__ __launch_bounds__(kDenseThreads) void dense_fp8_kernel(
         }
       }
     }
-    // acc += part * scale (f32 multiply, then f32 add)
+    // acc += part * scale (f32 multiply, then f32 add); PRE: acc += part
 #pragma unroll
     for (int j = 0; j < NBW; ++j) {
       const int64_t col = (int64_t)(nvalid[j] ? nb0 + j : 0) * 16 + (lane & 15);
-      const float wscale = A8 ? sw[(int64_t)kb * sw_ld + (col >> 7)] : sw[(int64_t)kb * sw_ld + col];
+      const float wscale = PRE ? 1.0f : (A8 ? sw[(int64_t)kb * sw_ld + (col >> 7)] : sw[(int64_t)kb * sw_ld + col]);
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) {
         if (mb < act_mb) {
@@ -894,13 +921,32 @@ static void launch_mfma(const void *x, const float *sx, int64_t M, int64_t K, in
                      w, sw, sw_ld, ks, out, partial);
 }
 
-template <int MB, int NBW, bool A8>
+template <int MB, int NBW, bool A8, bool PRE = false>
 static void launch_tiled(const void *x, const float *sx, int64_t M, int64_t K, int64_t N, const uint8_t *w,
                          const float *sw, int sw_ld, int ksplit, uint16_t *out, float *partial, hipStream_t st) {
   const int64_t NT = 64 * NBW, MT = 16 * MB;
   dim3 grid((unsigned)((N + NT - 1) / NT), (unsigned)((M + MT - 1) / MT), (unsigned)ksplit);
-  hipLaunchKernelGGL((dense_fp8_kernel<MB, NBW, A8>), grid, dim3(kDenseThreads), 0, st, x, sx, M, (int)K, (int)N,
-                     w, sw, sw_ld, ksplit, out, partial);
+  hipLaunchKernelGGL((dense_fp8_kernel<MB, NBW, A8, PRE>), grid, dim3(kDenseThreads), 0, st, x, sx, M, (int)K,
+                     (int)N, w, sw, sw_ld, ksplit, out, partial);
+}
+
+// The f32 partials [ks][M][N] summed in run order and rounded once.
+static int launch_reduce(const float *partial, int ks, int64_t MN, uint16_t *out, hipStream_t st) {
+  if ((((uintptr_t)partial | (uintptr_t)out) & 15) == 0) {
+    const int64_t blocks = (MN / 4 + 255) / 256 < 4096 ? (MN / 4 + 255) / 256 : 4096;
+    hipLaunchKernelGGL(dense_fp8_reduce4_kernel, dim3((unsigned)blocks), dim3(256), 0, st, partial, ks, MN, out);
+  } else {
+    const int64_t blocks = (MN + 255) / 256 < 4096 ? (MN + 255) / 256 : 4096;
+    hipLaunchKernelGGL(dense_fp8_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, st, partial, ks, MN, out);
+  }
+  return launch_status("dense_fp8 reduce");
+}
+
+// The "pre" rounding runs on the tiled kernel with its own plan for the shape.
+static dwm_dense_plan pre_plan(int64_t M, int64_t K, int64_t N) {
+  dwm_dense_plan p = tiled_default(M, K, N);
+  p.ksplit = whole_runs(K / 128, p.ksplit);
+  return p;
 }
 
 // Runs one dense GEMM with `plan` (NULL: the default plan).
@@ -940,15 +986,7 @@ static int run_dense(const void *x, const float *sx, int64_t M, int64_t K, int64
   if (rc != DWM_OK) return rc;
   t_last_plan = p;
   if (!partial) return DWM_OK;
-  const int64_t MN = M * N;
-  if ((((uintptr_t)partial | (uintptr_t)out) & 15) == 0) {
-    const int64_t blocks = (MN / 4 + 255) / 256 < 4096 ? (MN / 4 + 255) / 256 : 4096;
-    hipLaunchKernelGGL(dense_fp8_reduce4_kernel, dim3((unsigned)blocks), dim3(256), 0, st, partial, ks, MN, out);
-  } else {
-    const int64_t blocks = (MN + 255) / 256 < 4096 ? (MN + 255) / 256 : 4096;
-    hipLaunchKernelGGL(dense_fp8_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, st, partial, ks, MN, out);
-  }
-  return launch_status("dense_fp8 reduce");
+  return launch_reduce(partial, ks, M * N, out, st);
 }
 
 static int check_dense(int64_t M, int64_t K, int64_t N) {
@@ -1020,6 +1058,7 @@ extern "C" int dwm_dense_fp8_workspace_size(int64_t M, int64_t K, int64_t N, int
   // the larger of the W8A16 and W8A8 default plans' needs
   int64_t b = plan_workspace(M, N, default_plan(m, K, N, false));
   if (N % 128 == 0) b = max(b, plan_workspace(M, N, default_plan(m, K, N, true)));
+  b = max(b, plan_workspace(M, N, pre_plan(m, K, N)));
   *bytes = b;
   return DWM_OK;
 }
@@ -1060,4 +1099,32 @@ extern "C" int dwm_dense_fp8_w8a8(const uint8_t *xq, const float *sx, int64_t M,
                                   const uint8_t *w, const float *sw, uint16_t *out, void *workspace,
                                   int64_t workspace_bytes, void *stream) {
   return dwm_dense_fp8_w8a8_plan(xq, sx, M, K, N, w, sw, out, nullptr, workspace, workspace_bytes, stream);
+}
+
+extern "C" int dwm_dense_fp8_w8a16_pre(const uint16_t *x, int64_t M, int64_t K, int64_t N, const uint8_t *w,
+                                       const float *s, uint16_t *out, void *workspace, int64_t workspace_bytes,
+                                       void *stream) {
+  clear_error();
+  int rc = check_dense(M, K, N);
+  if (rc != DWM_OK) return rc;
+  if (M == 0) return DWM_OK;
+  DWM_CHECK_ARG(x && w && s && out, "dense_fp8_w8a16_pre: null pointer");
+  DWM_CHECK_ARG((uintptr_t)x % 16 == 0 && (uintptr_t)w % 16 == 0,
+                "dense_fp8_w8a16_pre: x and w must be 16-byte aligned");
+  const dwm_dense_plan p = pre_plan(M, K, N);
+  DWM_UNSUPPORTED_IF((M + p.tile_m - 1) / p.tile_m > 65535, "dense_fp8_w8a16_pre: M too large");
+  const int64_t need = plan_workspace(M, N, p);
+  DWM_CHECK_ARG(need == 0 || (workspace && workspace_bytes >= need),
+                "dense_fp8_w8a16_pre: workspace of %lld bytes needed", (long long)need);
+  float *const partial = need ? (float *)workspace : nullptr;
+  hipStream_t st = as_stream(stream);
+  const int ks = p.ksplit;
+  if (p.tile_m == 16) launch_tiled<1, 1, false, true>(x, nullptr, M, K, N, w, s, (int)N, ks, out, partial, st);
+  else if (p.tile_m == 64) launch_tiled<4, 2, false, true>(x, nullptr, M, K, N, w, s, (int)N, ks, out, partial, st);
+  else launch_tiled<8, 2, false, true>(x, nullptr, M, K, N, w, s, (int)N, ks, out, partial, st);
+  rc = launch_status("dense_fp8_w8a16_pre");
+  if (rc != DWM_OK) return rc;
+  t_last_plan = p;
+  if (!partial) return DWM_OK;
+  return launch_reduce(partial, ks, M * N, out, st);
 }

@@ -609,8 +609,14 @@ extern "C" int dwm_moe_dispatch_noalloc(const int32_t *topk_ids, int64_t T, int 
                      "moe_dispatch_noalloc: %lld ids over %d experts need %lld counter words, more than the "
                      "%lld of its static scratch (use dwm_moe_dispatch with a workspace)",
                      (long long)n, num_experts, (long long)words, (long long)kNoAllocWords);
-  int32_t *counts = device_scratch();
-  if (!counts) return DWM_ERR_HIP;
+  // Only the three-launch path (n > kFusedMax) uses the counters: smaller
+  // batches never look the array up, so their first call on a device does
+  // no runtime lookup (e.g. inside a stream capture).
+  int32_t *counts = nullptr;
+  if (n > kFusedMax) {
+    counts = device_scratch();
+    if (!counts) return DWM_ERR_HIP;
+  }
   return dispatch_launch(topk_ids, n, topk, num_experts, perm, tok_sorted, revert, group_sizes, group_offsets,
                          flags, counts, as_stream(stream));
 }

@@ -54,6 +54,7 @@ SIGNATURES = {
     "dwm_dense_fp8_workspace_size": [_i64, _i64, _i64, _p],
     "dwm_dense_fp8_w8a16": [_p, _i64, _i64, _i64, _p, _p, _p, _p, _i64, _p],
     "dwm_dense_fp8_w8a8": [_p, _p, _i64, _i64, _i64, _p, _p, _p, _p, _i64, _p],
+    "dwm_dense_fp8_w8a16_pre": [_p, _i64, _i64, _i64, _p, _p, _p, _p, _i64, _p],
     "dwm_dense_fp8_plan": [_i64, _i64, _i64, _i32, _p],
     "dwm_dense_fp8_plan_check": [_i64, _i64, _i64, _i32, _p],
     "dwm_dense_fp8_plan_workspace_size": [_i64, _i64, _i64, _p, _p],

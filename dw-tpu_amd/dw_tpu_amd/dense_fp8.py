@@ -14,8 +14,12 @@ weight tensors are prepacked on every call (one extra pass over the weight).
 Tiles: ``select_tile`` returns the ``(mode, tm, tk, tn)`` of the launch the
 library will make (``dense_fp8_tiles`` maps it to and from the C plan), and
 ``matmul`` passes a given tile through to the kernel.
+
+Modes: "native", "wide", "flipped" and "megablox" are one arithmetic on
+MI355X; "pre" (``matmul_pre``) is the reference's other rounding.
 """
 import ctypes
+import warnings
 from dataclasses import dataclass
 
 import torch
@@ -72,18 +76,36 @@ def _aligned(t):
     return t.clone() if t.data_ptr() % 16 else t
 
 
+# Modes of the reference's matmul that compute the "native" arithmetic
+# (a per-128-K-block f32 dot, scaled in f32 after the dot) and differ only in
+# how the TPU schedules it (dense_fp8.py:1-5, 33-53): "wide" widens the
+# weight tile to bf16 first (exact for e4m3), "flipped" computes the dot as
+# (w^T x^T)^T.  Here they take the native launches.
+SAME_MATH_MODES = {"native": "native", "wide": "native", "flipped": "native", "megablox": "megablox"}
+
+
 def matmul(x, w, s, *, tn=None, tk=None, tm=None, mode="native", stages=0):
     """W8A16 dense GEMM: x [M, K] bf16, w [K, N] e4m3 (or ``Fp8Weight``),
     s [K/128, 1, N] f32 -> bf16 [M, N].
 
+    mode "native", "wide", "flipped" and "megablox" are the same arithmetic
+    (f32 dot per 128-deep K block, times the f32 scale, f32 accumulation);
+    "pre" (the reference's other rounding: each weight times its bf16 scale,
+    rounded to bf16, before one f32 dot) is ``matmul_pre``.
+
     With tm, tk and tn left unset the library launches its own plan.  Given,
     they name a launch (``dense_fp8_tiles``: mode "native" = the skinny or
     MFMA kernel, "megablox" = the general tiled kernel; tk = the K depth per
-    block; ``stages`` = ring depth) and a tile the library has no kernel for
-    raises ValueError.  The reference's "pre" mode (weights scaled in bf16
-    before the dot) is a different rounding and is not provided."""
-    if mode not in ("native", "megablox"):
+    block; ``stages`` = ring depth).  A tile that names no launch of this
+    library (the reference's TPU tiles, e.g. its defaults tm=16, tk=1024,
+    tn=1024) gets the library's own plan and a ``UserWarning``: tiles change
+    the schedule, never the result.  (An override file that names such a
+    tile is rejected when it is read.)"""
+    if mode == "pre":
+        return matmul_pre(x, w, s)
+    if mode not in SAME_MATH_MODES:
         raise NotImplementedError(f"dense_fp8 mode {mode!r} is not supported")
+    mode = SAME_MATH_MODES[mode]
     pw = prepack_fp8(w)
     m, k = x.shape
     n = pw.n
@@ -93,10 +115,39 @@ def matmul(x, w, s, *, tn=None, tk=None, tm=None, mode="native", stages=0):
     sc = s.reshape(k // 128, n).to(torch.float32).contiguous()
     dev = _lib.require_cuda(x, pw.weight, sc)
     tile = None if (tm, tk, tn) == (None, None, None) else DenseTile(mode, tm, tk, tn, stages)
-    plan, ws, wsb = _plan_and_workspace(m, k, n, dev, tile, False)
+    try:
+        plan, ws, wsb = _plan_and_workspace(m, k, n, dev, tile, False)
+    except ValueError as exc:
+        warnings.warn(f"dense_fp8.matmul: tile {tuple(tile)!r} names no launch of this library ({exc}); "
+                      f"using the library's own plan", stacklevel=2)
+        plan, ws, wsb = _plan_and_workspace(m, k, n, dev, None, False)
     out = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
     _lib.call("dwm_dense_fp8_w8a16_plan", _lib.ptr(x), m, k, n, _lib.ptr(pw.weight), _lib.ptr(sc), _lib.ptr(out),
               plan, _lib.ptr(ws), wsb, _lib.stream_handle(dev))
+    return out
+
+
+def matmul_pre(x, w, s):
+    """The reference's "pre" mode of the W8A16 GEMM (dense_fp8.py:33-43):
+    every e4m3 weight times the bf16-rounded scale of its (128-deep K block,
+    column), rounded to bf16 before one f32 dot over K; nothing is scaled
+    after the dot.  x [M, K] bf16, w [K, N] e4m3 (or ``Fp8Weight``),
+    s [K/128, 1, N] f32 -> bf16 [M, N].  A different rounding from the other
+    modes; it runs the general tiled kernel with its own plan."""
+    pw = prepack_fp8(w)
+    m, k = x.shape
+    n = pw.n
+    if k != pw.k:
+        raise ValueError(f"x K={k} does not match weight K={pw.k}")
+    x = _aligned(x)
+    sc = s.reshape(k // 128, n).to(torch.float32).contiguous()
+    dev = _lib.require_cuda(x, pw.weight, sc)
+    b = ctypes.c_int64(0)
+    _lib.call("dwm_dense_fp8_workspace_size", m, k, n, ctypes.byref(b))
+    ws = None if b.value == 0 else torch.empty(b.value, dtype=torch.uint8, device=dev)
+    out = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+    _lib.call("dwm_dense_fp8_w8a16_pre", _lib.ptr(x), m, k, n, _lib.ptr(pw.weight), _lib.ptr(sc), _lib.ptr(out),
+              _lib.ptr(ws), b.value, _lib.stream_handle(dev))
     return out
 
 

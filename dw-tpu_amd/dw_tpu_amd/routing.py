@@ -40,7 +40,8 @@ def fused_moe_fp4_routing(gating_output: torch.Tensor, top_k: int, renormalize: 
     (0901-...:671-675): it comes after hash routing and before the
     correction bias, so a bias in ``extra`` is popped but not applied.  The
     exact top-k of the scores is returned; it meets every ``recall_target``
-    (default MOE_APPROX_TOPK_RECALL_TARGET, else 0.95; accepted in (0, 1]).
+    (default MOE_APPROX_TOPK_RECALL_TARGET, else 0.95; accepted in (0, 1]),
+    which is read and checked only when that branch is taken.
     """
     extra = {} if extra is None else extra
     hash_ids = extra.pop("hash_based_topk_indices", None)
@@ -48,11 +49,13 @@ def fused_moe_fp4_routing(gating_output: torch.Tensor, top_k: int, renormalize: 
     num_valid = extra.pop("num_valid_tokens", None)
     if approx_topk is None:
         approx_topk = _env_flag("MOE_APPROX_TOPK")
-    if recall_target is None:
-        recall_target = float(os.environ.get("MOE_APPROX_TOPK_RECALL_TARGET", "0.95"))
-    if not 0.0 < recall_target <= 1.0:
-        raise ValueError(f"recall_target must be in (0, 1], got {recall_target}")
     if approx_topk and hash_ids is None:
+        # The recall target is read only in the approx_max_k branch, as in
+        # the reference: a malformed value cannot affect the exact path.
+        if recall_target is None:
+            recall_target = float(os.environ.get("MOE_APPROX_TOPK_RECALL_TARGET", "0.95"))
+        if not 0.0 < recall_target <= 1.0:
+            raise ValueError(f"recall_target must be in (0, 1], got {recall_target}")
         bias = None  # the approx_max_k branch ranks the unbiased scores
     _lib.require_cuda(gating_output)
     if gating_output.dim() != 2:

@@ -232,7 +232,13 @@ int dwm_mx_quant_e4m3(const uint16_t *x, int64_t rows, int64_t K, uint8_t *codes
  * the grouped operand is row r of lhs, or row row_idx[r] (JAX gather
  * semantics) when row_idx is not NULL (then lhs_rows may differ from M).
  * Other arguments and rules as dwm_gmm_fp4; lhs_rows * K < 2^32; lhs_scale
- * 4-byte aligned.  Replaces gmm_v2(..., lhs_quant_dtype=float8_e4m3fn). */
+ * 4-byte aligned.  Stands in for gmm_v2(..., lhs_quant_dtype=float8_e4m3fn)
+ * (patches/tokamax/0001-gmm_v2-fp4-emulation-v6e.patch:89-99): the MX
+ * quantization (block 32, power-of-two e8m0 scales, dwm_mx_quant_e4m3) is
+ * this library's choice, the reference's checkpoint quantizer
+ * quantize_tensor(e4m3, x, -1, 32, power_of_two_scale=True); tokamax's own
+ * online lhs quantizer is not vendored, so parity with that path is
+ * unpinned.  The result is held to this library's stated MX bound. */
 int dwm_gmm_fp4_mx(const uint8_t *lhs, const uint8_t *lhs_scale, int64_t lhs_rows, const int32_t *row_idx,
                    int64_t M, int64_t K, const uint8_t *weight, const uint8_t *scale,
                    const int32_t *group_sizes, int num_groups, const int32_t *group_offset, int64_t E_local,
@@ -267,7 +273,11 @@ int dwm_moe_dispatch(const int32_t *topk_ids, int64_t T, int topk, int num_exper
  * 4,177,920 at 256 experts); larger requests return DWM_ERR_UNSUPPORTED
  * before any device work.  Every call on a GPU uses that GPU's one array:
  * calls that overlap on one GPU (on different streams) race and must not be
- * issued.  Results are bit-identical to dwm_moe_dispatch's. */
+ * issued.  Results are bit-identical to dwm_moe_dispatch's.  The array's
+ * address on a device is looked up (hipGetSymbolAddress) by the first call
+ * there with more than 8192 ids; batches of at most 8192 ids never use it.
+ * A caller that captures a larger batch into a HIP graph makes one such
+ * call on that device before the capture. */
 int dwm_moe_dispatch_noalloc(const int32_t *topk_ids, int64_t T, int topk, int num_experts, int32_t *perm,
                              int32_t *tok_sorted, int32_t *revert, int32_t *group_sizes, int32_t *group_offsets,
                              int32_t *flags, void *stream);
@@ -301,8 +311,9 @@ int dwm_moe_combine(const void *x, int x_dtype, int64_t x_rows, int64_t H, const
  * Requires K % 128 == 0, N % 16 == 0; out holds K*N bytes. */
 int dwm_dense_fp8_prepack(const uint8_t *w, int64_t K, int64_t N, uint8_t *out, void *stream);
 
-/* Workspace bytes the next two entry points need for M x K x N (split-K
- * partials for small M; 0 when none). */
+/* Workspace bytes the W8A16, W8A8 and "pre" entry points below need for
+ * M x K x N with their default plans (split-K partials for small M; 0 when
+ * none). */
 int dwm_dense_fp8_workspace_size(int64_t M, int64_t K, int64_t N, int64_t *bytes);
 
 /* W8A16: out[M, N] bf16 = sum over 128-row K blocks kb of
@@ -314,6 +325,18 @@ int dwm_dense_fp8_workspace_size(int64_t M, int64_t K, int64_t N, int64_t *bytes
 int dwm_dense_fp8_w8a16(const uint16_t *x, int64_t M, int64_t K, int64_t N, const uint8_t *w,
                         const float *s, uint16_t *out, void *workspace, int64_t workspace_bytes,
                         void *stream);
+
+/* The reference's "pre" rounding of the W8A16 GEMM: out[M, N] bf16 =
+ * sum_k x[m, k] * bf16(w[k, n] * bf16(s[k/128, n])), f32 accumulation: every
+ * weight is multiplied by its bf16-rounded scale and rounded to bf16 (round
+ * to nearest even) before the dot, and nothing is scaled after it.  Replaces
+ * dense_fp8.matmul(..., mode='pre')
+ * (kernels/tpu_inference/kernels/experimental/dense_fp8.py:33-43).  Same
+ * arguments as dwm_dense_fp8_w8a16; it runs the general tiled kernel
+ * (DWM_DENSE_TILED) with that kernel's default plan for the shape. */
+int dwm_dense_fp8_w8a16_pre(const uint16_t *x, int64_t M, int64_t K, int64_t N, const uint8_t *w,
+                            const float *s, uint16_t *out, void *workspace, int64_t workspace_bytes,
+                            void *stream);
 
 /* W8A8 block variant: out[m, n] = sum_kb sx[m, kb] * sw[kb, n/128] *
  * dot(xq[m, kb], wq[kb, n]), bf16 output.  No reference kernel (the

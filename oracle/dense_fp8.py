@@ -5,6 +5,9 @@ Test infrastructure only (see oracle/__init__.py).
 * W8A16: kernels/tpu_inference/kernels/experimental/dense_fp8.py:23-59.
   For each 128-row K block kb: acc += dot(x_bf16[:, kb], w_e4m3[kb, :]) (f32)
   * s[kb, :] (f32), acc initialised to zero; stored as bf16.
+* W8A16 "pre" mode: dense_fp8.py:33-43 -- the weight tile is widened to
+  bf16, each weight multiplied by bf16(s[kb, n]) with the product rounded to
+  bf16, then one f32 dot over K (no scale after the dot).
 * W8A8 (activations e4m3 with per-(token, 128-K) f32 scales, weights e4m3 with
   128x128 f32 block scales): no reference kernel; the closed form is
   out[m, n] = sum_kb sx[m, kb] * sw[kb, n // 128] * dot(xq[m, kb], wq[kb, n]).
@@ -26,6 +29,28 @@ def matmul_w8a16(x, w_codes, s, accumulate: str = "f64", out_dtype: str = "bfloa
     for kb in range(k // 128):
         part = x[:, kb * 128:(kb + 1) * 128].astype(dt) @ w[kb * 128:(kb + 1) * 128].astype(dt)
         acc = acc + part * s[kb].astype(dt)[None, :]
+    if out_dtype == "bfloat16":
+        return round_bf16(acc.astype(np.float32))
+    return acc
+
+
+def pre_weight(w_codes, s):
+    """The "pre" mode's bf16 weight (dense_fp8.py:39-41):
+    w_pre[k, n] = bf16(e4m3(w[k, n]) * bf16(s[k // 128, n])), each rounding
+    to nearest even.  The f32 product of a bf16 and an e4m3 value is exact,
+    so this is the correctly rounded bf16 product.  Returns float32."""
+    w = E4M3_VALUES[np.asarray(w_codes)].astype(np.float32)
+    k, n = w.shape
+    sb = round_bf16(np.asarray(s, np.float32).reshape(k // 128, n))
+    prod = (w.reshape(k // 128, 128, n) * sb[:, None, :]).reshape(k, n)
+    return round_bf16(prod.astype(np.float32))
+
+
+def matmul_pre(x, w_codes, s, accumulate: str = "f64", out_dtype: str = "bfloat16"):
+    """The "pre" mode: x [M, K] f32 (bf16-exact) @ pre_weight(w_codes, s)."""
+    x = np.asarray(x, np.float32)
+    dt = np.float64 if accumulate == "f64" else np.float32
+    acc = x.astype(dt) @ pre_weight(w_codes, s).astype(dt)
     if out_dtype == "bfloat16":
         return round_bf16(acc.astype(np.float32))
     return acc

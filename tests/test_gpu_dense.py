@@ -9,6 +9,7 @@ from conftest import bf16_bits, bf16_tensor
 from oracle import dense_fp8 as odf
 from oracle import gmm as ogmm
 from oracle.numerics import E4M3_VALUES, bf16_to_f32
+from oracle.numerics import bf16_bits as f32_to_bf16_bits
 
 pytestmark = pytest.mark.gpu
 
@@ -230,3 +231,85 @@ def test_w8a8_tile_choice_is_launched(dev, tile, plan):
     assert last_plan().astuple() == plan
     y64 = odf.matmul_w8a8(wl.xq, wl.sx, wl.wq, wl.sw, out_dtype="float64")
     print(tile, _check(out, y64, odf.abs_product_w8a8(wl.xq, wl.sx, wl.wq, wl.sw), _K))
+
+
+def _dense_inputs(dev, M, K, N, seed):
+    from dw_tpu_amd.workloads import make_dense_workload
+    wl = make_dense_workload(M, K, N, seed=seed)
+    x = bf16_tensor(wl.x_bits, dev)
+    w = torch.from_numpy(wl.wq).to(dev).view(torch.float8_e4m3fn)
+    return wl, x, w
+
+
+def test_same_math_modes_are_bitwise_equal(dev):
+    """"wide", "flipped" and "megablox" compute the native arithmetic
+    (reference dense_fp8.py:1-5, 33-53): the same launch, the same bits."""
+    from dw_tpu_amd.dense_fp8 import matmul
+    for M in (4, 128):
+        wl, x, w = _dense_inputs(dev, M, 1024, 512, 81)
+        s = torch.from_numpy(wl.s_w8a16).to(dev)
+        ref = bf16_bits(matmul(x, w, s))
+        for mode in ("wide", "flipped", "megablox"):
+            assert np.array_equal(bf16_bits(matmul(x, w, s, mode=mode)), ref), (M, mode)
+
+
+@pytest.mark.parametrize("M,tile", [(16, ("native", 16, 1024, 1024)),     # the reference's defaults
+                                    (4, ("native", 4, 1024, 2048)),       # _TUNED entries
+                                    (512, ("megablox", 128, 1024, 2048))])
+def test_reference_tiles_take_the_library_plan_with_a_warning(dev, M, tile):
+    """A tile of the reference's TPU tables names no launch here: matmul warns
+    and runs the library's own plan, with the same bits."""
+    from dw_tpu_amd.dense_fp8 import matmul
+    wl, x, w = _dense_inputs(dev, M, 2048, 4096, 82)
+    s = torch.from_numpy(wl.s_w8a16).to(dev)
+    mode, tm, tk, tn = tile
+    with pytest.warns(UserWarning, match="names no launch"):
+        got = matmul(x, w, s, mode=mode, tm=tm, tk=tk, tn=tn)
+    assert np.array_equal(bf16_bits(got), bf16_bits(matmul(x, w, s)))
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 1024, 512), (17, 512, 256), (64, 1024, 384), (128, 1024, 512),
+                                   (300, 768, 4096)])
+def test_pre_mode_against_oracle(dev, M, K, N):
+    """mode="pre" (reference dense_fp8.py:33-43): x @ bf16(w * bf16(s)) in
+    f32 against the float64 oracle of the same rounding, within the stated
+    dense bound (computed on the pre weights)."""
+    from dw_tpu_amd.dense_fp8 import matmul
+    wl, x, w = _dense_inputs(dev, M, K, N, 83)
+    out = matmul(x, w, torch.from_numpy(wl.s_w8a16).to(dev), mode="pre")
+    xf = bf16_to_f32(wl.x_bits)
+    y64 = odf.matmul_pre(xf, wl.wq, wl.s_w8a16, out_dtype="float64")
+    ap = np.abs(xf.astype(np.float64)) @ np.abs(odf.pre_weight(wl.wq, wl.s_w8a16).astype(np.float64))
+    print(M, K, N, _check(out, y64, ap, K))
+
+
+def test_pre_mode_products_bit_exact(dev):
+    """One-hot activation rows make each output element a single rounded
+    product: y[m, n] = bf16(w[k_m, n] * bf16(s[k_m // 128, n])) bit for bit
+    (random non-power-of-two scales, every K block and column)."""
+    from dw_tpu_amd.dense_fp8 import matmul
+    M, K, N = 96, 1024, 256
+    wl, _, w = _dense_inputs(dev, M, K, N, 84)
+    rng = np.random.default_rng(85)
+    s = (rng.random((K // 128, 1, N)) * 3.0 + 0.01).astype(np.float32)
+    ks = rng.integers(0, K, M)
+    x = np.zeros((M, K), np.float32)
+    x[np.arange(M), ks] = 1.0
+    out = matmul(bf16_tensor(f32_to_bf16_bits(x), dev), w, torch.from_numpy(s).to(dev), mode="pre")
+    want = odf.pre_weight(wl.wq, s)[ks]
+    assert np.array_equal(bf16_to_f32(bf16_bits(out)), want)
+
+
+def test_pre_mode_power_of_two_scales_equal_native_on_its_plan(dev):
+    """With power-of-two scales every pre product is exact, so "pre" and the
+    native scaling on the same launch plan give the same bits."""
+    from dw_tpu_amd.dense_fp8 import last_plan, matmul
+    from dw_tpu_amd.dense_fp8_tiles import plan_to_tile
+    rng = np.random.default_rng(86)
+    for M, K, N in ((16, 1024, 512), (200, 2048, 384)):
+        wl, x, w = _dense_inputs(dev, M, K, N, 87)
+        s = torch.from_numpy(np.ldexp(np.float32(1), rng.integers(-8, 3, (K // 128, 1, N))).astype(np.float32)).to(dev)
+        pre = bf16_bits(matmul(x, w, s, mode="pre"))
+        t = plan_to_tile(last_plan(), K)
+        nat = bf16_bits(matmul(x, w, s, mode=t.mode, tm=t.tm, tk=t.tk, tn=t.tn, stages=t.stages))
+        assert np.array_equal(pre, nat), (M, K, N, t)

@@ -282,6 +282,45 @@ def test_dense_w8a8_brute_force(rng):
             assert got[m, n] == pytest.approx(acc, rel=1e-12)
 
 
+def _e4m3_code(v):
+    return int(np.flatnonzero(E4M3_VALUES == v)[0])
+
+
+@pytest.mark.parametrize("w,s,want", [
+    (1.125, 1.0078125, 1.1328125),   # 1.1337890625 = 145.125 ulps of 2^-7: rounds down
+    (1.5, 1.0078125, 1.515625),      # 1.51171875 = 193.5 ulps: a tie, to the even 194
+    (1.75, 1.0078125, 1.765625),     # 1.763671875 = 225.75 ulps: rounds up
+    (1.5, 1.005859375, 1.515625),    # the scale rounds to bf16 first (1 + 2^-7), then the tie
+    (-3.0, 0.3, -0.90234375),        # bf16(0.3) = 0.30078125; -0.90234375 = -231 ulps of 2^-8: exact
+    (448.0, 2.0 ** -10, 0.4375),     # power-of-two scales are exact
+])
+def test_dense_pre_weight_rounding_hand_cases(w, s, want):
+    """The "pre" weight bf16(w * bf16(s)) on hand-computed cases: round to
+    nearest even after an exact product, and the scale rounded to bf16
+    before the product (the fourth case gives 1.5078125 if it is not)."""
+    codes = np.zeros((128, 1), np.uint8)
+    codes[5, 0] = _e4m3_code(w)
+    got = dense_fp8.pre_weight(codes, np.full((1, 1, 1), s, np.float32))
+    assert got[5, 0] == want
+    assert np.all(np.delete(got[:, 0], 5) == 0.0)
+
+
+def test_dense_pre_equals_native_for_power_of_two_scales(rng):
+    """With power-of-two scales the pre rounding is exact, so "pre" and the
+    native per-block scaling are the same sum (float64, up to summation
+    order); the scale is per (128-deep K block, column), not transposed."""
+    M, K, N = 4, 384, 40
+    x = round_bf16(rng.standard_normal((M, K)).astype(np.float32))
+    wq = to_e4m3(rng.standard_normal((K, N)).astype(np.float32))
+    s = np.ldexp(np.float32(1), rng.integers(-6, 4, (K // 128, 1, N))).astype(np.float32)
+    pre = dense_fp8.matmul_pre(x, wq, s, out_dtype="float64")
+    nat = dense_fp8.matmul_w8a16(x, wq, s, out_dtype="float64")
+    np.testing.assert_allclose(pre, nat, rtol=1e-12, atol=1e-12)
+    # a planted mistake -- the scale indexed by (column, K block) -- is caught
+    bad = dense_fp8.matmul_pre(x, wq, s.reshape(N, 1, K // 128).transpose(2, 1, 0).copy()[::-1], out_dtype="float64")
+    assert not np.allclose(bad, nat, rtol=1e-6)
+
+
 def test_block_quantizers_bound_and_shape(rng):
     w = rng.standard_normal((256, 384)).astype(np.float32)
     q, s = quant.quantize_fp8_blocks(w)

@@ -30,3 +30,18 @@ def test_recall_target_from_env(monkeypatch):
 def test_host_tensor_still_rejected():
     with pytest.raises(ValueError, match="device tensor"):
         routing.fused_moe_fp4_routing(torch.zeros(4, 8), 2, False, "softmax", torch.float32, {}, approx_topk=True)
+
+
+@pytest.mark.parametrize("value", ["2", "not-a-number"])
+def test_recall_target_env_ignored_off_the_approx_branch(monkeypatch, value):
+    """The recall target is read only when the approx_max_k branch is taken:
+    with approx off (or hash routing given) a malformed value is ignored and
+    the call proceeds to its usual checks (here: host tensors are rejected)."""
+    monkeypatch.setenv("MOE_APPROX_TOPK_RECALL_TARGET", value)
+    monkeypatch.delenv("MOE_APPROX_TOPK", raising=False)
+    with pytest.raises(ValueError, match="device tensor"):
+        routing.fused_moe_fp4_routing(torch.zeros(4, 8), 2, False, "softmax", torch.float32, {})
+    with pytest.raises(ValueError, match="device tensor"):
+        routing.fused_moe_fp4_routing(torch.zeros(4, 8), 2, False, "softmax", torch.float32,
+                                      {"hash_based_topk_indices": torch.zeros(4, 2, dtype=torch.int32)},
+                                      approx_topk=True)

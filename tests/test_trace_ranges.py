@@ -24,10 +24,15 @@ def test_calls_are_wrapped_when_on(monkeypatch):
     assert pushed == [("push", "dwm_row_gather"), ("pop", None), ("push", "dwm_moe_combine"), ("pop", None)]
 
 
-def test_off_by_default_and_decorator(monkeypatch):
+def test_switch_and_decorator(monkeypatch):
+    """Whatever DWTPU_ROCTX this process started with (a marker-trace pass
+    sets it), enable(False) turns the ranges off and enable(True) on."""
     pushed = []
     monkeypatch.setattr(torch.cuda.nvtx, "range_push", lambda n: pushed.append(n))
     monkeypatch.setattr(torch.cuda.nvtx, "range_pop", lambda: None)
+    was = _trace.enabled()
+    monkeypatch.delenv("DWTPU_ROCTX", raising=False)
+    _trace.enable(False)
 
     @_trace.traced("op")
     def f(x):
@@ -39,13 +44,18 @@ def test_off_by_default_and_decorator(monkeypatch):
     try:
         assert f(2) == 3 and pushed == ["op"]
     finally:
-        _trace.enable(False)
+        _trace.enable(was)
 
 
-def test_environment_switch():
+@pytest.mark.parametrize("value,want", [(None, "False"), ("1", "True")])
+def test_environment_switch_and_default(value, want):
+    """Off by default in a clean environment; DWTPU_ROCTX=1 turns it on."""
     code = "from dw_tpu_amd import _trace; print(_trace.enabled())"
     import os
     pkg = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "dw-tpu_amd")
-    env = dict(os.environ, DWTPU_ROCTX="1", PYTHONPATH=pkg)
+    env = {k: v for k, v in os.environ.items() if k != "DWTPU_ROCTX"}
+    env["PYTHONPATH"] = pkg
+    if value is not None:
+        env["DWTPU_ROCTX"] = value
     out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env, timeout=120)
-    assert out.stdout.strip() == "True", out.stderr[-500:]
+    assert out.stdout.strip() == want, out.stderr[-500:]

@@ -56,3 +56,46 @@ def test_noalloc_dispatch_rejects_sizes_past_its_scratch():
     with pytest.raises(_lib.Unsupported, match="static scratch"):
         _lib.call("dwm_moe_dispatch_noalloc", ctypes.c_void_p(16), T, topk, E, ctypes.c_void_p(16),
                   ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16), None, None, None)
+
+
+def _static_outs(n, E, dev):
+    return [torch.full((k,), -7, dtype=torch.int32, device=dev) for k in (n, n, n, E, E + 1)] + [
+        torch.zeros(1, dtype=torch.int32, device=dev)]
+
+
+@pytest.mark.gpu
+def test_noalloc_dispatch_under_graph_capture(dev):
+    """The no-alloc dispatch captured into a HIP graph and replayed with new
+    ids copied in, eager work and synchronisations between the replays; every
+    replay bit-identical to dwm_moe_dispatch with a workspace.  The 2048-id
+    batch is captured with no earlier no-alloc call of its size class (it
+    never looks the static array up); the 20,000-id batch (three launches
+    on the static counters) is captured after one eager call, as the header
+    asks of batches above 8192 ids."""
+    rng = np.random.default_rng(5)
+    for T, topk, E in ((256, 8, 32), (2500, 8, 256)):
+        n = T * topk
+        ids = torch.zeros((T, topk), dtype=torch.int32, device=dev)
+        outs = _static_outs(n, E, dev)
+        args = lambda: (_lib.ptr(ids), T, topk, E) + tuple(_lib.ptr(t) for t in outs)  # noqa: E731
+        if n > 8192:
+            _lib.call("dwm_moe_dispatch_noalloc", *args(), _lib.stream_handle(dev))
+            torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            outs[5].zero_()  # flags start at zero on every replay (a fill kernel, not a memset node)
+            _lib.call("dwm_moe_dispatch_noalloc", *args(), _lib.stream_handle(dev))
+        torch.cuda.synchronize()
+        for rep in range(4):
+            ids_np = rng.integers(0, E, (T, topk)).astype(np.int32)
+            if rep == 2:
+                ids_np[1, 3] = E + 5  # an invalid id: flagged and ordered last
+            ids.copy_(torch.from_numpy(ids_np))
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            got = [t.cpu().numpy().copy() for t in outs]
+            want = _dispatch(ids, T, topk, E, dev, noalloc=False)
+            for a, b in zip(got, want):
+                assert np.array_equal(a, b), (T, E, rep)
+            assert got[5][0] == (1 if rep == 2 else 0)
