@@ -340,13 +340,20 @@ __global__ __launch_bounds__(kFusedThreads) void dispatch_small_kernel(const int
   }
 }
 
+// Floor division by a positive divisor (Python / JAX `//` on integers).
+__device__ __forceinline__ int64_t floor_div(int64_t i, int64_t d) {
+  return i >= 0 ? i / d : -((-i + d - 1) / d);
+}
+
+// out[r] = src[idx[r] // div] (div = 1: a plain row gather; div = topk: the
+// dispatch gather of the token rows behind an expert-sorted argsort).
 template <typename V>
 __global__ __launch_bounds__(256) void row_gather_kernel(const char *src, int64_t src_rows,
                                                          int64_t row_bytes, const int32_t *idx,
-                                                         int64_t rows, char *out) {
+                                                         int64_t rows, char *out, int div) {
   const int64_t nv = row_bytes / (int64_t)sizeof(V);
   for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
-    const int64_t s = gather_index(idx[r], src_rows);
+    const int64_t s = gather_index(div == 1 ? (int64_t)idx[r] : floor_div(idx[r], div), src_rows);
     const V *sp = (const V *)(src + s * row_bytes);
     V *dp = (V *)(out + r * row_bytes);
     for (int64_t i = threadIdx.x; i < nv; i += blockDim.x) __builtin_nontemporal_store(sp[i], dp + i);
@@ -621,26 +628,38 @@ extern "C" int dwm_moe_dispatch_noalloc(const int32_t *topk_ids, int64_t T, int 
                          flags, counts, as_stream(stream));
 }
 
-extern "C" int dwm_row_gather(const void *src, int64_t src_rows, int64_t row_bytes,
-                              const int32_t *idx, int64_t rows, void *out, void *stream) {
-  clear_error();
-  DWM_CHECK_ARG(src_rows >= 0 && row_bytes >= 0 && rows >= 0, "row_gather: bad sizes");
+static int gather_run(const char *what, const void *src, int64_t src_rows, int64_t row_bytes, const int32_t *idx,
+                      int64_t rows, int div, void *out, void *stream) {
+  DWM_CHECK_ARG(src_rows >= 0 && row_bytes >= 0 && rows >= 0 && div > 0, "%s: bad sizes", what);
   if (rows == 0 || row_bytes == 0) return DWM_OK;
-  DWM_CHECK_ARG(src_rows > 0, "row_gather: empty source with rows to gather");
-  DWM_CHECK_ARG(src && idx && out, "row_gather: null pointer");
+  DWM_CHECK_ARG(src_rows > 0, "%s: empty source with rows to gather", what);
+  DWM_CHECK_ARG(src && idx && out, "%s: null pointer", what);
   const unsigned grid = (unsigned)(rows < 65536 ? rows : 65536);
   hipStream_t st = as_stream(stream);
   const uintptr_t al = (uintptr_t)src | (uintptr_t)out | (uintptr_t)row_bytes;
   if (al % 16 == 0)
     hipLaunchKernelGGL(row_gather_kernel<u32x4_t>, dim3(grid), dim3(256), 0, st, (const char *)src,
-                       src_rows, row_bytes, idx, rows, (char *)out);
+                       src_rows, row_bytes, idx, rows, (char *)out, div);
   else if (al % 4 == 0)
     hipLaunchKernelGGL(row_gather_kernel<uint32_t>, dim3(grid), dim3(256), 0, st, (const char *)src,
-                       src_rows, row_bytes, idx, rows, (char *)out);
+                       src_rows, row_bytes, idx, rows, (char *)out, div);
   else
     hipLaunchKernelGGL(row_gather_kernel<uint8_t>, dim3(grid), dim3(256), 0, st, (const char *)src,
-                       src_rows, row_bytes, idx, rows, (char *)out);
-  return launch_status("row_gather");
+                       src_rows, row_bytes, idx, rows, (char *)out, div);
+  return launch_status(what);
+}
+
+extern "C" int dwm_row_gather(const void *src, int64_t src_rows, int64_t row_bytes,
+                              const int32_t *idx, int64_t rows, void *out, void *stream) {
+  clear_error();
+  return gather_run("row_gather", src, src_rows, row_bytes, idx, rows, 1, out, stream);
+}
+
+extern "C" int dwm_dispatch_gather(const void *hidden, int64_t T, int64_t row_bytes, const int32_t *argsort,
+                                   int64_t rows, int topk, void *out, void *stream) {
+  clear_error();
+  DWM_CHECK_ARG(topk > 0, "dispatch_gather: topk must be positive (got %d)", topk);
+  return gather_run("dispatch_gather", hidden, T, row_bytes, argsort, rows, topk, out, stream);
 }
 
 extern "C" int dwm_moe_combine(const void *x, int x_dtype, int64_t x_rows, int64_t H,

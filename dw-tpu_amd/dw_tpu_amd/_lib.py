@@ -49,6 +49,7 @@ SIGNATURES = {
     "dwm_moe_dispatch": [_p, _i64, _i32, _i32, _p, _p, _p, _p, _p, _p, _p, _p],
     "dwm_moe_dispatch_noalloc": [_p, _i64, _i32, _i32, _p, _p, _p, _p, _p, _p, _p],
     "dwm_row_gather": [_p, _i64, _i64, _p, _i64, _p, _p],
+    "dwm_dispatch_gather": [_p, _i64, _i64, _p, _i64, _i32, _p, _p],
     "dwm_moe_combine": [_p, _i32, _i64, _i64, _p, _p, _i32, _i64, _i32, _p, _i32, _p],
     "dwm_dense_fp8_prepack": [_p, _i64, _i64, _p, _p],
     "dwm_dense_fp8_workspace_size": [_i64, _i64, _i64, _p],

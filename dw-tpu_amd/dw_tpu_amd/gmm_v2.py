@@ -26,7 +26,10 @@ path (patches/tokamax/0001-...:89-100).  An ``MxLhs`` (already quantized)
 may be passed as ``lhs`` directly.  The default (no lhs_quant_dtype) keeps
 the reference's W4A16 arithmetic: bf16 lhs, weights decoded exactly.
 """
+import collections
 import ctypes
+import threading
+import weakref
 from dataclasses import dataclass
 
 import torch
@@ -214,6 +217,43 @@ def prepack_fp4(rhs: torch.Tensor, rhs_scale: torch.Tensor, rhs_fp4_codes: bool 
     return Fp4Weight(wout, sout, e, k, n, gate_up)
 
 
+# Raw weights handed to gmm_v2 call after call (the reference's per-call
+# form) are prepacked and checked once: the prepacked copy is kept while the
+# raw rhs and scale tensors are alive and unmodified (the same objects with
+# the same in-place version counters).  Each entry holds the prepacked bytes
+# (the size of the raw weight) in device memory; clear_prepack_cache() drops
+# them.
+_PREPACK_CACHE_SIZE = 8
+_prepack_cache = collections.OrderedDict()
+_prepack_lock = threading.Lock()
+
+
+def clear_prepack_cache():
+    """Drop the prepacked copies gmm_v2 keeps for raw weight tensors."""
+    with _prepack_lock:
+        _prepack_cache.clear()
+
+
+def _prepack_cached(rhs, rhs_scale, rhs_fp4_codes, gate_up):
+    if rhs_scale is None:
+        return prepack_fp4(rhs, rhs_scale, rhs_fp4_codes=rhs_fp4_codes, gate_up=gate_up)
+    key = (id(rhs), id(rhs_scale), bool(rhs_fp4_codes), bool(gate_up))
+    with _prepack_lock:
+        hit = _prepack_cache.get(key)
+        if hit is not None:
+            r_ref, s_ref, r_ver, s_ver, w = hit
+            if r_ref() is rhs and s_ref() is rhs_scale and rhs._version == r_ver and rhs_scale._version == s_ver:
+                _prepack_cache.move_to_end(key)
+                return w
+            del _prepack_cache[key]
+    w = prepack_fp4(rhs, rhs_scale, rhs_fp4_codes=rhs_fp4_codes, gate_up=gate_up)
+    with _prepack_lock:
+        _prepack_cache[key] = (weakref.ref(rhs), weakref.ref(rhs_scale), rhs._version, rhs_scale._version, w)
+        while len(_prepack_cache) > _PREPACK_CACHE_SIZE:
+            _prepack_cache.popitem(last=False)
+    return w
+
+
 def gmm_v2(lhs: torch.Tensor,
            rhs,
            group_sizes: torch.Tensor,
@@ -234,7 +274,9 @@ def gmm_v2(lhs: torch.Tensor,
     """Ragged grouped matmul: out[rows of g] = lhs[rows of g] @ dequant(rhs[g - group_offset]).
 
     lhs: [M, K] bf16, rows sorted by group (or an ``MxLhs``: the MX mode).  rhs: ``Fp4Weight`` (prepacked)
-    or packed fp4 bytes [E, K, N/2] (prepacked per call).  group_sizes:
+    or packed fp4 bytes [E, K, N/2] (prepacked and checked on the first call with those rhs / rhs_scale
+    tensors, which synchronises the stream once; the prepacked copy is reused while both tensors are alive
+    and unmodified, see ``clear_prepack_cache``).  group_sizes:
     int32 [G] device tensor.  group_offset: None, an int, or an int32 [1]
     device tensor (first local group).  Returns [M, N] in
     ``preferred_element_type`` (bf16 default, or float32).  Rows outside the
@@ -277,7 +319,7 @@ def gmm_v2(lhs: torch.Tensor,
             raise ValueError("gmm_v2: a prepacked Fp4Weight carries its own scales; pass rhs_scale=None")
         w = rhs
     else:
-        w = prepack_fp4(rhs, rhs_scale, rhs_fp4_codes=rhs_fp4_codes, gate_up=fused)
+        w = _prepack_cached(rhs, rhs_scale, rhs_fp4_codes, fused)
     if w.gate_up != fused:
         raise ValueError("gmm_v2: gate/up-prepacked weights run only (and always) with the fused activation"
                          if w.gate_up else "gmm_v2: the fused activation needs weights prepacked with gate_up=True")

@@ -95,7 +95,19 @@ def fast_dispatch_gather(hidden: torch.Tensor, topk_argsort_indices: torch.Tenso
                          mode: int = 2) -> torch.Tensor:
     """hidden[arange(T).repeat(topk)[argsort]], bitwise (moe_fast_dispatch.py:188-194).
 
-    ``mode`` is accepted for signature compatibility; both modes run the same
-    HIP gather.
+    One launch (``dwm_dispatch_gather``): the token of each sorted row,
+    argsort // topk, is computed inside the gather.  ``mode`` is accepted for
+    signature compatibility; both modes run the same HIP gather.
     """
-    return row_gather(hidden, sorted_token_indices(topk_argsort_indices, topk))
+    if hidden.dim() != 2:
+        raise ValueError("fast_dispatch_gather: hidden must be 2-D")
+    if topk <= 0:
+        raise ValueError(f"fast_dispatch_gather: topk must be positive, got {topk}")
+    src = hidden.contiguous()
+    idx = topk_argsort_indices.to(torch.int32).contiguous().reshape(-1)
+    dev = _lib.require_cuda(src, idx)
+    rows = idx.numel()
+    out = torch.empty((rows, src.shape[1]), dtype=src.dtype, device=dev)
+    _lib.call("dwm_dispatch_gather", _lib.ptr(src), src.shape[0], src.shape[1] * src.element_size(),
+              _lib.ptr(idx), rows, int(topk), _lib.ptr(out), _lib.stream_handle(dev))
+    return out

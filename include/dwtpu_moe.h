@@ -289,6 +289,14 @@ int dwm_moe_dispatch_noalloc(const int32_t *topk_ids, int64_t T, int topk, int n
 int dwm_row_gather(const void *src, int64_t src_rows, int64_t row_bytes, const int32_t *idx,
                    int64_t rows, void *out, void *stream);
 
+/* out[j, :] = hidden[argsort[j] // topk, :] for j < rows (floor division,
+ * then the JAX gather index semantics of dwm_row_gather), bitwise: the rows
+ * of the expert-sorted argsort's tokens in one launch.  Replaces
+ * fast_dispatch_gather(hidden, topk_argsort_indices, topk)
+ * (moe_fast_dispatch.py:41-44, 188-194). */
+int dwm_dispatch_gather(const void *hidden, int64_t T, int64_t row_bytes, const int32_t *argsort, int64_t rows,
+                        int topk, void *out, void *stream);
+
 /* out[t] = round(sum_{k=0..topk-1} f32(x[idx[t*topk+k]]) * f32(w[t, k])),
  * summed left to right from +0.0 with separately rounded f32 multiply and
  * add (no FMA), one rounding to out_dtype.  Bit-exact to combine_xla /

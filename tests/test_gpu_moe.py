@@ -85,6 +85,20 @@ def test_row_gather_bitwise(dev, rng, T, H, dtype):
     assert np.array_equal(got.float().numpy(), want)
 
 
+@pytest.mark.parametrize("T,topk,H", [(64, 8, 1024), (513, 3, 7168), (10, 2, 100), (7, 5, 3)])
+def test_dispatch_gather_floor_div_bitwise(dev, rng, T, topk, H):
+    """fast_dispatch_gather computes argsort // topk inside the gather
+    (moe_fast_dispatch.py:41-44, 188-194): floor division, then JAX gather
+    index semantics, for any argsort values (negative and past T * topk
+    included) and unaligned rows."""
+    from dw_tpu_amd import fast_dispatch_gather
+    src = torch.from_numpy(rng.standard_normal((T, H)).astype(np.float32)).to(torch.bfloat16).to(dev)
+    idx = rng.integers(-2 * T * topk, 2 * T * topk, 3 * T * topk).astype(np.int32)
+    got = fast_dispatch_gather(src, torch.from_numpy(idx).to(dev), topk).cpu()
+    want = moe.gather_rows(src.cpu().float().numpy(), np.floor_divide(idx, topk))
+    assert np.array_equal(got.float().numpy(), want)
+
+
 def test_fast_dispatch_gather_workload(dev):
     from dw_tpu_amd import fast_dispatch_gather, moe_dispatch
     from dw_tpu_amd.workloads import make_gmm_workload
