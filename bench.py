@@ -23,6 +23,9 @@ gmm), the expert block, dense FP8, router and format kernels.
 experts on this host's cores (and one expert on one thread), the same for
 prefill and a dense GEMM, and reports the max abs and relative Frobenius
 error of one expert's GPU output rows against the oracle's float64 product.
+The same leg adds `vs_w4a16` to each `<name>_mx` line: the MX output's max
+abs and relative Frobenius distance from the reference's W4A16 result
+(float64, sampled rows and columns), the lhs quantization included.
 
 The headline is timed last, right after the `extra` workloads (its inputs
 are in HBM beforehand), so that the GPU runs at the clock it holds under
@@ -190,16 +193,20 @@ def prep_gmm(name, dev, steps, warmup):
     return run
 
 
-def prep_gmm_mx(name, dev, steps, warmup):
+def prep_gmm_mx(name, dev, steps, warmup, keep=None):
     """The MX mode of one gmm workload: the gmm on the quantized lhs, the
     lhs quantization (bf16 [M, K] -> e4m3 + scales), and the two back to back
-    (what gmm_v2(lhs_quant_dtype=float8_e4m3fn) runs on a bf16 lhs)."""
+    (what gmm_v2(lhs_quant_dtype=float8_e4m3fn) runs on a bf16 lhs).  With
+    ``keep`` (a dict), keep[name] = (workload, device output of the timed
+    gmm) for the CPU leg's distance from the W4A16 result."""
     from dw_tpu_amd.workloads import make_gmm_workload
     wl = make_gmm_workload(name)
     b = GmmBench(wl, dev, copies_for(wl), "mx")
 
     def run():
         r = gmm_result(wl, time_median(b.step, steps, warmup), "mx")
+        if keep is not None:
+            keep[name] = (wl, b.out[0])
         q_ms = time_steps(b.quant_step, steps, warmup)
         qb = wl.M * wl.K * 2 + wl.M * wl.K + wl.M * wl.K // 32
         r["quant"] = {"ms": round(q_ms, 5), "GB_s": round(qb / (q_ms * 1e-3) / 1e9, 1),
@@ -674,6 +681,29 @@ def cpu_gmm_baseline(wl, budget_s, gpu_check=None):
     return res
 
 
+def cpu_mx_distance(kept, seed=20261202):
+    """The MX mode's distance from the reference's arithmetic: max abs and
+    relative Frobenius error of the timed MX gmm's output against the W4A16
+    float64 result (bf16 lhs, exactly decoded weights) on sampled rows and
+    columns -- the same oracle functions and sampling as tests/test_gpu_mx.py.
+    kept: {name: (workload, device output)}."""
+    import numpy as np
+    import torch
+
+    from oracle import gmm as ogmm
+    res = {}
+    for name, (wl, out) in kept.items():
+        rows, cols = ogmm.sample_rows_cols(wl.group_sizes, wl.N, np.random.default_rng(seed))
+        got = out[torch.from_numpy(rows).to(out.device)][:, torch.from_numpy(cols).to(out.device)].float().cpu()
+        y64 = ogmm.w4a16_rows(wl.lhs_bits[rows], wl.rhs_e2m1, wl.scale_codes, wl.group_sizes, rows, cols)
+        st = ogmm.error_stats(got.numpy(), y64)
+        res[name] = {"max_abs": round(st["max_abs"], 4), "rel_fro": round(st["rel_fro"], 6),
+                     "max_abs_ref": round(float(np.abs(y64).max()), 2), "rows": int(len(rows)),
+                     "cols": int(len(cols)),
+                     "vs": "float64 W4A16 result (bf16 lhs x exactly decoded fp4 weights), sampled rows x cols"}
+    return res
+
+
 def cpu_dense_baseline(m, budget_s):
     """numpy oracle of the dense W8A16 GEMM (K=7168, N=4096): e4m3 decode,
     per-128-K-block f32 dot times the block scale, f32 accumulate, on
@@ -761,6 +791,7 @@ def main():
     wl = make_gmm_workload("decode_gate_up")
     b = GmmBench(wl, dev, copies_for(wl))
     extra = {}
+    mx_out = {}  # MX outputs kept for the CPU leg's distance from the W4A16 result
     if args.extra == "all":
         # Inputs of every workload first, then every timed region back to
         # back (the GPU never waits on host-side input generation between
@@ -777,7 +808,7 @@ def main():
             # (~0.1 s of prefill load) let the clock come back up to its
             # power-limited level first (with 5 the MX prefill measured
             # 1.65 ms against 1.55 ms after a settled clock).
-            runs.append(prep_gmm_mx(name, dev, args.steps, max(args.warmup, 60)))
+            runs.append(prep_gmm_mx(name, dev, args.steps, max(args.warmup, 60), mx_out))
             log(f"bench: inputs of {name} gmm")
             runs.append(prep_gmm(name, dev, args.steps, args.warmup))
         for label, prep in (("moe block", prep_moe_block), ("dense fp8", prep_dense),
@@ -787,7 +818,7 @@ def main():
             runs.append(prep(dev, args.steps, args.warmup))
         for name in ("decode_down", "decode_gate_up"):
             log(f"bench: inputs of {name} gmm, MX mode")
-            runs.append(prep_gmm_mx(name, dev, args.steps, args.warmup))
+            runs.append(prep_gmm_mx(name, dev, args.steps, args.warmup, mx_out))
         # The last region runs at least 200 warmup launches (~30 ms of
         # decode-type load): after memory-bound regions the power manager
         # can hold the clock low for tens of milliseconds, and a
@@ -818,6 +849,10 @@ def main():
     if args.cpu_budget > 0:
         log("bench: cpu baseline")
         cpu = cpu_gmm_baseline(wl, args.cpu_budget, gpu_check)
+        if mx_out:
+            for name, d in cpu_mx_distance(mx_out).items():
+                extra[f"{name}_mx"]["vs_w4a16"] = d
+        mx_out.clear()
         if args.extra == "all":
             from dw_tpu_amd.workloads import make_gmm_workload
             cpu["other_workloads"] = {

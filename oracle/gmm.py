@@ -132,6 +132,37 @@ def error_stats(y, y64, mask=None):
             "rel_fro": float(np.linalg.norm(d) / den) if den > 0 else float(np.linalg.norm(d))}
 
 
+def sample_rows_cols(group_sizes, n, rng, ncols=64):
+    """Rows and columns on which full-size workloads are checked: the first,
+    last and one random row of every non-empty group, and columns 0, N - 1
+    and ncols - 2 random ones (sorted, unique)."""
+    gs = np.asarray(group_sizes, np.int64)
+    starts = np.concatenate([[0], np.cumsum(gs)])
+    rows = np.unique(np.concatenate([[s, s + g - 1, s + rng.integers(0, g)]
+                                     for s, g in zip(starts[:-1], gs) if g > 0]))
+    cols = np.unique(np.r_[0, n - 1, rng.integers(0, n, ncols - 2)])
+    return rows, cols
+
+
+def w4a16_rows(lhs_bits_rows, rhs_e2m1, scale_codes, group_sizes, rows, cols):
+    """The reference's W4A16 result (bf16 lhs times exactly decoded e2m1 x
+    e8m0 weights, patches/tokamax/0001-...:58-66, 93-96) in float64 for the
+    given rows (lhs_bits_rows: their bf16 bit patterns) and columns of a
+    grouped matmul over all groups: rhs_e2m1 [E, K, N/2] packed nibbles
+    (low nibble = even column), scale_codes [E, K/32, 1, N] e8m0 codes."""
+    from .fp4 import e2m1_to_codes, e8m0_decode
+    from .numerics import bf16_to_f32
+    cols = np.asarray(cols)
+    b = rhs_e2m1[:, :, cols // 2]
+    nib = np.where(cols % 2 == 1, b >> 4, b & 0xF).astype(np.uint8)
+    w = dequant_rhs(e2m1_to_codes(nib), e8m0_decode(scale_codes[..., cols]))
+    starts = np.concatenate([[0], np.cumsum(np.asarray(group_sizes, np.int64))])
+    grp = np.searchsorted(starts, rows, side="right") - 1
+    sub_gs = np.bincount(grp, minlength=len(group_sizes)).astype(np.int32)
+    y64, _ = gmm(bf16_to_f32(lhs_bits_rows), None, None, sub_gs, out_dtype="float64", w=w)
+    return y64
+
+
 def acceptance_policy(y, y_base, y64, mask=None):
     """The reference's kernel-acceptance rule
     (results/dsv4-dense-gemm-kernel-1/NOTES.md:26-27): against the float64

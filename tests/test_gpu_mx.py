@@ -246,10 +246,7 @@ def test_gmm_mx_workloads(dev, rng, name):
     if name == "cpu_plumbing":
         rows, cols = np.arange(wl.M), np.arange(wl.N)
     else:
-        starts = np.concatenate([[0], np.cumsum(wl.group_sizes)])
-        rows = np.unique(np.concatenate([[s, s + n - 1, s + rng.integers(0, n)]
-                                         for s, n in zip(starts[:-1], wl.group_sizes) if n > 0]))
-        cols = np.unique(np.r_[0, wl.N - 1, rng.integers(0, wl.N, 62)])
+        rows, cols = gmm.sample_rows_cols(wl.group_sizes, wl.N, rng)
     r_t = torch.from_numpy(rows).to(dev)
     codes, scales = q.codes[r_t].cpu().numpy(), q.scales[r_t].cpu().numpy()
     want_c, want_s = quant.mx_quantize_e4m3(bf16_to_f32(wl.lhs_bits[rows]))
@@ -263,10 +260,16 @@ def test_gmm_mx_workloads(dev, rng, name):
     y64, ap, _ = _oracle_mx(wl.lhs_bits[rows], w, sub_gs)
     got = out[r_t][:, torch.from_numpy(cols).to(dev)]
     stats = _check(got, y64, ap, wl.K, torch.bfloat16)
-    y_bf16, _ = gmm.gmm(bf16_to_f32(wl.lhs_bits[rows]), None, None, sub_gs, out_dtype="float64", w=w)
-    stats["quant_rel_fro_vs_bf16_path"] = gmm.error_stats(got.float().cpu().numpy(), y_bf16)["rel_fro"]
+    # The distance a caller sees: the MX output against the reference's W4A16
+    # result (the lhs quantization included).  bench.py's CPU leg reports the
+    # same figures for each <name>_mx line, from the same oracle functions.
+    y_w4a16 = gmm.w4a16_rows(wl.lhs_bits[rows], wl.rhs_e2m1, wl.scale_codes, wl.group_sizes, rows, cols)
+    assert np.allclose(y_w4a16, gmm.gmm(bf16_to_f32(wl.lhs_bits[rows]), None, None, sub_gs,
+                                        out_dtype="float64", w=w)[0], rtol=0, atol=0)
+    vs = gmm.error_stats(got.float().cpu().numpy(), y_w4a16)
+    stats["vs_w4a16_max_abs"], stats["vs_w4a16_rel_fro"] = vs["max_abs"], vs["rel_fro"]
     print(name, stats, flush=True)
-    assert stats["quant_rel_fro_vs_bf16_path"] < 0.05
+    assert stats["vs_w4a16_rel_fro"] < 0.05
 
 
 @pytest.mark.parametrize("name", ["decode_gate_up", "prefill"])

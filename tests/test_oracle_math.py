@@ -109,6 +109,25 @@ def test_gmm_seq32_is_the_sequential_f32_sum(rng):
     assert np.any(ys != y64)  # it does round
 
 
+def test_w4a16_rows_and_sampling_match_the_full_product():
+    """The sampled W4A16 reference (used for the MX mode's distance) is the
+    full float64 gmm's rows and columns; the sample has the first, last and
+    one more row of every non-empty group, and columns 0 and N - 1."""
+    from dw_tpu_amd.workloads import make_gmm_workload
+    from oracle.numerics import bf16_to_f32
+    wl = make_gmm_workload("cpu_plumbing")
+    rows, cols = gmm.sample_rows_cols(wl.group_sizes, wl.N, np.random.default_rng(3), ncols=20)
+    starts = np.concatenate([[0], np.cumsum(wl.group_sizes)])
+    for s0, g in zip(starts[:-1], wl.group_sizes):
+        if g > 0:
+            assert s0 in rows and s0 + g - 1 in rows
+    assert cols[0] == 0 and cols[-1] == wl.N - 1
+    full, _ = gmm.gmm(bf16_to_f32(wl.lhs_bits), fp4.e2m1_to_codes(fp4.unpack_nibbles(wl.rhs_e2m1)),
+                      fp4.e8m0_decode(wl.scale_codes), wl.group_sizes, out_dtype="float64")
+    got = gmm.w4a16_rows(wl.lhs_bits[rows], wl.rhs_e2m1, wl.scale_codes, wl.group_sizes, rows, cols)
+    np.testing.assert_allclose(got, full[np.ix_(rows, cols)], rtol=1e-13, atol=1e-9)
+
+
 def test_gmm_acceptance_policy(rng):
     K = 512
     lhs, nib, codes, exps, scale, gs = _tiny_gmm_case(rng, [40, 24], K=K, N=32)
