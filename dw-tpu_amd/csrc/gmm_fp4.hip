@@ -324,14 +324,14 @@ __global__ __launch_bounds__(C::THREADS) void gmm_fp4_ws_kernel(
     const uint8_t *__restrict__ wpk,
     const uint8_t *__restrict__ spk, const int32_t *__restrict__ group_sizes, int num_groups,
     const int32_t *__restrict__ group_offset, int64_t e_local, int N, void *__restrict__ out,
-    int out_f32, GmmEpilogue ep, int ncu) {
+    int out_f32, GmmEpilogue ep, int ncu, int bal) {
   constexpr int CW = C::CONS;
   constexpr int NC = 2 * MB;  // tile classes: 16-row blocks holding rows
   static_assert(MB == 3, "consumer variants are written for 96-row tiles");
   static_assert(C::STAGES * C::STAGE >= (kMaxGroups + NC * kClsStride) * 4, "tile classes alias the stages");
   static_assert(C::GT % (2 * C::NPROD) == 0, "a narrow tile's groups split evenly over the producers");
   __shared__ __attribute__((aligned(1024))) uint8_t s_lds[C::STAGES * C::STAGE];
-  __shared__ int s_info[3];
+  __shared__ int s_info[4];
   int *s_rowstart = (int *)s_lds;
   int *s_cls = s_rowstart + kMaxGroups;
 
@@ -341,8 +341,8 @@ __global__ __launch_bounds__(C::THREADS) void gmm_fp4_ws_kernel(
   const int n_tiles = (G + C::GT - 1) / C::GT;
   const int n_tiles_n = NARROW ? (G + C::GT / 2 - 1) / (C::GT / 2) : 0;
   TileRef ref;
-  if (!find_tile<MB, 16, C::THREADS>(group_sizes, num_groups, go, e_local, M, n_tiles, n_tiles_n, ncu, s_rowstart,
-                                     s_cls, s_info, ref))
+  if (!find_tile<MB, 16, C::THREADS>(group_sizes, num_groups, go, e_local, M, n_tiles, n_tiles_n, ncu, bal,
+                                     s_rowstart, s_cls, s_info, ref))
     return;
   const int g = ref.g, nt = ref.nt, rows = ref.rows;
   const bool narrow = NARROW && ref.narrow;
@@ -445,7 +445,7 @@ template <int MB, int CW, int JW, int NP, int NS, bool ACT, bool NARROW>
 static int launch_gmm_ws(const uint16_t *lhs, const int32_t *row_idx, int64_t lhs_rows, int64_t M, int64_t K,
                          const uint8_t *w, const uint8_t *s,
                          const int32_t *gs, int ng, const int32_t *go, int64_t e_local, int64_t N, void *out,
-                         int out_f32, const GmmEpilogue &ep, int ncu, hipStream_t st) {
+                         int out_f32, const GmmEpilogue &ep, int ncu, int bal, hipStream_t st) {
   using C = WsCfg<MB, CW, JW, NP, NS>;
   constexpr int MT = 32 * MB, NT = C::NT, NC = 2 * MB;
   const int64_t n_tiles = (N + NT - 1) / NT;
@@ -457,9 +457,13 @@ static int launch_gmm_ws(const uint16_t *lhs, const int32_t *row_idx, int64_t lh
   DWM_UNSUPPORTED_IF(grid > (1ll << 31) - 1, "gmm_fp4: too many tiles (%lld)", (long long)grid);
   DWM_UNSUPPORTED_IF(K > (1 << 24), "gmm_fp4: K <= 2^24 required");
   hipLaunchKernelGGL((gmm_fp4_ws_kernel<C, MB, ACT, NARROW>), dim3((unsigned)grid), dim3(C::THREADS), 0, st, lhs,
-                     row_idx, lhs_rows, M, (int)K, w, s, gs, ng, go, e_local, (int)N, out, out_f32, ep, ncu);
+                     row_idx, lhs_rows, M, (int)K, w, s, gs, ng, go, e_local, (int)N, out, out_f32, ep, ncu, bal);
   return launch_status("gmm_fp4");
 }
+
+// Groups of 2 .. kGmmBalancedTiles row tiles split their rows evenly, and
+// their row tiles of one column tile run side by side on one XCD (find_tile).
+constexpr int kGmmBalancedTiles = 4;
 
 // The bf16 grouped matmul (arguments checked by the caller).
 int launch_gmm_bf16(const uint16_t *lhs, const int32_t *row_idx, int64_t lhs_rows, int64_t M, int64_t K,
@@ -477,7 +481,7 @@ int launch_gmm_bf16(const uint16_t *lhs, const int32_t *row_idx, int64_t lhs_row
   const bool narrow = ((M + 95) / 96) * ((N + 511) / 512) < ncu;
 #define DWM_GMM_WS(ACT, NARROW)                                                                                   \
   launch_gmm_ws<3, 8, 2, 4, 4, ACT, NARROW>(lhs, row_idx, lhs_rows, M, K, weight, scale, group_sizes, num_groups, \
-                                             group_offset, E_local, N, out, out_f32, ep, ncu, st)
+                                             group_offset, E_local, N, out, out_f32, ep, ncu, kGmmBalancedTiles, st)
   if (gated) return narrow ? DWM_GMM_WS(true, true) : DWM_GMM_WS(true, false);
   return narrow ? DWM_GMM_WS(false, true) : DWM_GMM_WS(false, false);
 #undef DWM_GMM_WS

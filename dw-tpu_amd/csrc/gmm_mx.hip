@@ -375,14 +375,14 @@ __global__ __launch_bounds__(C::THREADS) void gmm_mx_kernel(
   constexpr int CW = C::CONS, NP = C::NPROD, TMB = C::TMB, CMB = C::CMB;
   static_assert(C::STAGES * C::STAGE >= (kMaxGroups + TMB * kClsStride) * 4, "tile classes alias the stages");
   __shared__ __attribute__((aligned(1024))) uint8_t s_lds[C::STAGES * C::STAGE];
-  __shared__ int s_info[3];
+  __shared__ int s_info[4];
   int *s_rowstart = (int *)s_lds;
   int *s_cls = s_rowstart + kMaxGroups;
 
   const int tid = threadIdx.x, wave = tid >> 6;
   const int go = group_offset ? group_offset[0] : 0;
   TileRef ref;
-  if (!find_tile<TMB, 32, C::THREADS>(group_sizes, num_groups, go, e_local, M, (N + C::NT - 1) / C::NT, 0, 0,
+  if (!find_tile<TMB, 32, C::THREADS>(group_sizes, num_groups, go, e_local, M, (N + C::NT - 1) / C::NT, 0, 0, 0,
                                       s_rowstart, s_cls, s_info, ref))
     return;
   const int g = ref.g, nt = ref.nt, rows = ref.rows;
@@ -606,14 +606,14 @@ __global__ __launch_bounds__(C::THREADS) void gmm_mx128_kernel(
   constexpr int CW = C::CONS, NP = C::NPROD;
   static_assert(C::STAGES * C::STAGE >= (kMaxGroups + MB * kClsStride) * 4, "tile classes alias the stages");
   __shared__ __attribute__((aligned(1024))) uint8_t s_lds[C::STAGES * C::STAGE];
-  __shared__ int s_info[3];
+  __shared__ int s_info[4];
   int *s_rowstart = (int *)s_lds;
   int *s_cls = s_rowstart + kMaxGroups;
   const int tid = threadIdx.x, wave = tid >> 6;
   const int go = group_offset ? group_offset[0] : 0;
   TileRef ref;
-  if (!find_tile<MB, 32, C::THREADS>(group_sizes, num_groups, go, e_local, M, (N + C::NT - 1) / C::NT, 0, 0, s_rowstart,
-                                 s_cls, s_info, ref))
+  if (!find_tile<MB, 32, C::THREADS>(group_sizes, num_groups, go, e_local, M, (N + C::NT - 1) / C::NT, 0, 0, 0,
+                                 s_rowstart, s_cls, s_info, ref))
     return;
   const int g = ref.g, nt = ref.nt, rows = ref.rows;
   const int64_t row0 = ref.row0;

@@ -19,11 +19,36 @@ constexpr float kSwigluLimit = 10.0f;  // DeepSeek V4 swiglu_limit of silu_and_m
 // class (index 0 = NC blocks, largest first), the exclusive prefix over groups
 // of that class's row tiles; s_cls[a * kClsStride + num_groups] is the class
 // total.
+//
+// Balanced groups (bal > 0): a group of n = ceil(sz / MT) row tiles with
+// 2 <= n <= bal splits its nb = ceil(sz / CG) blocks evenly instead: tile tt
+// holds nb / n blocks, one more for tt < nb % n (only the last block of the
+// group is partial).  All n tiles are listed in the class of the largest, and
+// a group's entries run (column tile, row tile) with the row tile innermost,
+// so the n row tiles of one column tile are adjacent in one XCD's run: they
+// run together and stream the expert's weights through that XCD's L2 once
+// (a 96-row tile plus a small one would run at different times and each read
+// the weights from HBM).  Each row's result depends only on its own lhs row
+// and expert (every 16-row block sums K in the same grouping), so the split
+// does not change any output bit.
 constexpr int kClsStride = kMaxGroups + 1;
+
+template <int MT, int CG>
+struct RowSplit {
+  // Tiles, blocks and the largest tile's block count of a local group of sz rows.
+  int n, nb, top;
+  bool bal;
+  __device__ __forceinline__ RowSplit(int sz, int bal_max) {  // sz >= 0; no sum that could overflow int32
+    n = sz / MT + (sz % MT != 0 ? 1 : 0);
+    nb = sz / CG + (sz % CG != 0 ? 1 : 0);
+    bal = n >= 2 && n <= bal_max;
+    top = bal ? (nb + n - 1) / n : 0;
+  }
+};
 
 template <int MB, int CG>
 __device__ __forceinline__ void tile_classes(const int32_t *group_sizes, int num_groups, int go, int64_t e_local,
-                                             int *s_rowstart, int *s_cls) {
+                                             int bal, int *s_rowstart, int *s_cls) {
   constexpr int MT = 32 * MB, NC = MT / CG;
   static_assert(NC * CG == MT, "class granularity divides the tile");
   const int lane = threadIdx.x & 63;
@@ -37,15 +62,17 @@ __device__ __forceinline__ void tile_classes(const int32_t *group_sizes, int num
       int sz = g < num_groups ? group_sizes[g] : 0;
       sz = sz > 0 ? sz : 0;
       const bool local = g >= go && (int64_t)g < (int64_t)go + e_local;
-      const int n_full = local ? sz / MT : 0;
-      const int rem = local ? sz % MT : 0;
+      const RowSplit<MT, CG> sp(local ? sz : 0, bal);
+      const int n_full = local && !sp.bal ? sz / MT : 0;
+      const int rem = local && !sp.bal ? sz % MT : 0;
       const int rem_cls = (rem + CG - 1) / CG;  // 0 when there is no partial tile
       const int ri = wave_inclusive_scan(sz);
       if (g < num_groups) s_rowstart[g] = row_carry + ri - sz;
       row_carry += __shfl(ri, 63, 64);
 #pragma unroll
       for (int a = 0; a < NC; ++a) {
-        const int cnt = (a == 0 ? n_full : 0) + (rem_cls == NC - a ? 1 : 0);
+        const int cnt = sp.bal ? (sp.top == NC - a ? sp.n : 0)
+                               : (a == 0 ? n_full : 0) + (rem_cls == NC - a ? 1 : 0);
         const int ci = wave_inclusive_scan(cnt);
         if (g < num_groups) s_cls[a * kClsStride + g] = carry[a] + ci - cnt;
         carry[a] += __shfl(ci, 63, 64);
@@ -79,11 +106,11 @@ struct TileRef {
 // idle CUs.  Returns false when the block has no tile.
 template <int MB, int CG, int THREADS>
 __device__ __forceinline__ bool find_tile(const int32_t *__restrict__ group_sizes, int num_groups, int go,
-                                          int64_t e_local, int64_t M, int n_tiles, int n_tiles_n, int ncu,
+                                          int64_t e_local, int64_t M, int n_tiles, int n_tiles_n, int ncu, int bal,
                                           int *s_rowstart, int *s_cls, int *s_info, TileRef &ref) {
   constexpr int MT = 32 * MB, NC = MT / CG;
   const int tid = threadIdx.x;
-  tile_classes<MB, CG>(group_sizes, num_groups, go, e_local, s_rowstart, s_cls);
+  tile_classes<MB, CG>(group_sizes, num_groups, go, e_local, bal, s_rowstart, s_cls);
   if (tid == 0) s_info[0] = -1;
   __syncthreads();
   int nsplit = 0;
@@ -130,19 +157,33 @@ __device__ __forceinline__ bool find_tile(const int32_t *__restrict__ group_size
     for (int g = tid; g < num_groups; g += THREADS) {
       if (cs[g] <= trow && trow < cs[g + 1]) {
         const int sz = group_sizes[g];
-        // Class 0 holds the full tiles (then a partial one of NC blocks);
-        // the other classes hold one partial tile per group.
-        const int tt = cls == 0 ? trow - cs[g] : sz / MT;
+        const RowSplit<MT, CG> sp(sz, bal);
         s_info[0] = g;
-        s_info[1] = s_rowstart[g] + tt * MT;
-        s_info[2] = min(MT, sz - tt * MT);
+        if (sp.bal) {
+          // (column tile, row tile) with the row tile innermost; tile tt
+          // starts after tt * base + min(tt, extra) blocks.
+          const int64_t local = entry - (int64_t)cs[g] * per_row;
+          const int tt = (int)(local % sp.n);
+          const int base = sp.nb / sp.n, extra = sp.nb % sp.n;
+          const int b0 = tt * base + min(tt, extra);
+          s_info[1] = s_rowstart[g] + CG * b0;
+          s_info[2] = min(CG * (base + (tt < extra ? 1 : 0)), sz - CG * b0);
+          s_info[3] = (int)(local / sp.n);
+        } else {
+          // Class 0 holds the full tiles (then a partial one of NC blocks);
+          // the other classes hold one partial tile per group.
+          const int tt = cls == 0 ? trow - cs[g] : sz / MT;
+          s_info[1] = s_rowstart[g] + tt * MT;
+          s_info[2] = min(MT, sz - tt * MT);
+          s_info[3] = (int)(entry % per_row);
+        }
       }
     }
   }
   __syncthreads();  // also retires the class reads before the stages overwrite them
   ref.g = s_info[0];
   if (cls < 0 || ref.g < 0) return false;
-  ref.nt = (int)(entry % per_row);
+  ref.nt = s_info[3];
   ref.narrow = cls < nsplit;
   ref.row0 = s_info[1];
   // group_sizes lives on the device and is not checked by the host: sizes
