@@ -221,6 +221,90 @@ __device__ __forceinline__ void ws_consumer(int T, uint8_t *s_lds, int cw, int64
 #pragma unroll
     for (int i = 0; i < nb; ++i) an[i] = *(const u32x4_t *)(st + arow + (3 * rg + i) * 2048 + ach);
   };
+  if constexpr (NH >= 3 && NH <= 5) {
+  // Decode ahead (3 to 5 row blocks, where the registers allow it): the B
+  // operands of each half step (MFMA step v) are decoded during the previous
+  // half step.  Its last MFMA group -- three row blocks, so three MFMAs
+  // cover each column block's decode -- runs column block by column block,
+  // and right after the last MFMA that reads bop[u] the next half step's
+  // bop[u] is decoded in its place, so after a barrier the MFMAs start at
+  // once.  The next K step's weights and scales are read at the end of this
+  // step's v = 0 half.  Row groups: blocks [0, G0) then [G0, NH).
+  constexpr int G0 = NH - 3, DRG = G0 > 0 ? 2 : 1;
+  u32x4_t bop[4];
+  auto decode = [&](int u, int v, int parity) {
+    const float sc = __builtin_bit_cast(float, __builtin_amdgcn_ubfe(sn[u & 1], 16 * parity + 8 * (u >> 1), 8) << 23);
+    bop[u][0] = cvt_fp4x2_bf16<0>(wn[u][v], sc);
+    bop[u][1] = cvt_fp4x2_bf16<1>(wn[u][v], sc);
+    bop[u][2] = cvt_fp4x2_bf16<2>(wn[u][v], sc);
+    bop[u][3] = cvt_fp4x2_bf16<3>(wn[u][v], sc);
+  };
+  // lhs fragments of row group g of MFMA step v
+  auto read_g = [&](const uint8_t *st, int v, int g) {
+    const int ach = ((qk + 2 * v) ^ x) << 4;
+    const int b0 = (DRG == 2 && g == 1) ? G0 : 0;
+    const int nb = (DRG == 2 && g == 0) ? G0 : 3;
+#pragma unroll
+    for (int i = 0; i < nb; ++i) an[i] = *(const u32x4_t *)(st + arow + (b0 + i) * 2048 + ach);
+  };
+  static_assert(NS % 2 == 0, "t & 1 == cur & 1");
+  for (int t0 = 0; t0 < T; t0 += NS) {
+#pragma unroll
+  for (int cur = 0; cur < NS; ++cur) {
+    const int t = t0 + cur;
+    if (t >= T) break;
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    const uint8_t *const st = s_lds + cur * C::STAGE;
+    const int nxt = cur == NS - 1 ? 0 : cur + 1;
+    // Step t + 1 was published at this barrier (stale contents in the last step, never used).
+    const uint8_t *const sx = s_lds + nxt * C::STAGE;
+    if (t == 0) {
+      read_w(st);
+      read_g(st, 0, 0);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) decode(u, 0, 0);
+    }
+#pragma unroll
+    for (int v = 0; v < 2; ++v) {
+#pragma unroll
+      for (int rg = 0; rg < DRG; ++rg) {
+        const int nb = (DRG == 2 && rg == 0) ? G0 : 3;
+        const int b0 = (DRG == 2 && rg == 1) ? G0 : 0;
+        u32x4_t a[3];
+#pragma unroll
+        for (int i = 0; i < nb; ++i) a[i] = an[i];
+        __builtin_amdgcn_sched_barrier(0);
+        if (rg + 1 < DRG) read_g(st, v, rg + 1);
+        else if (v == 0) read_g(st, 1, 0);
+        else read_g(sx, 0, 0);
+        if (rg + 1 < DRG) {
+#pragma unroll
+          for (int i = 0; i < nb; ++i)
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+              acc[b0 + i][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                  __builtin_bit_cast(bf16x8_t, a[i]), __builtin_bit_cast(bf16x8_t, bop[u]), acc[b0 + i][u], 0, 0, 0);
+        } else {
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+#pragma unroll
+            for (int i = 0; i < nb; ++i)
+              acc[b0 + i][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                  __builtin_bit_cast(bf16x8_t, a[i]), __builtin_bit_cast(bf16x8_t, bop[u]), acc[b0 + i][u], 0, 0, 0);
+            decode(u, v == 0 ? 1 : 0, v == 0 ? (cur & 1) : ((cur + 1) & 1));
+            __builtin_amdgcn_sched_barrier(0);  // keep each decode after the MFMAs that read the old bop[u]
+          }
+          if (v == 0) read_w(sx);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  }
+  }
+  } else {
   // Steps in runs of NS, one per stage, so that every stage address is a
   // constant offset (cur = t % NS is known in each copy of the body).
   static_assert(NS % 2 == 0, "t & 1 == cur & 1");
@@ -281,6 +365,7 @@ __device__ __forceinline__ void ws_consumer(int T, uint8_t *s_lds, int cw, int64
         __builtin_amdgcn_sched_barrier(0);
       }
     }
+  }
   }
   }
   // One more barrier: every wave is done with the stages and every load has
