@@ -105,9 +105,12 @@ __global__ void fp4_decode_kernel(const uint8_t *packed, int format, int64_t nby
 // j * N/2 + 32 g + c: half 0 of every group is 32 gate columns and half 1 the
 // matching up columns of a [w1 | w3] weight, so the kernel's fused activation
 // finds both in one wave.
+// transposed: rhs is [E, N, K/2] (two K values per byte, low nibble = even
+// k) instead of [E, K, N/2].
 __global__ void gmm_fp4_prepack_kernel(const uint8_t *rhs, int format, const void *scale,
                                        int scale_dtype, int64_t E, int64_t K, int64_t N,
-                                       uint8_t *wout, uint8_t *sout, int32_t *flags, int gate_up) {
+                                       uint8_t *wout, uint8_t *sout, int32_t *flags, int gate_up,
+                                       int transposed) {
   const int64_t G = (N + 63) / 64, KB = K / 128, T = K / 64;
   int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t total = E * G * KB * 64;
@@ -139,8 +142,9 @@ __global__ void gmm_fp4_prepack_kernel(const uint8_t *rhs, int format, const voi
 #pragma unroll
           for (int i = 0; i < 8; ++i) {
             const int64_t k = k0 + 8 * w + i;
-            const uint32_t byte = rhs[(e * K + k) * half_n + (n >> 1)];
-            uint32_t nib = (n & 1) ? (byte >> 4) : (byte & 0xFu);
+            const uint32_t byte = transposed ? rhs[(e * N + n) * (K / 2) + (k >> 1)]
+                                             : rhs[(e * K + k) * half_n + (n >> 1)];
+            uint32_t nib = ((transposed ? k : n) & 1) ? (byte >> 4) : (byte & 0xFu);
             nib = format == DWM_FP4_CODES ? code_to_e2m1(nib, &bad_code) : canon_e2m1(nib);
             if (code == 0u) nib &= 8u;  // zero scale: keep only the sign -> +-0
             word |= nib << (4 * i);
@@ -208,7 +212,7 @@ extern "C" int dwm_gmm_fp4_prepack_size(int64_t E, int64_t K, int64_t N, int64_t
 
 static int gmm_fp4_prepack_impl(const uint8_t *rhs, int format, const void *scale, int scale_dtype, int64_t E,
                                 int64_t K, int64_t N, uint8_t *weight_out, uint8_t *scale_out, int32_t *flags,
-                                int gate_up, void *stream) {
+                                int gate_up, int transposed, void *stream) {
   int64_t wb, sb;
   int st = dwm_gmm_fp4_prepack_size(E, K, N, &wb, &sb);
   if (st != DWM_OK) return st;
@@ -223,7 +227,7 @@ static int gmm_fp4_prepack_impl(const uint8_t *rhs, int format, const void *scal
   const int64_t blocks = (total + 255) / 256;
   DWM_CHECK_ARG(blocks < (1ll << 31), "gmm_fp4_prepack: too large");
   hipLaunchKernelGGL(gmm_fp4_prepack_kernel, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream), rhs, format,
-                     scale, scale_dtype, E, K, N, weight_out, scale_out, flags, gate_up);
+                     scale, scale_dtype, E, K, N, weight_out, scale_out, flags, gate_up, transposed);
   return launch_status("gmm_fp4_prepack");
 }
 
@@ -231,11 +235,18 @@ extern "C" int dwm_gmm_fp4_prepack(const uint8_t *rhs, int format, const void *s
                                    int scale_dtype, int64_t E, int64_t K, int64_t N,
                                    uint8_t *weight_out, uint8_t *scale_out, int32_t *flags,
                                    void *stream) {
-  return gmm_fp4_prepack_impl(rhs, format, scale, scale_dtype, E, K, N, weight_out, scale_out, flags, 0, stream);
+  return gmm_fp4_prepack_impl(rhs, format, scale, scale_dtype, E, K, N, weight_out, scale_out, flags, 0, 0, stream);
 }
 
 extern "C" int dwm_gmm_fp4_prepack_gate_up(const uint8_t *rhs, int format, const void *scale, int scale_dtype,
                                            int64_t E, int64_t K, int64_t N, uint8_t *weight_out,
                                            uint8_t *scale_out, int32_t *flags, void *stream) {
-  return gmm_fp4_prepack_impl(rhs, format, scale, scale_dtype, E, K, N, weight_out, scale_out, flags, 1, stream);
+  return gmm_fp4_prepack_impl(rhs, format, scale, scale_dtype, E, K, N, weight_out, scale_out, flags, 1, 0, stream);
+}
+
+extern "C" int dwm_gmm_fp4_prepack_transposed(const uint8_t *rhs, int format, const void *scale, int scale_dtype,
+                                              int64_t E, int64_t K, int64_t N, int gate_up, uint8_t *weight_out,
+                                              uint8_t *scale_out, int32_t *flags, void *stream) {
+  return gmm_fp4_prepack_impl(rhs, format, scale, scale_dtype, E, K, N, weight_out, scale_out, flags,
+                              gate_up ? 1 : 0, 1, stream);
 }

@@ -40,6 +40,7 @@ SIGNATURES = {
     "dwm_gmm_fp4_prepack_size": [_i64, _i64, _i64, _p, _p],
     "dwm_gmm_fp4_prepack": [_p, _i32, _p, _i32, _i64, _i64, _i64, _p, _p, _p, _p],
     "dwm_gmm_fp4_prepack_gate_up": [_p, _i32, _p, _i32, _i64, _i64, _i64, _p, _p, _p, _p],
+    "dwm_gmm_fp4_prepack_transposed": [_p, _i32, _p, _i32, _i64, _i64, _i64, _i32, _p, _p, _p, _p],
     "dwm_gmm_fp4": [_p, _i64, _i64, _p, _p, _p, _i32, _p, _i64, _i64, _p, _i32, _i32, _i32, _p],
     "dwm_gmm_fp4_gather": [_p, _i64, _p, _i64, _i64, _p, _p, _p, _i32, _p, _i64, _i64, _p, _i32, _i32, _i32, _p],
     "dwm_gmm_fp4_ex": [_p, _i64, _i64, _p, _p, _p, _i32, _p, _i32, _p, _i64, _i64, _p, _i32, _i32, _i32, _p],

@@ -169,13 +169,16 @@ class Fp4Weight:
 
 
 def prepack_fp4(rhs: torch.Tensor, rhs_scale: torch.Tensor, rhs_fp4_codes: bool = False,
-                gate_up: bool = False) -> Fp4Weight:
+                gate_up: bool = False, transpose_rhs: bool = False) -> Fp4Weight:
     """One-time relayout of packed fp4 expert weights and their scales.
 
     rhs: [E, K, N/2] packed bytes -- e2m1 nibbles (uint8 or
-    float4_e2m1fn_x2), or gmm_v2 codes when ``rhs_fp4_codes``.
-    rhs_scale: [E, K/32, 1, N] or [E, K/32, N]: uint8 e8m0 codes, or f32 /
-    bf16 powers of two (the lossless e8m0 set, e8m0_scale.py:25-34).
+    float4_e2m1fn_x2), or gmm_v2 codes when ``rhs_fp4_codes``; with
+    ``transpose_rhs`` the transposed weight [E, N, K/2] (two K values per
+    byte, low nibble = even k).
+    rhs_scale: [E, K/32, 1, N] or [E, K/32, N] in either case: uint8 e8m0
+    codes, or f32 / bf16 powers of two (the lossless e8m0 set,
+    e8m0_scale.py:25-34).
     ``gate_up``: rhs is a [w1 | w3] gate/up weight for the fused activation
     (N % 64 == 0).  Synchronises the stream once to check the scales (load time).
     """
@@ -184,9 +187,14 @@ def prepack_fp4(rhs: torch.Tensor, rhs_scale: torch.Tensor, rhs_fp4_codes: bool 
     src = _as_bytes(rhs).contiguous()
     _lib.require_cuda(src, rhs_scale)
     if src.dim() != 3:
-        raise ValueError(f"rhs must be [E, K, N/2] packed bytes, got shape {tuple(src.shape)}")
-    e, k, half_n = src.shape
-    n = 2 * half_n
+        raise ValueError(f"rhs must be [E, {'N, K/2' if transpose_rhs else 'K, N/2'}] packed bytes, "
+                         f"got shape {tuple(src.shape)}")
+    if transpose_rhs:
+        e, n, half_k = src.shape
+        k = 2 * half_k
+    else:
+        e, k, half_n = src.shape
+        n = 2 * half_n
     if rhs_scale is None:
         raise ValueError("fp4 weights need block scales")
     sc = rhs_scale
@@ -205,9 +213,14 @@ def prepack_fp4(rhs: torch.Tensor, rhs_scale: torch.Tensor, rhs_fp4_codes: bool 
     sout = torch.zeros(sb.value, dtype=torch.uint8, device=src.device)
     flags = torch.zeros(1, dtype=torch.int32, device=src.device)
     fmt = _lib.FP4_CODES if rhs_fp4_codes else _lib.FP4_E2M1
-    entry = "dwm_gmm_fp4_prepack_gate_up" if gate_up else "dwm_gmm_fp4_prepack"
-    _lib.call(entry, _lib.ptr(src), fmt, _lib.ptr(sc), _lib.dtype_code(sc.dtype), e, k, n,
-              _lib.ptr(wout), _lib.ptr(sout), _lib.ptr(flags), _lib.stream_handle(src.device))
+    if transpose_rhs:
+        _lib.call("dwm_gmm_fp4_prepack_transposed", _lib.ptr(src), fmt, _lib.ptr(sc), _lib.dtype_code(sc.dtype), e,
+                  k, n, 1 if gate_up else 0, _lib.ptr(wout), _lib.ptr(sout), _lib.ptr(flags),
+                  _lib.stream_handle(src.device))
+    else:
+        entry = "dwm_gmm_fp4_prepack_gate_up" if gate_up else "dwm_gmm_fp4_prepack"
+        _lib.call(entry, _lib.ptr(src), fmt, _lib.ptr(sc), _lib.dtype_code(sc.dtype), e, k, n,
+                  _lib.ptr(wout), _lib.ptr(sout), _lib.ptr(flags), _lib.stream_handle(src.device))
     f = int(flags.item())
     if f & 1:
         raise ValueError("rhs_scale holds a value that is not +0.0 or a power of two in the e8m0 range "
@@ -234,10 +247,10 @@ def clear_prepack_cache():
         _prepack_cache.clear()
 
 
-def _prepack_cached(rhs, rhs_scale, rhs_fp4_codes, gate_up):
+def _prepack_cached(rhs, rhs_scale, rhs_fp4_codes, gate_up, transpose_rhs=False):
     if rhs_scale is None:
-        return prepack_fp4(rhs, rhs_scale, rhs_fp4_codes=rhs_fp4_codes, gate_up=gate_up)
-    key = (id(rhs), id(rhs_scale), bool(rhs_fp4_codes), bool(gate_up))
+        return prepack_fp4(rhs, rhs_scale, rhs_fp4_codes=rhs_fp4_codes, gate_up=gate_up, transpose_rhs=transpose_rhs)
+    key = (id(rhs), id(rhs_scale), bool(rhs_fp4_codes), bool(gate_up), bool(transpose_rhs))
     with _prepack_lock:
         hit = _prepack_cache.get(key)
         if hit is not None:
@@ -246,7 +259,7 @@ def _prepack_cached(rhs, rhs_scale, rhs_fp4_codes, gate_up):
                 _prepack_cache.move_to_end(key)
                 return w
             del _prepack_cache[key]
-    w = prepack_fp4(rhs, rhs_scale, rhs_fp4_codes=rhs_fp4_codes, gate_up=gate_up)
+    w = prepack_fp4(rhs, rhs_scale, rhs_fp4_codes=rhs_fp4_codes, gate_up=gate_up, transpose_rhs=transpose_rhs)
     with _prepack_lock:
         _prepack_cache[key] = (weakref.ref(rhs), weakref.ref(rhs_scale), rhs._version, rhs_scale._version, w)
         while len(_prepack_cache) > _PREPACK_CACHE_SIZE:
@@ -292,7 +305,10 @@ def gmm_v2(lhs: torch.Tensor,
     ``rhs_bias`` ([E, N] or [E, 1, N], f32 or bf16, in the weight's column
     order) is added to the f32 accumulators of each expert's rows before the
     activation and the rounding.  Tiling / VMEM arguments of the TPU kernel
-    are accepted and ignored.
+    are accepted and ignored.  ``transpose_rhs`` (raw weights only): rhs is
+    stored transposed, [E, N, K/2] packed along K, and is transposed once
+    when it is prepacked (``prepack_fp4``); a prepacked ``Fp4Weight``
+    already carries its layout.
 
     ``lhs_row_indices`` (an addition; int32 [M] device tensor): row r of the
     grouped operand is ``lhs[lhs_row_indices[r]]`` (JAX gather index
@@ -309,8 +325,6 @@ def gmm_v2(lhs: torch.Tensor,
     if fuse_act not in _lib.FUSE_ACTS:
         raise NotImplementedError(f"gmm_v2: fused activation {fuse_act!r} is not supported")
     fused = fuse_act is not None
-    if transpose_rhs:
-        raise NotImplementedError("gmm_v2: transpose_rhs is not supported")
     if lhs_quant_dtype is not None and lhs_quant_dtype not in (E4M3, "float8_e4m3fn"):
         raise NotImplementedError(f"gmm_v2: lhs_quant_dtype {lhs_quant_dtype!r}: only float8_e4m3fn (MX) is supported")
     mx = lhs_quant_dtype is not None or isinstance(lhs, MxLhs)
@@ -319,7 +333,7 @@ def gmm_v2(lhs: torch.Tensor,
             raise ValueError("gmm_v2: a prepacked Fp4Weight carries its own scales; pass rhs_scale=None")
         w = rhs
     else:
-        w = _prepack_cached(rhs, rhs_scale, rhs_fp4_codes, fused)
+        w = _prepack_cached(rhs, rhs_scale, rhs_fp4_codes, fused, transpose_rhs)
     if w.gate_up != fused:
         raise ValueError("gmm_v2: gate/up-prepacked weights run only (and always) with the fused activation"
                          if w.gate_up else "gmm_v2: the fused activation needs weights prepacked with gate_up=True")

@@ -136,6 +136,17 @@ int dwm_gmm_fp4_prepack_gate_up(const uint8_t *rhs, int format, const void *scal
                                 int64_t E, int64_t K, int64_t N, uint8_t *weight_out,
                                 uint8_t *scale_out, int32_t *flags, void *stream);
 
+/* dwm_gmm_fp4_prepack (gate_up = 0) or dwm_gmm_fp4_prepack_gate_up
+ * (gate_up != 0) from a transposed weight: rhs is [E, N, K/2] bytes, two K
+ * values per byte (low nibble = even k), the layout gmm_v2(...,
+ * transpose_rhs=True) takes (patches/tokamax/0001-gmm_v2-fp4-emulation-
+ * v6e.patch:64-65, :111); scale keeps the [E, K/32, N] layout above.  The
+ * prepacked output is the same bytes the untransposed weight gives, so the
+ * grouped matmul runs unchanged (the transpose happens once, at load). */
+int dwm_gmm_fp4_prepack_transposed(const uint8_t *rhs, int format, const void *scale, int scale_dtype,
+                                   int64_t E, int64_t K, int64_t N, int gate_up, uint8_t *weight_out,
+                                   uint8_t *scale_out, int32_t *flags, void *stream);
+
 /* Ragged grouped matmul on prepacked weights:
  *   for g in [group_offset, group_offset + E_local):
  *     out[off_g : off_g + size_g] = lhs[off_g : off_g + size_g] @ dequant(rhs[g - group_offset])

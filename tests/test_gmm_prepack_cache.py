@@ -11,8 +11,8 @@ g = importlib.import_module("dw_tpu_amd.gmm_v2")  # the package attribute gmm_v2
 def test_prepack_cache_hits_and_misses(monkeypatch):
     calls = []
 
-    def fake_prepack(rhs, rhs_scale, rhs_fp4_codes=False, gate_up=False):
-        calls.append((id(rhs), rhs_fp4_codes, gate_up))
+    def fake_prepack(rhs, rhs_scale, rhs_fp4_codes=False, gate_up=False, transpose_rhs=False):
+        calls.append((id(rhs), rhs_fp4_codes, gate_up, transpose_rhs))
         return object()
 
     monkeypatch.setattr(g, "prepack_fp4", fake_prepack)
@@ -22,6 +22,8 @@ def test_prepack_cache_hits_and_misses(monkeypatch):
     w1 = g._prepack_cached(rhs, sc, True, False)
     assert g._prepack_cached(rhs, sc, True, False) is w1 and len(calls) == 1
     assert g._prepack_cached(rhs, sc, True, True) is not w1 and len(calls) == 2  # gate/up layout
+    assert g._prepack_cached(rhs, sc, True, False, True) is not w1 and len(calls) == 3  # transposed source
+    calls.pop()
     rhs.add_(1)  # in place: the version counter moves
     w3 = g._prepack_cached(rhs, sc, True, False)
     assert w3 is not w1 and len(calls) == 3

@@ -376,3 +376,40 @@ def test_gmm_many_groups_window(dev, rng, mx, num_groups, go, e_local):
     assert written.sum() == sizes[go:go + e_local].sum()
     assert np.all(y[~written] == 0)
     assert np.all(np.abs(y - y64)[written] <= bound[written])
+
+
+def _transpose_packed(rhs):
+    """[E, K, N/2] bytes (low nibble = even n) -> [E, N, K/2] (low nibble = even k)."""
+    nib = np.stack([rhs & 0xF, rhs >> 4], axis=-1).reshape(rhs.shape[0], rhs.shape[1], -1)  # [E, K, N]
+    t = np.ascontiguousarray(nib.transpose(0, 2, 1))  # [E, N, K]
+    return (t[..., 0::2] | (t[..., 1::2] << 4)).astype(np.uint8)
+
+
+@pytest.mark.parametrize("codes,gate_up", [(False, False), (True, False), (False, True)])
+def test_transpose_rhs_prepacks_the_same_weight(dev, rng, codes, gate_up):
+    """gmm_v2(transpose_rhs=True) (patches/tokamax/0001-...:64-65, 111):
+    rhs stored [E, N, K/2] prepacks to the same bytes as the untransposed
+    weight, and the grouped matmul gives the same bits."""
+    from dw_tpu_amd import gmm_v2
+    from dw_tpu_amd.gmm_v2 import prepack_fp4
+    E, K, N = 5, 512, 384
+    sizes = [40, 0, 97, 3, 60]
+    lhs_bits = bf16_bits_np(rng.standard_normal((sum(sizes), K)).astype(np.float32))
+    rhs = rng.integers(0, 256, (E, K, N // 2), dtype=np.uint8)
+    if codes:  # uint4 codes never hold 8 (q = -8)
+        rhs = np.where((rhs & 0xF) == 8, rhs ^ 0x1, rhs)
+        rhs = np.where((rhs >> 4) == 8, rhs ^ 0x10, rhs).astype(np.uint8)
+    sc = torch.from_numpy(rng.integers(123, 130, (E, K // 32, 1, N), dtype=np.uint8)).to(dev)
+    r = torch.from_numpy(rhs).to(dev)
+    rt = torch.from_numpy(_transpose_packed(rhs)).to(dev)
+    assert tuple(rt.shape) == (E, N, K // 2)
+    a = prepack_fp4(r, sc, rhs_fp4_codes=codes, gate_up=gate_up)
+    b = prepack_fp4(rt, sc, rhs_fp4_codes=codes, gate_up=gate_up, transpose_rhs=True)
+    assert torch.equal(a.weight, b.weight) and torch.equal(a.scale, b.scale)
+    lhs = bf16_tensor(lhs_bits, dev)
+    gs = torch.tensor(sizes, dtype=torch.int32, device=dev)
+    act = "silu_and_mul_with_clamp" if gate_up else None
+    y = gmm_v2(lhs, r, gs, sc, fuse_act=act, rhs_fp4_codes=codes)
+    yt = gmm_v2(lhs, rt, gs, sc, fuse_act=act, rhs_fp4_codes=codes, transpose_rhs=True)
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int16), yt.view(torch.int16))
