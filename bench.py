@@ -18,14 +18,16 @@ fp4 weights, bf16 MFMA).
 combine, prefill) the same way, each gmm workload again in the MX mode
 (`<name>_mx`: e4m3 lhs with e8m0 block-32 scales on the scaled MFMA, a
 lossier computation, with the quantization kernel timed alone and with the
-gmm), the expert block, dense FP8, router and format kernels.
+gmm; `<name>_mxfp4`: the same with an e2m1 lhs, fp4 x fp4, lossier still),
+the expert block, dense FP8, router and format kernels.
 `cpu_baseline` times the numpy oracle of the same math on a bounded sample of
 experts on this host's cores (and one expert on one thread), the same for
 prefill and a dense GEMM, and reports the max abs and relative Frobenius
 error of one expert's GPU output rows against the oracle's float64 product.
-The same leg adds `vs_w4a16` to each `<name>_mx` line: the MX output's max
-abs and relative Frobenius distance from the reference's W4A16 result
-(float64, sampled rows and columns), the lhs quantization included.
+The same leg adds `vs_w4a16` to each `<name>_mx` / `<name>_mxfp4` line:
+the output's max abs and relative Frobenius distance from the reference's
+W4A16 result (float64, sampled rows and columns), the lhs quantization
+included.
 
 The headline is timed last, right after the `extra` workloads (its inputs
 are in HBM beforehand), so that the GPU runs at the clock it holds under
@@ -54,7 +56,9 @@ METRIC = "FP4 MoE gmm TFLOP/s + HBM GB/s (% of peak) at decode & prefill sizes"
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 FP8_PEAK_TFLOPS = 5000.0
+FP4_PEAK_TFLOPS = 10100.0
 ONLY_CHOICES = ("decode_gate_up", "decode_down", "prefill", "decode_gate_up_mx", "decode_down_mx", "prefill_mx",
+                "decode_gate_up_mxfp4", "decode_down_mxfp4", "prefill_mxfp4",
                 "dense_M1", "dense_M16", "dense_M128", "dense_M1024", "dense_M4096")
 MALL_BYTES = 256 * 2 ** 20
 HEADLINE_SAMPLES = 9  # timed samples of the headline; value is their median
@@ -75,7 +79,8 @@ class GmmBench:
 
     mode "bf16": dwm_gmm_fp4 (the reference's W4A16 arithmetic); mode "mx":
     dwm_gmm_fp4_mx on the lhs quantized once beforehand (e4m3 codes + e8m0
-    block-32 scales), and ``quant_step`` times that quantization."""
+    block-32 scales); mode "mxfp4": dwm_gmm_fp4_mxfp4 on an e2m1 lhs.
+    ``quant_step`` times the quantization."""
 
     def __init__(self, wl, dev, copies, mode="bf16"):
         import torch
@@ -93,12 +98,14 @@ class GmmBench:
         self.stream = _lib.stream_handle(dev)
         P = ctypes.c_void_p
         self.args = []
-        if mode == "mx":
-            self.mx = mx_quantize(self.lhs[0])
+        if mode in ("mx", "mxfp4"):
+            fmt = "e2m1" if mode == "mxfp4" else "e4m3"
+            self.mx = mx_quantize(self.lhs[0], fmt)
             self.qcodes = torch.empty_like(self.mx.codes)
             self.qscales = torch.empty_like(self.mx.scales)
             self.quant_args = (P(self.lhs[0].data_ptr()), wl.M, wl.K, P(self.qcodes.data_ptr()),
                                P(self.qscales.data_ptr()), self.stream)
+            self.quant_fn = self.lib.dwm_mx_quant_e2m1 if mode == "mxfp4" else self.lib.dwm_mx_quant_e4m3
         for i in range(copies):
             w = self.weights[i]
             tail = (P(w.weight.data_ptr()), P(w.scale.data_ptr()), P(self.gs.data_ptr()), wl.E, None, wl.E, wl.N,
@@ -106,9 +113,12 @@ class GmmBench:
             if mode == "mx":
                 self.args.append((P(self.mx.codes.data_ptr()), P(self.mx.scales.data_ptr()), wl.M, None, wl.M,
                                   wl.K) + tail)
+            elif mode == "mxfp4":  # no bias: (weight, scale, bias NULL, bias dtype 0, ...)
+                self.args.append((P(self.mx.codes.data_ptr()), P(self.mx.scales.data_ptr()), wl.M, None, wl.M,
+                                  wl.K) + tail[:2] + (None, 0) + tail[2:])
             else:
                 self.args.append((P(self.lhs[i].data_ptr()), wl.M, wl.K) + tail)
-        self.fn = self.lib.dwm_gmm_fp4_mx if mode == "mx" else self.lib.dwm_gmm_fp4
+        self.fn = {"mx": self.lib.dwm_gmm_fp4_mx, "mxfp4": self.lib.dwm_gmm_fp4_mxfp4}.get(mode, self.lib.dwm_gmm_fp4)
 
     def step(self, i):
         rc = self.fn(*self.args[i % len(self.args)])
@@ -116,7 +126,7 @@ class GmmBench:
             raise RuntimeError(self.lib.dwm_last_error().decode())
 
     def quant_step(self, i):
-        rc = self.lib.dwm_mx_quant_e4m3(*self.quant_args)
+        rc = self.quant_fn(*self.quant_args)
         if rc:
             raise RuntimeError(self.lib.dwm_last_error().decode())
 
@@ -156,6 +166,8 @@ def gmm_result(wl, ms, mode="bf16"):
     bts = wl.algorithmic_bytes()
     if mode == "mx":
         bts += wl.M * wl.K // 32 - wl.M * wl.K  # e4m3 codes + scales in place of bf16
+    elif mode == "mxfp4":
+        bts += wl.M * wl.K // 32 - wl.M * wl.K * 3 // 2  # e2m1 codes + scales in place of bf16
     fl = wl.flops()
     gbs = bts / (ms * 1e-3) / 1e9
     tfl = fl / (ms * 1e-3) / 1e12
@@ -163,6 +175,10 @@ def gmm_result(wl, ms, mode="bf16"):
     if mode == "mx":
         r["mfma_fp8_frac"] = round(tfl / FP8_PEAK_TFLOPS, 4)
         r["dtype"] = "e4m3 lhs (e8m0 block-32 scales) x e2m1 weights, scaled MFMA, f32 accumulate"
+    elif mode == "mxfp4":
+        r["mfma_fp4_frac"] = round(tfl / FP4_PEAK_TFLOPS, 4)
+        r["mfma_fp8_frac"] = round(tfl / FP8_PEAK_TFLOPS, 4)
+        r["dtype"] = "e2m1 lhs (e8m0 block-32 scales) x e2m1 weights, scaled MFMA, f32 accumulate"
     else:
         r["mfma_bf16_frac"] = round(tfl / BF16_PEAK_TFLOPS, 4)
     r.update({"bytes": bts, "flops": fl, "M": wl.M, "K": wl.K, "N": wl.N, "E": wl.E,
@@ -193,7 +209,7 @@ def prep_gmm(name, dev, steps, warmup):
     return run
 
 
-def prep_gmm_mx(name, dev, steps, warmup, keep=None):
+def prep_gmm_mx(name, dev, steps, warmup, keep=None, mode="mx"):
     """The MX mode of one gmm workload: the gmm on the quantized lhs, the
     lhs quantization (bf16 [M, K] -> e4m3 + scales), and the two back to back
     (what gmm_v2(lhs_quant_dtype=float8_e4m3fn) runs on a bf16 lhs).  With
@@ -201,25 +217,25 @@ def prep_gmm_mx(name, dev, steps, warmup, keep=None):
     gmm) for the CPU leg's distance from the W4A16 result."""
     from dw_tpu_amd.workloads import make_gmm_workload
     wl = make_gmm_workload(name)
-    b = GmmBench(wl, dev, copies_for(wl), "mx")
+    b = GmmBench(wl, dev, copies_for(wl), mode)
 
     def run():
-        r = gmm_result(wl, time_median(b.step, steps, warmup), "mx")
+        r = gmm_result(wl, time_median(b.step, steps, warmup), mode)
         if keep is not None:
-            keep[name] = (wl, b.out[0])
+            keep[f"{name}_{mode}"] = (wl, b.out[0])
         q_ms = time_steps(b.quant_step, steps, warmup)
-        qb = wl.M * wl.K * 2 + wl.M * wl.K + wl.M * wl.K // 32
+        qb = wl.M * wl.K * 2 + (wl.M * wl.K // 2 if mode == "mxfp4" else wl.M * wl.K) + wl.M * wl.K // 32
         r["quant"] = {"ms": round(q_ms, 5), "GB_s": round(qb / (q_ms * 1e-3) / 1e9, 1),
                       "hbm_frac": round(qb / (q_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "bytes": qb}
         both = time_steps(b.quant_and_step, steps, warmup)
         r["ms_with_quant"] = round(both, 5)
         r["TFLOP_s_with_quant"] = round(wl.flops() / (both * 1e-3) / 1e12, 1)
-        return {f"{name}_mx": r}
+        return {f"{name}_{mode}": r}
     return run
 
 
-def bench_gmm_mx(name, dev, steps, warmup):
-    return prep_gmm_mx(name, dev, steps, warmup)()[f"{name}_mx"]
+def bench_gmm_mx(name, dev, steps, warmup, mode="mx"):
+    return prep_gmm_mx(name, dev, steps, warmup, mode=mode)()[f"{name}_{mode}"]
 
 
 def prep_dispatch_combine(dev, steps, warmup):
@@ -770,11 +786,13 @@ def main():
         log("calib copy: 3 x 1 GiB device-to-device copies done")
         return
     if args.only:
-        name = args.only[:-3] if args.only.endswith("_mx") else args.only
+        name = args.only.rsplit("_mx", 1)[0] if "_mx" in args.only else args.only
         if args.only.startswith("dense_M"):
             r = prep_dense(dev, args.steps, args.warmup, ms_list=(int(args.only[len("dense_M"):]),))()
         elif args.only.endswith("_mx"):
             r = bench_gmm_mx(name, dev, args.steps, args.warmup)
+        elif args.only.endswith("_mxfp4"):
+            r = bench_gmm_mx(name, dev, args.steps, args.warmup, mode="mxfp4")
         else:
             wl1, _, ms1 = bench_gmm(name, dev, args.steps, args.warmup)
             r = gmm_result(wl1, ms1)
@@ -809,6 +827,8 @@ def main():
             # power-limited level first (with 5 the MX prefill measured
             # 1.65 ms against 1.55 ms after a settled clock).
             runs.append(prep_gmm_mx(name, dev, args.steps, max(args.warmup, 60), mx_out))
+            log(f"bench: inputs of {name} gmm, MXFP4 lhs")
+            runs.append(prep_gmm_mx(name, dev, args.steps, args.warmup, mx_out, mode="mxfp4"))
             log(f"bench: inputs of {name} gmm")
             runs.append(prep_gmm(name, dev, args.steps, args.warmup))
         for label, prep in (("moe block", prep_moe_block), ("dense fp8", prep_dense),
@@ -819,6 +839,7 @@ def main():
         for name in ("decode_down", "decode_gate_up"):
             log(f"bench: inputs of {name} gmm, MX mode")
             runs.append(prep_gmm_mx(name, dev, args.steps, args.warmup, mx_out))
+            runs.append(prep_gmm_mx(name, dev, args.steps, args.warmup, mx_out, mode="mxfp4"))
         # The last region runs at least 200 warmup launches (~30 ms of
         # decode-type load): after memory-bound regions the power manager
         # can hold the clock low for tens of milliseconds, and a
@@ -850,8 +871,8 @@ def main():
         log("bench: cpu baseline")
         cpu = cpu_gmm_baseline(wl, args.cpu_budget, gpu_check)
         if mx_out:
-            for name, d in cpu_mx_distance(mx_out).items():
-                extra[f"{name}_mx"]["vs_w4a16"] = d
+            for key, d in cpu_mx_distance(mx_out).items():
+                extra[key]["vs_w4a16"] = d
         mx_out.clear()
         if args.extra == "all":
             from dw_tpu_amd.workloads import make_gmm_workload

@@ -573,12 +573,13 @@ int launch_gmm_bf16(const uint16_t *lhs, const int32_t *row_idx, int64_t lhs_row
 }
 
 // Checks shared by every form of the grouped matmul, then the launch.
+// lhs_fp4: the MX lhs is e2m1 codes [rows, K / 2] (MXFP4) instead of e4m3.
 static int gmm_run(const dwm_gmm_lhs &L, int64_t M, int64_t K, const uint8_t *weight, const uint8_t *scale,
                    const void *bias, int bias_dtype, const int32_t *group_sizes, int num_groups,
                    const int32_t *group_offset, int64_t E_local, int64_t N, void *out, int out_dtype, int zero_init,
-                   int fuse_act, void *stream) {
+                   int fuse_act, void *stream, bool lhs_fp4 = false) {
   const bool mx = L.scale != nullptr;
-  const char *const what = mx ? "gmm_fp4_mx" : (L.row_idx ? "gmm_fp4_gather" : "gmm_fp4");
+  const char *const what = lhs_fp4 ? "gmm_fp4_mxfp4" : mx ? "gmm_fp4_mx" : (L.row_idx ? "gmm_fp4_gather" : "gmm_fp4");
   DWM_CHECK_ARG(M >= 0 && K > 0 && N > 0 && E_local >= 0 && num_groups >= 0 && L.rows >= 0,
                 "%s: bad sizes M=%lld K=%lld N=%lld E_local=%lld groups=%d lhs_rows=%lld", what, (long long)M,
                 (long long)K, (long long)N, (long long)E_local, num_groups, (long long)L.rows);
@@ -596,7 +597,7 @@ static int gmm_run(const dwm_gmm_lhs &L, int64_t M, int64_t K, const uint8_t *we
   DWM_CHECK_ARG(L.data && out && (num_groups == 0 || group_sizes) && (!L.row_idx || L.rows > 0),
                 "%s: null pointer or empty lhs with rows to read", what);
   // The MX kernels and the fused gather address lhs rows with 32-bit byte offsets.
-  DWM_UNSUPPORTED_IF((mx || L.row_idx) && L.rows * K * (mx ? 1 : 2) >= (1ll << 32),
+  DWM_UNSUPPORTED_IF((mx || L.row_idx) && L.rows * K * (lhs_fp4 ? 1 : mx ? 2 : 4) >= (1ll << 33),
                      "%s: lhs of %lld rows is too large", what, (long long)L.rows);
   DWM_CHECK_ARG(E_local == 0 || (weight && scale), "%s: null weight pointer", what);
   DWM_CHECK_ARG((uintptr_t)L.data % 16 == 0 && (uintptr_t)weight % 16 == 0 && (uintptr_t)out % 16 == 0 &&
@@ -616,7 +617,7 @@ static int gmm_run(const dwm_gmm_lhs &L, int64_t M, int64_t K, const uint8_t *we
   const bool gated = fuse_act != DWM_ACT_NONE;
   if (mx)
     return launch_gmm_mx((const uint8_t *)L.data, L.scale, L.row_idx, L.rows, M, K, weight, scale, group_sizes,
-                         num_groups, group_offset, E_local, N, out, out_f32, gated, ep, st);
+                         num_groups, group_offset, E_local, N, out, out_f32, gated, ep, st, lhs_fp4);
   return launch_gmm_bf16((const uint16_t *)L.data, L.row_idx, L.rows, M, K, weight, scale, group_sizes, num_groups,
                          group_offset, E_local, N, out, out_f32, gated, ep, st);
 }
@@ -657,6 +658,19 @@ extern "C" int dwm_gmm_fp4_gather(const uint16_t *lhs, int64_t lhs_rows, const i
   const dwm_gmm_lhs L{lhs, nullptr, lhs_rows, row_idx};
   return gmm_run(L, M, K, weight, scale, nullptr, 0, group_sizes, num_groups, group_offset, E_local, N, out,
                  out_dtype, zero_init, fuse_act, stream);
+}
+
+extern "C" int dwm_gmm_fp4_mxfp4(const uint8_t *lhs, const uint8_t *lhs_scale, int64_t lhs_rows,
+                                 const int32_t *row_idx, int64_t M, int64_t K, const uint8_t *weight,
+                                 const uint8_t *scale, const void *rhs_bias, int bias_dtype,
+                                 const int32_t *group_sizes, int num_groups, const int32_t *group_offset,
+                                 int64_t E_local, int64_t N, void *out, int out_dtype, int zero_init, int fuse_act,
+                                 void *stream) {
+  clear_error();
+  DWM_CHECK_ARG(lhs_scale || M == 0, "gmm_fp4_mxfp4: null lhs_scale");
+  const dwm_gmm_lhs L{lhs, lhs_scale ? lhs_scale : (const uint8_t *)lhs, lhs_rows, row_idx};
+  return gmm_run(L, M, K, weight, scale, rhs_bias, bias_dtype, group_sizes, num_groups, group_offset, E_local, N,
+                 out, out_dtype, zero_init, fuse_act, stream, true);
 }
 
 extern "C" int dwm_gmm_fp4_mx(const uint8_t *lhs, const uint8_t *lhs_scale, int64_t lhs_rows, const int32_t *row_idx,

@@ -102,6 +102,68 @@ __global__ __launch_bounds__(256) void mx_quant_e4m3_kernel(const uint16_t *__re
   }
 }
 
+// MXFP4 lhs: the smallest e >= -126 with a <= 6 * 2^e, for finite a >= 0
+// (a = (1 + m / 2^23) 2^(ef - 127) <= 1.5 * 2^(2 + e)).
+__device__ __forceinline__ int mx_exponent_e2m1(float a) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, a);
+  const int ef = (int)(u >> 23);
+  if (ef == 0) return kMxMinExp;  // zero or subnormal: far below 6 * 2^-126
+  const int e = ef - 129 + ((u & 0x7FFFFFu) > 0x400000u ? 1 : 0);
+  return e < kMxMinExp ? kMxMinExp : e;
+}
+
+// |q| <= 6 -> e2m1 nibble, round to nearest even (magnitudes 0, .5, 1, 1.5
+// in steps of .5, then 2, 3, 4 in steps of 1, then 4, 6; every difference
+// below is exact), sign in bit 3.
+__device__ __forceinline__ uint32_t f32_e2m1(float q) {
+  const float a = fabsf(q);
+  uint32_t c;
+  if (a < 2.0f) c = (uint32_t)__builtin_rintf(a * 2.0f);
+  else if (a < 4.0f) c = 4u + (uint32_t)__builtin_rintf(a - 2.0f);
+  else c = 6u + (uint32_t)__builtin_rintf((a - 4.0f) * 0.5f);
+  return c | ((__builtin_bit_cast(uint32_t, q) >> 28) & 8u);
+}
+
+// bf16 [rows, K] -> e2m1 codes [rows, K / 2] (value 2 j in the low nibble
+// of byte j) + e8m0 scale codes [rows, K / 32]: per 32-value block the
+// exponent of mx_exponent_e2m1(absmax), codes = RNE e2m1 of x * 2^-e (exact
+// rescale); a block holding a NaN or an infinity gets codes 0 and scale code
+// 255.  Thread i handles values 8 i .. 8 i + 7 (4 threads per block).
+__global__ __launch_bounds__(256) void mx_quant_e2m1_kernel(const uint16_t *__restrict__ x, int64_t n8,
+                                                            uint8_t *__restrict__ codes,
+                                                            uint8_t *__restrict__ scales) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n8; i += stride) {
+    const u32x4_t raw = __builtin_nontemporal_load((const u32x4_t *)(x + 8 * i));
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[2 * j] = bf16_bits_to_f32(raw[j] & 0xFFFFu);
+      v[2 * j + 1] = bf16_bits_to_f32(raw[j] >> 16);
+    }
+    float amax = 0.0f;
+    int bad = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float a = fabsf(v[j]);
+      bad |= !(a <= 3.4028234663852886e38f);  // NaN or infinity
+      amax = fmaxf(amax, bad ? 0.0f : a);
+    }
+    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+    bad |= __shfl_xor(bad, 1, 64);
+    bad |= __shfl_xor(bad, 2, 64);
+    const int e = mx_exponent_e2m1(amax);
+    uint32_t w = 0u;
+    if (!bad) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) w |= f32_e2m1(ldexpf(v[j], -e)) << (4 * j);  // exact: |x 2^-e| <= 6
+    }
+    *(uint32_t *)(codes + 4 * i) = w;
+    if ((i & 3) == 0) scales[i >> 2] = (uint8_t)(bad ? 255 : e + 127);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // The MX tile kernel.
 
@@ -109,26 +171,32 @@ __global__ __launch_bounds__(256) void mx_quant_e4m3_kernel(const uint16_t *__re
 // columns), consumer cw owning column group cw % GT of row half cw / GT (the
 // two consumers of a SIMD, cw and cw + 4, then hold both halves).  A group
 // of up to 192 rows then reads its weights once, not once per 96 rows.
-template <int MB, int CW, int NP, int NS, int RH = 1>
+// AF4: the lhs is e2m1 (MXFP4: 32 bytes per row and 64-deep step, one
+// 16-byte A operand per lane, A format 4 in the MFMA) instead of e4m3 (64
+// bytes per row and step).
+template <int MB, int CW, int NP, int NS, int RH = 1, bool AF4 = false>
 struct MxCfg {
   static constexpr int CONS = CW, NPROD = NP, STAGES = NS, HALVES = RH;
+  static constexpr bool A_FP4 = AF4;
   static constexpr int GT = CW / RH;                     // 64-column groups per tile
   static constexpr int THREADS = 64 * (CW + NP);
   static constexpr int NT = 64 * GT;
   static constexpr int CMB = MB;                         // 32-row blocks of one consumer
   static constexpr int TMB = MB * RH;                    // 32-row blocks of the tile
   static constexpr int ROWS = 32 * TMB;
+  static constexpr int AB = AF4 ? 32 : 64;               // lhs bytes per row and step
+  static constexpr int RL = 1024 / AB;                   // rows per 1 KiB lhs load
   static constexpr int W = 0;                            // group i: 2 KiB at W + 2048 i
-  static constexpr int A = GT * 2048;                    // ROWS x 64 bytes
-  static constexpr int AS = A + ROWS * 64;               // 128-row groups x 256 bytes (dword per row)
+  static constexpr int A = GT * 2048;                    // ROWS x AB bytes
+  static constexpr int AS = A + ROWS * AB;               // 128-row groups x 256 bytes (dword per row)
   static constexpr int AS_LOADS = (ROWS + 63) / 64;      // 256-byte row-scale loads per even step
   static constexpr int S = AS + AS_LOADS * 256;          // group i: 256 bytes at S + 256 i
   static constexpr int STAGE = S + GT * 256;
-  static constexpr int A_GROUPS = ROWS / 16;             // 1 KiB lhs loads (16 rows) per step
+  static constexpr int A_GROUPS = ROWS / RL;             // 1 KiB lhs loads (RL rows) per step
   static constexpr int G_LOADS = GT / NP;                // weight groups per producer
   static constexpr int AHEAD = 2;                        // steps published per barrier
   static constexpr int EP_STRIDE = 72;
-  static_assert(ROWS % 16 == 0 && G_LOADS * NP == GT && GT * RH == CW, "load split");
+  static_assert(ROWS % RL == 0 && G_LOADS * NP == GT && GT * RH == CW, "load split");
   static_assert(AS_LOADS <= NP, "one row-scale load per producer at most");
   static constexpr int INFLIGHT = NS - 1 - AHEAD;        // steps loading behind the published pair
   static_assert(INFLIGHT >= 1, "stage count");
@@ -136,6 +204,11 @@ struct MxCfg {
 };
 
 __device__ __forceinline__ int mx_swizzle(int r) { return (r >> 2) & 3; }
+// e2m1 rows hold two 16-byte chunks: rows r and r + 8 of one LDS cycle's 16
+// swap them, so the cycle's 16 reads hit 16 distinct 16-byte bank groups.
+__device__ __forceinline__ int mx_swizzle4(int r) { return (r >> 3) & 1; }
+template <class C>
+__device__ __forceinline__ int mx_swz(int r) { return C::A_FP4 ? mx_swizzle4(r) : mx_swizzle(r); }
 
 // Producer wave pw: its lhs row groups are pw, pw + NP, ... (< A_GROUPS); NA
 // of them hold rows of the tile (the others are zero in every stage).
@@ -171,13 +244,15 @@ __device__ __forceinline__ void mx_producer(const uint8_t *__restrict__ lhs, con
     const int rs = r < rows ? r : rows - 1;
     return row_idx ? gather_index(row_idx[row0 + rs], lhs_rows) : row0 + rs;
   };
-  // lhs load i: rows 16 (pw + NP i) .. + 15; lane l fills physical chunk
-  // l % 4 of row + l / 4 with the logical chunk of the swizzle.
+  // lhs load i: rows RL (pw + NP i) .. + RL - 1; lane l fills physical
+  // chunk l % LPR of row + l / LPR with the logical chunk of the swizzle.
+  constexpr int LPR = C::AB / 16;                 // 16-byte chunks per row and step
+  const int64_t KR = C::A_FP4 ? K / 2 : K;        // lhs bytes per row
   uint32_t aoff[NA > 0 ? NA : 1];
 #pragma unroll
   for (int i = 0; i < NA; ++i) {
-    const int r = 16 * (pw + NP * i) + (lane >> 2);
-    aoff[i] = (uint32_t)(src_row(r) * K) + (uint32_t)(((lane & 3) ^ mx_swizzle(r)) << 4);
+    const int r = C::RL * (pw + NP * i) + lane / LPR;
+    aoff[i] = (uint32_t)(src_row(r) * KR) + (uint32_t)(((lane % LPR) ^ mx_swz<C>(r)) << 4);
   }
   const int aspart = pw - (NP - C::AS_LOADS);  // row-scale load of producers NP - AS_LOADS .. NP - 1
   const uint32_t asoff = ASL ? (uint32_t)(src_row(64 * aspart + lane) * KS) : 0u;
@@ -191,7 +266,7 @@ __device__ __forceinline__ void mx_producer(const uint8_t *__restrict__ lhs, con
   }
   auto issue = [&](int stage, int t) {
     uint8_t *const st = s_lds + stage * C::STAGE;
-    const uint8_t *const a = lhs + (int64_t)t * 64;
+    const uint8_t *const a = lhs + (int64_t)t * C::AB;
 #pragma unroll
     for (int i = 0; i < NA; ++i)
       __builtin_amdgcn_global_load_lds((const void *)(a + aoff[i]),
@@ -253,10 +328,11 @@ __device__ __forceinline__ void mx_consumer(int T, uint8_t *s_lds, int cw, int c
   const int woff = C::W + cg * 2048 + lane * 16;
   const int soff = C::S + cg * 256 + lane * 4;
   // A fragment of row block mb: row rb + mb * 32 + c32 (same swizzle for all
-  // mb, rb % 16 == 0), logical chunks h and 2 + h.
-  const int sw = mx_swizzle(c32);
-  const int alo = C::A + (rb + c32) * 64 + ((h ^ sw) << 4);
-  const int ahi = C::A + (rb + c32) * 64 + (((2 + h) ^ sw) << 4);
+  // mb, rb % 16 == 0), logical chunks h and 2 + h (e4m3: k = 16 h .. + 15
+  // and 32 + 16 h .. + 15), or chunk h alone (e2m1: k = 32 h .. + 31).
+  const int sw = mx_swz<C>(c32);
+  const int alo = C::A + (rb + c32) * C::AB + ((h ^ sw) << 4);
+  const int ahi = C::A + (rb + c32) * C::AB + (((2 + h) ^ sw) << 4);
   u32x4_t wn[2];
   uint32_t sn = 0, asn[AM];
   i32x8_t an;
@@ -270,9 +346,13 @@ __device__ __forceinline__ void mx_consumer(int T, uint8_t *s_lds, int cw, int c
     for (int mb = 0; mb < AM; ++mb) asn[mb] = *(const uint32_t *)(st + C::AS + (rb + mb * 32 + c32) * 4);
   };
   auto read_a = [&](const uint8_t *st, int mb) {
-    const u32x4_t lo = *(const u32x4_t *)(st + alo + mb * 32 * 64);
-    const u32x4_t hi = *(const u32x4_t *)(st + ahi + mb * 32 * 64);
-    an = i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+    const u32x4_t lo = *(const u32x4_t *)(st + alo + mb * 32 * C::AB);
+    if constexpr (C::A_FP4) {
+      an = i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], 0, 0, 0, 0};
+    } else {
+      const u32x4_t hi = *(const u32x4_t *)(st + ahi + mb * 32 * C::AB);
+      an = i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+    }
   };
   uint32_t sw_cur = 0, sa_cur[AM];
 #pragma unroll
@@ -324,8 +404,9 @@ __device__ __forceinline__ void mx_consumer(int T, uint8_t *s_lds, int cw, int c
         read_w(sx);
         if ((t & 1) == 1) read_s(sx);
       }
-      acc[mb][0] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b0, acc[mb][0], 0, 4, 0, sa, 0, sb);
-      acc[mb][1] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b1, acc[mb][1], 0, 4, 0, sa, 1, sb);
+      constexpr int AFMT = C::A_FP4 ? 4 : 0;  // A operand format: e2m1 or e4m3 (B: e2m1)
+      acc[mb][0] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b0, acc[mb][0], AFMT, 4, 0, sa, 0, sb);
+      acc[mb][1] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b1, acc[mb][1], AFMT, 4, 0, sa, 1, sb);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
@@ -394,9 +475,9 @@ __global__ __launch_bounds__(C::THREADS) void gmm_mx_kernel(
     const int pw = wave - CW;
     const uint8_t *const wexp = wpk + e * G * T * 2048;
     const uint8_t *const sexp = spk + e * G * KB * 256;
-    // Row groups pw + NP i (< A_GROUPS) with 16 (pw + NP i) < rows are loaded.
+    // Row groups pw + NP i (< A_GROUPS) with RL (pw + NP i) < rows are loaded.
     int na = 0;
-    for (int ga = pw; ga < C::A_GROUPS; ga += NP) na += 16 * ga < rows ? 1 : 0;
+    for (int ga = pw; ga < C::A_GROUPS; ga += NP) na += C::RL * ga < rows ? 1 : 0;
     const bool asl = pw >= NP - C::AS_LOADS;
     mx_produce<C>(na, asl, lhs, lsc, row_idx, lhs_rows, row0, rows, K, T, KB, wexp, sexp, g0, G, s_lds, pw);
     return;
@@ -674,7 +755,7 @@ static int launch_mx(const uint8_t *lhs, const uint8_t *lsc, const int32_t *row_
 int launch_gmm_mx(const uint8_t *lhs, const uint8_t *lhs_scale, const int32_t *row_idx, int64_t lhs_rows, int64_t M,
                   int64_t K, const uint8_t *weight, const uint8_t *scale, const int32_t *group_sizes, int num_groups,
                   const int32_t *group_offset, int64_t E_local, int64_t N, void *out, int out_f32, bool gated,
-                  const GmmEpilogue &ep, hipStream_t st) {
+                  const GmmEpilogue &ep, hipStream_t st, bool lhs_fp4) {
   // 96-row x 512-column tiles, 8 consumer + 4 producer waves.  64-deep K
   // steps in a five-stage ring (two published per barrier, two in flight),
   // or 128-deep steps in a three-stage ring (one published, one in flight).
@@ -686,11 +767,19 @@ int launch_gmm_mx(const uint8_t *lhs, const uint8_t *lhs_scale, const int32_t *r
   using C64 = MxCfg<3, 8, 4, 5>;
   using C64H = MxCfg<3, 8, 4, 5, 2>;
   using C128 = Mx128Cfg<3, 8, 4, 3>;
-  const bool deep = K >= kMx128MinK;
+  // MXFP4 lhs: the 64-deep kernel at every K (its stages are 22 KB), with
+  // the same row-half stacking.
+  using F64 = MxCfg<3, 8, 4, 5, 1, true>;
+  using F64H = MxCfg<3, 8, 4, 5, 2, true>;
+  const bool deep = !lhs_fp4 && K >= kMx128MinK;
   const bool halves = !deep && M > 96 * E_local && M <= 192 * E_local;
 #define DWM_MX(CFG, TMB, ACT, DEEP)                                                                                \
   launch_mx<CFG, TMB, ACT, DEEP>(lhs, lhs_scale, row_idx, lhs_rows, M, K, weight, scale, group_sizes, num_groups, \
                                  group_offset, E_local, N, out, out_f32, ep, st)
+  if (lhs_fp4) {
+    if (gated) return halves ? DWM_MX(F64H, 6, true, false) : DWM_MX(F64, 3, true, false);
+    return halves ? DWM_MX(F64H, 6, false, false) : DWM_MX(F64, 3, false, false);
+  }
   if (gated)
     return deep ? DWM_MX(C128, 3, true, true) : halves ? DWM_MX(C64H, 6, true, false) : DWM_MX(C64, 3, true, false);
   return deep ? DWM_MX(C128, 3, false, true) : halves ? DWM_MX(C64H, 6, false, false) : DWM_MX(C64, 3, false, false);
@@ -700,6 +789,23 @@ int launch_gmm_mx(const uint8_t *lhs, const uint8_t *lhs_scale, const int32_t *r
 }  // namespace dwm
 
 using namespace dwm;
+
+extern "C" int dwm_mx_quant_e2m1(const uint16_t *x, int64_t rows, int64_t K, uint8_t *codes, uint8_t *scales,
+                                 void *stream) {
+  clear_error();
+  DWM_CHECK_ARG(rows >= 0 && K > 0, "mx_quant_e2m1: bad sizes rows=%lld K=%lld", (long long)rows, (long long)K);
+  DWM_UNSUPPORTED_IF(K % kMxBlock != 0, "mx_quant_e2m1: K %% 32 == 0 required (K=%lld)", (long long)K);
+  if (rows == 0) return DWM_OK;
+  DWM_CHECK_ARG(x && codes && scales, "mx_quant_e2m1: null pointer");
+  DWM_CHECK_ARG((uintptr_t)x % 16 == 0 && (uintptr_t)codes % 4 == 0,
+                "mx_quant_e2m1: x must be 16-byte and codes 4-byte aligned");
+  const int64_t n8 = rows * K / 8;
+  int64_t blocks = (n8 + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  hipLaunchKernelGGL(mx_quant_e2m1_kernel, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream), x, n8, codes,
+                     scales);
+  return launch_status("mx_quant_e2m1");
+}
 
 extern "C" int dwm_mx_quant_e4m3(const uint16_t *x, int64_t rows, int64_t K, uint8_t *codes, uint8_t *scales,
                                  void *stream) {

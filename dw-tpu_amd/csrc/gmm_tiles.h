@@ -390,6 +390,6 @@ int launch_gmm_bf16(const uint16_t *lhs, const int32_t *row_idx, int64_t lhs_row
 int launch_gmm_mx(const uint8_t *lhs, const uint8_t *lhs_scale, const int32_t *row_idx, int64_t lhs_rows, int64_t M,
                   int64_t K, const uint8_t *weight, const uint8_t *scale, const int32_t *group_sizes, int num_groups,
                   const int32_t *group_offset, int64_t E_local, int64_t N, void *out, int out_f32, bool gated,
-                  const GmmEpilogue &ep, hipStream_t st);
+                  const GmmEpilogue &ep, hipStream_t st, bool lhs_fp4 = false);
 
 }  // namespace dwm

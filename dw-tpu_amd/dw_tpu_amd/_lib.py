@@ -46,6 +46,9 @@ SIGNATURES = {
     "dwm_gmm_fp4_ex": [_p, _i64, _i64, _p, _p, _p, _i32, _p, _i32, _p, _i64, _i64, _p, _i32, _i32, _i32, _p],
     "dwm_mx_quant_e4m3": [_p, _i64, _i64, _p, _p, _p],
     "dwm_gmm_fp4_mx": [_p, _p, _i64, _p, _i64, _i64, _p, _p, _p, _i32, _p, _i64, _i64, _p, _i32, _i32, _i32, _p],
+    "dwm_mx_quant_e2m1": [_p, _i64, _i64, _p, _p, _p],
+    "dwm_gmm_fp4_mxfp4": [_p, _p, _i64, _p, _i64, _i64, _p, _p, _p, _i32, _p, _i32, _p, _i64, _i64, _p, _i32, _i32,
+                          _i32, _p],
     "dwm_moe_dispatch_workspace_size": [_i64, _i32, _p],
     "dwm_moe_dispatch": [_p, _i64, _i32, _i32, _p, _p, _p, _p, _p, _p, _p, _p],
     "dwm_moe_dispatch_noalloc": [_p, _i64, _i32, _i32, _p, _p, _p, _p, _p, _p, _p],

@@ -9,8 +9,9 @@ time so that gmm_v2 does not re-encode them per call.  Here the load-time step
 is ``prepack_fp4`` (and ``fused_moe_gmm.fp4_weight_to_codes``), which also
 takes the block scales and returns an ``Fp4Weight`` in the K-major layout the
 gfx950 kernel streams with 16-byte loads.  ``gmm_v2`` accepts an ``Fp4Weight``
-directly; a raw packed weight tensor is prepacked on every call (a full pass
-over all experts, as the reference's per-call re-encoding is).
+directly; a raw packed weight tensor is prepacked (a full pass over all
+experts, as the reference's per-call re-encoding is) on its first call, and
+the prepacked copy is reused while the raw tensors are alive and unchanged.
 
 Tensor conventions (torch has no uint4): a 4-bit array of shape [..., N] is a
 uint8 tensor [..., N/2] with element 2j in the low nibble, or a
@@ -23,8 +24,12 @@ patches/tpu-inference/0001-dsv4-v6e-enablement.patch:315-350, at block 32)
 and contracts it with the fp4 weights on the gfx950 scaled MFMA -- the lhs
 quantization tokamax performs for chips with a native low-precision matrix
 path (patches/tokamax/0001-...:89-100).  An ``MxLhs`` (already quantized)
-may be passed as ``lhs`` directly.  The default (no lhs_quant_dtype) keeps
-the reference's W4A16 arithmetic: bf16 lhs, weights decoded exactly.
+may be passed as ``lhs`` directly.  ``lhs_quant_dtype=float4_e2m1fn`` (or
+``torch.float4_e2m1fn_x2``) quantizes the lhs to e2m1 instead (MXFP4, the
+same block-32 power-of-two quantizer at the e2m1 range) and runs the scaled
+MFMA with both operands fp4: lossier still, and also opt-in.  The default
+(no lhs_quant_dtype) keeps the reference's W4A16 arithmetic: bf16 lhs,
+weights decoded exactly.
 """
 import collections
 import ctypes
@@ -41,17 +46,25 @@ E4M3 = torch.float8_e4m3fn
 MX_BLOCK = 32
 
 
+# e2m1 magnitudes by code (bit 3 is the sign).
+_E2M1_MAGS = (0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0)
+MX_FORMATS = ("e4m3", "e2m1")
+
+
 @dataclass(frozen=True)
 class MxLhs:
     """An lhs quantized for the MX mode: ``codes`` uint8 [rows, K] (e4m3 bit
-    patterns) and ``scales`` uint8 [rows, K/32] (e8m0 exponent codes, value
-    2^(code - 127))."""
+    patterns) or, with ``fmt`` "e2m1" (MXFP4), uint8 [rows, K/2] (two e2m1
+    codes per byte, element 2 j in the low nibble); ``scales`` uint8
+    [rows, K/32] (e8m0 exponent codes, value 2^(code - 127))."""
     codes: torch.Tensor
     scales: torch.Tensor
+    fmt: str = "e4m3"
 
     @property
     def shape(self):
-        return tuple(self.codes.shape)
+        rows, c = self.codes.shape
+        return (rows, 2 * c if self.fmt == "e2m1" else c)
 
     @property
     def device(self):
@@ -59,17 +72,28 @@ class MxLhs:
 
     def dequantize(self) -> torch.Tensor:
         """The float32 values the codes and scales stand for (exact)."""
-        v = self.codes.view(E4M3).float()
+        rows, k = self.shape
+        if self.fmt == "e2m1":
+            nib = torch.stack([self.codes & 0xF, self.codes >> 4], dim=-1).reshape(rows, k).long()
+            mags = torch.tensor(_E2M1_MAGS, device=self.codes.device)
+            v = torch.where((nib & 8) != 0, -mags[nib & 7], mags[nib & 7])
+        else:
+            v = self.codes.view(E4M3).float()
         s = torch.ldexp(torch.ones((), device=self.scales.device), self.scales.to(torch.int32) - 127)
-        rows, k = self.codes.shape
         return (v.view(rows, k // MX_BLOCK, MX_BLOCK) * s[..., None]).view(rows, k)
 
 
-def mx_quantize(x: torch.Tensor) -> MxLhs:
-    """bf16 [rows, K] -> ``MxLhs``: per 32-value block along K, scale 2^e with
-    e the smallest exponent such that absmax <= 448 * 2^e (at least -126),
-    codes = e4m3 of x * 2^-e rounded to nearest even; a block with a NaN or
-    infinity gets NaN codes and scale code 255.  One device pass."""
+def mx_quantize(x: torch.Tensor, fmt: str = "e4m3") -> MxLhs:
+    """bf16 [rows, K] -> ``MxLhs`` in one device pass, per 32-value block
+    along K with scale 2^e (e at least -126):
+    fmt "e4m3": e the smallest exponent with absmax <= 448 * 2^e, codes =
+    e4m3 of x * 2^-e rounded to nearest even; a block with a NaN or infinity
+    gets NaN codes and scale code 255.
+    fmt "e2m1" (MXFP4): e the smallest exponent with absmax <= 6 * 2^e, codes
+    = e2m1 of x * 2^-e rounded to nearest even, packed two per byte; a block
+    with a NaN or infinity gets codes 0 and scale code 255."""
+    if fmt not in MX_FORMATS:
+        raise ValueError(f"mx_quantize: fmt must be one of {MX_FORMATS}, got {fmt!r}")
     if x.dtype != torch.bfloat16 or x.dim() != 2:
         raise ValueError(f"mx_quantize: expected a 2-D bfloat16 tensor, got {x.dtype} {tuple(x.shape)}")
     rows, k = x.shape
@@ -79,10 +103,23 @@ def mx_quantize(x: torch.Tensor) -> MxLhs:
     if x.data_ptr() % 16:
         x = x.clone()
     dev = _lib.require_cuda(x)
-    codes = torch.empty((rows, k), dtype=torch.uint8, device=dev)
+    codes = torch.empty((rows, k // 2 if fmt == "e2m1" else k), dtype=torch.uint8, device=dev)
     scales = torch.empty((rows, k // MX_BLOCK), dtype=torch.uint8, device=dev)
-    _lib.call("dwm_mx_quant_e4m3", _lib.ptr(x), rows, k, _lib.ptr(codes), _lib.ptr(scales), _lib.stream_handle(dev))
-    return MxLhs(codes, scales)
+    _lib.call("dwm_mx_quant_e2m1" if fmt == "e2m1" else "dwm_mx_quant_e4m3", _lib.ptr(x), rows, k, _lib.ptr(codes),
+              _lib.ptr(scales), _lib.stream_handle(dev))
+    return MxLhs(codes, scales, fmt)
+
+
+def _mx_format(lhs_quant_dtype):
+    """The MX lhs format a gmm_v2 lhs_quant_dtype names (None: no quantization)."""
+    if lhs_quant_dtype is None:
+        return None
+    if lhs_quant_dtype in (E4M3, "float8_e4m3fn"):
+        return "e4m3"
+    if lhs_quant_dtype in FP4_DTYPES or lhs_quant_dtype in ("float4_e2m1fn", "float4_e2m1fn_x2"):
+        return "e2m1"
+    raise NotImplementedError(f"gmm_v2: lhs_quant_dtype {lhs_quant_dtype!r}: float8_e4m3fn and float4_e2m1fn "
+                              "(the MX modes) are supported")
 
 
 def needs_fp4_emulation(dtype) -> bool:
@@ -319,15 +356,20 @@ def gmm_v2(lhs: torch.Tensor,
     ``lhs_quant_dtype=torch.float8_e4m3fn`` selects the MX mode (module
     docstring): the lhs is quantized with ``mx_quantize`` (unless it is an
     ``MxLhs`` already) and each product is e4m3 x e2m1 with both block scales,
-    on the scaled MFMA.  ``rhs_quant_dtype`` is accepted and ignored (the rhs
-    is fp4 either way).
+    on the scaled MFMA; ``lhs_quant_dtype`` float4_e2m1fn (or
+    ``torch.float4_e2m1fn_x2``) quantizes to e2m1 (MXFP4) and each product is
+    e2m1 x e2m1.  ``rhs_quant_dtype`` is accepted and ignored (the rhs is fp4
+    either way).
     """
     if fuse_act not in _lib.FUSE_ACTS:
         raise NotImplementedError(f"gmm_v2: fused activation {fuse_act!r} is not supported")
     fused = fuse_act is not None
-    if lhs_quant_dtype is not None and lhs_quant_dtype not in (E4M3, "float8_e4m3fn"):
-        raise NotImplementedError(f"gmm_v2: lhs_quant_dtype {lhs_quant_dtype!r}: only float8_e4m3fn (MX) is supported")
-    mx = lhs_quant_dtype is not None or isinstance(lhs, MxLhs)
+    mx_fmt = _mx_format(lhs_quant_dtype)
+    if isinstance(lhs, MxLhs):
+        if mx_fmt is not None and mx_fmt != lhs.fmt:
+            raise ValueError(f"gmm_v2: an {lhs.fmt} MxLhs with lhs_quant_dtype {lhs_quant_dtype!r}")
+        mx_fmt = lhs.fmt
+    mx = mx_fmt is not None
     if isinstance(rhs, Fp4Weight):
         if rhs_scale is not None:
             raise ValueError("gmm_v2: a prepacked Fp4Weight carries its own scales; pass rhs_scale=None")
@@ -350,11 +392,12 @@ def gmm_v2(lhs: torch.Tensor,
     if group_sizes.dtype != torch.int32 or group_sizes.dim() != 1:
         raise ValueError("gmm_v2: group_sizes must be a 1-D int32 tensor")
     if mx and not isinstance(lhs, MxLhs):
-        lhs = mx_quantize(lhs)
+        lhs = mx_quantize(lhs, mx_fmt)
     if isinstance(lhs, MxLhs):
         if lhs.codes.dtype != torch.uint8 or lhs.scales.dtype != torch.uint8 or \
                 tuple(lhs.scales.shape) != (lhs.shape[0], w.k // MX_BLOCK):
-            raise ValueError("gmm_v2: MxLhs needs uint8 codes [rows, K] and uint8 scales [rows, K/32]")
+            raise ValueError("gmm_v2: MxLhs needs uint8 codes [rows, K] (e2m1: [rows, K/2]) and uint8 scales "
+                             "[rows, K/32]")
         dev = _lib.require_cuda(lhs.codes, lhs.scales, w.weight, group_sizes)
     else:
         dev = _lib.require_cuda(lhs, w.weight, group_sizes)
@@ -386,6 +429,14 @@ def gmm_v2(lhs: torch.Tensor,
         bias = bias.contiguous()
         _lib.require_cuda(bias)
     out = torch.empty((m, w.n // 2 if fused else w.n), dtype=out_dtype, device=dev)
+    if mx_fmt == "e2m1":
+        codes, scales = lhs.codes.contiguous(), lhs.scales.contiguous()
+        _lib.call("dwm_gmm_fp4_mxfp4", _lib.ptr(codes), _lib.ptr(scales), codes.shape[0], _lib.ptr(idx), m, w.k,
+                  _lib.ptr(w.weight), _lib.ptr(w.scale), _lib.ptr(bias),
+                  _lib.dtype_code(bias.dtype) if bias is not None else 0, _lib.ptr(gs), gs.numel(), _lib.ptr(go),
+                  w.num_experts, w.n, _lib.ptr(out), _lib.dtype_code(out_dtype), 1 if zero_initialize else 0,
+                  _lib.FUSE_ACTS[fuse_act], _lib.stream_handle(dev))
+        return out
     if mx:
         codes, scales = lhs.codes.contiguous(), lhs.scales.contiguous()
         desc = _lib.GmmLhs(codes.data_ptr(), scales.data_ptr(), codes.shape[0], None if idx is None else idx.data_ptr())

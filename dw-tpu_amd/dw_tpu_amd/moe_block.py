@@ -13,8 +13,8 @@ activation of the accumulators is rounded once to bf16 (fused-moe-fp4
 or stays f32 (``f32_reduce``, 0106-...:243-250); the combine sums in f32 in
 top-k order and rounds once (moe_fast_combine.py:44-54).
 
-With ``lhs_quant_dtype=torch.float8_e4m3fn`` both gmm run in the MX mode
-(gmm_v2.py): ``hidden`` is quantized once, [T, H] before the gather (the
+With ``lhs_quant_dtype=torch.float8_e4m3fn`` (or float4_e2m1fn) both gmm
+run in the MX mode (gmm_v2.py): ``hidden`` is quantized once, [T, H] before the gather (the
 blocks run along each row, so gmm1 reads exactly the quantized rows of the
 gathered copy), and gmm2 quantizes the activation.
 """
@@ -23,7 +23,7 @@ from dataclasses import dataclass
 import torch
 
 from . import _trace
-from .gmm_v2 import Fp4Weight, gmm_v2, mx_quantize
+from .gmm_v2 import Fp4Weight, _mx_format, gmm_v2, mx_quantize
 from .moe_fast_combine import fast_combine
 from .moe_fast_dispatch import moe_dispatch, row_gather
 
@@ -46,8 +46,8 @@ def moe_block(hidden: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.
     f32 or bf16; w13: gate/up weights [E, H, 2I] prepacked with
     ``gate_up=True``; w2: down weights [E, I, H].  Returns [T, H] bf16 (or
     ``MoeBlockOutputs`` with ``return_intermediates``).  ``lhs_quant_dtype``:
-    None (the reference's bf16 activations) or torch.float8_e4m3fn (the MX
-    mode for both gmm)."""
+    None (the reference's bf16 activations), torch.float8_e4m3fn (the MX
+    mode for both gmm) or float4_e2m1fn (MXFP4 activations)."""
     if not w13.gate_up:
         raise ValueError("moe_block: w13 must be prepacked with gate_up=True")
     if w13.k != hidden.shape[1] or w2.k != w13.n // 2 or w2.n != hidden.shape[1]:
@@ -56,7 +56,7 @@ def moe_block(hidden: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.
     d = moe_dispatch(topk_ids, num_experts)
     # gmm1 reads hidden[token_indices_sorted] itself (the row gather fused
     # into its loads), the same rows the separate gather would write.
-    src = hidden if lhs_quant_dtype is None else mx_quantize(hidden)
+    src = hidden if lhs_quant_dtype is None else mx_quantize(hidden, _mx_format(lhs_quant_dtype))
     h = gmm_v2(src, w13, d.group_sizes, group_offset=group_offset, zero_initialize=False,
                fuse_act="silu_and_mul_with_clamp", lhs_row_indices=d.token_indices_sorted,
                lhs_quant_dtype=lhs_quant_dtype)

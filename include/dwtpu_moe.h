@@ -255,6 +255,33 @@ int dwm_gmm_fp4_mx(const uint8_t *lhs, const uint8_t *lhs_scale, int64_t lhs_row
                    const int32_t *group_sizes, int num_groups, const int32_t *group_offset, int64_t E_local,
                    int64_t N, void *out, int out_dtype, int zero_init, int fuse_act, void *stream);
 
+/* MXFP4 lhs quantization: bf16 x [rows, K] -> e2m1 codes [rows, K/2] (value
+ * 2j in the low nibble of byte j) + e8m0 scale codes [rows, K/32]: per 32
+ * values along K the exponent e = the smallest >= -126 with absmax <= 6 *
+ * 2^e (the scale 2^ceil(log2(absmax / 6)) of the reference's
+ * quantize_tensor(e2m1, x, -1, 32, power_of_two_scale=True),
+ * patches/tpu-inference/0001-dsv4-v6e-enablement.patch:315-350), codes the
+ * round-to-nearest-even e2m1 of x * 2^-e, scale code e + 127.  A block with a
+ * NaN or an infinity gets codes 0 and scale code 255.  K % 32 == 0; x
+ * 16-byte and codes 4-byte aligned. */
+int dwm_mx_quant_e2m1(const uint16_t *x, int64_t rows, int64_t K, uint8_t *codes, uint8_t *scales,
+                      void *stream);
+
+/* dwm_gmm_fp4_mx on an MXFP4 lhs (dwm_mx_quant_e2m1: e2m1 codes [lhs_rows,
+ * K/2], e8m0 scales [lhs_rows, K/32]): the gfx950 scaled MFMA with both
+ * operands e2m1 (32x32x64, both block scales in the instruction), f32
+ * accumulation, with rhs_bias (NULL or [E_local, N], DWM_F32 / DWM_BF16) and
+ * fuse_act as dwm_gmm_fp4_ex.  Stands in for gmm_v2(...,
+ * lhs_quant_dtype=float4_e2m1fn) (patches/tokamax/0001-gmm_v2-fp4-emulation-
+ * v6e.patch:89-99); like the e4m3 MX mode it is this library's choice of
+ * lhs quantization, opt-in, lossier than e4m3 (e2m1 keeps two significant
+ * bits of each activation), and held to its own stated bound. */
+int dwm_gmm_fp4_mxfp4(const uint8_t *lhs, const uint8_t *lhs_scale, int64_t lhs_rows, const int32_t *row_idx,
+                      int64_t M, int64_t K, const uint8_t *weight, const uint8_t *scale, const void *rhs_bias,
+                      int bias_dtype, const int32_t *group_sizes, int num_groups, const int32_t *group_offset,
+                      int64_t E_local, int64_t N, void *out, int out_dtype, int zero_init, int fuse_act,
+                      void *stream);
+
 /* ---------------------------------------------------------------------- */
 /* MoE dispatch and combine.                                               */
 /* ---------------------------------------------------------------------- */

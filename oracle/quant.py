@@ -162,3 +162,49 @@ def mx_dequantize(codes: np.ndarray, scale_codes: np.ndarray, block: int = MX_BL
     shp = v.shape
     out = v.reshape(shp[:-1] + (shp[-1] // block, block)) * s[..., None]
     return out.reshape(shp).astype(np.float32)
+
+
+def mx_quantize_e2m1(x: np.ndarray, block: int = MX_BLOCK):
+    """MXFP4 activations (gmm_v2(lhs_quant_dtype=float4_e2m1fn)): the
+    reference's quantize_tensor(e2m1, x, axis=-1, block,
+    power_of_two_scale=True) (patches/tpu-inference/0001-dsv4-v6e-
+    enablement.patch:315-350): per block, scale = 2^ceil(log2(absmax / 6))
+    and codes = round-to-nearest-even e2m1 of x / scale (|x / scale| <= 6).
+    The scale is stored as its e8m0 code (exponent + 127) with the exponent
+    kept in [-126, 127]; a block holding a NaN or an infinity gets scale code
+    255 and element codes 0.
+
+    The exponent comes from the bits: absmax = mf * 2^ef with mf in [0.5, 1)
+    (frexp); absmax <= 6 * 2^e = 0.75 * 2^(e + 3) holds from e = ef - 3 when
+    mf <= 0.75, else from e = ef - 2.  (For bf16 inputs this is the same
+    power of two as the reference's f32 absmax / 6 rounded up: a bf16
+    quotient by 6 lands on a power of two only when it is one exactly.)
+
+    x: float32 [..., K], K % block == 0.  Returns (nibble codes uint8
+    [..., K] in 0..15, sign in bit 3; scale codes uint8 [..., K / block]).
+    """
+    x = np.asarray(x, np.float32)
+    shp = x.shape
+    xb = x.reshape(shp[:-1] + (shp[-1] // block, block))
+    bad = ~np.all(np.isfinite(xb), axis=-1)
+    amax = np.where(bad, 0, np.abs(np.where(np.isfinite(xb), xb, 0)).max(axis=-1)).astype(np.float64)
+    mf, ef = np.frexp(amax)
+    e = np.where(mf > 0.75, ef - 2, ef - 3)
+    e = np.where(amax == 0, MX_MIN_EXP, np.maximum(e, MX_MIN_EXP)).astype(np.int64)
+    finite = np.where(np.isfinite(xb) & ~bad[..., None], xb, 0).astype(np.float64)
+    q = np.ldexp(finite, -e[..., None]).astype(np.float32)  # exact: a power-of-two rescale
+    codes = np.where(bad[..., None], np.uint8(0), to_e2m1(q)).astype(np.uint8)
+    scale_codes = np.where(bad, 255, e + 127).astype(np.uint8)
+    return codes.reshape(shp), scale_codes
+
+
+def mx_dequantize_e2m1(codes: np.ndarray, scale_codes: np.ndarray, block: int = MX_BLOCK) -> np.ndarray:
+    """e2m1 nibble codes [..., K] and e8m0 scale codes [..., K / block] ->
+    float32 values (exact; scale code 255 gives NaN)."""
+    v = E2M1_VALUES[np.asarray(codes, np.uint8)].astype(np.float64)
+    sc = np.asarray(scale_codes, np.int64)
+    s = np.where(sc == 255, np.nan, np.ldexp(1.0, sc - 127))
+    shp = v.shape
+    out = v.reshape(shp[:-1] + (shp[-1] // block, block)) * s[..., None]
+    return out.reshape(shp).astype(np.float32)
+

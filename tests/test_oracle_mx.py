@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 
 from oracle import quant
-from oracle.numerics import E4M3_VALUES, bf16_bits, bf16_to_f32
+from oracle.numerics import E4M3_VALUES, bf16_bits, bf16_to_f32, round_bf16
 
 
 def _bf16(x):
@@ -106,3 +106,50 @@ def test_block_max_product_brute_force(rng):
             for b in range(2):
                 want[m, n] += max(abs(float(a[m, k]) * float(w[owner[m], k, n])) for k in range(32 * b, 32 * b + 32))
     assert np.allclose(got, want, rtol=1e-12, atol=0)
+
+
+# --------------------------------------------------------------- MXFP4 lhs
+
+def test_mx_e2m1_matches_the_reference_quantizer_on_bf16(rng):
+    """mx_quantize_e2m1 is quantize_tensor(e2m1, x, -1, 32,
+    power_of_two_scale=True) (0001-...:315-350, restated as
+    quantize_tensor_pow2 and pinned by the reference's MXFP4 requant test)
+    on bf16 inputs across 60 binades, where the exponent clamp is not hit."""
+    x = rng.standard_normal((64, 256)).astype(np.float32)
+    x *= np.ldexp(np.float32(1), rng.integers(-30, 30, (64, 8))).repeat(32, axis=1).astype(np.float32)
+    x = round_bf16(x)
+    codes, sc = quant.mx_quantize_e2m1(x)
+    ref_codes, ref_scale = quant.quantize_tensor_pow2(x, "e2m1", -1, 32)
+    assert np.array_equal(codes, ref_codes)
+    assert np.array_equal(np.ldexp(np.float32(1), sc.astype(np.int64) - 127).astype(np.float32), ref_scale)
+
+
+@pytest.mark.parametrize("v,want", [(6.0, 6.0), (-0.25, -0.0), (0.75, 1.0), (1.25, 1.0), (1.75, 2.0),
+                                    (2.5, 2.0), (3.5, 4.0), (5.0, 4.0), (0.5, 0.5), (-3.0, -3.0)])
+def test_mx_e2m1_rounds_to_nearest_even(v, want):
+    """Within a block whose largest value is 6 (scale 1): e2m1 ties go to the
+    even code (0.25 -> 0, 0.75 -> 1, 1.25 -> 1, 1.75 -> 2, 2.5 -> 2, 3.5 -> 4,
+    5 -> 4)."""
+    x = np.zeros((1, 32), np.float32)
+    x[0, 0] = 6.0
+    x[0, 7] = v
+    c, s = quant.mx_quantize_e2m1(x)
+    assert s[0, 0] == 127
+    got = quant.mx_dequantize_e2m1(c, s)[0, 7]
+    assert got == want and np.signbit(got) == np.signbit(np.float32(want))
+
+
+def test_mx_e2m1_scale_boundaries_and_special_blocks():
+    """absmax exactly 6 * 2^e keeps exponent e, one bf16 ulp above takes
+    e + 1; an all-zero block gets the clamped exponent -126; a block with a
+    NaN or an infinity gets scale code 255."""
+    x = np.zeros((5, 32), np.float32)
+    x[0, 3] = 6.0 * 2.0 ** 5                       # exactly 6 * 2^5
+    x[1, 3] = 6.0 * 2.0 ** 5 * (1 + 2.0 ** -7)     # next bf16 value up
+    x[2, 3] = -6.0 * 2.0 ** -20
+    x[3, 5] = np.nan
+    x[4, 9] = -np.inf
+    _, s = quant.mx_quantize_e2m1(x)
+    assert [int(v) for v in s[:, 0]] == [132, 133, 107, 255, 255]
+    _, z = quant.mx_quantize_e2m1(np.zeros((1, 32), np.float32))
+    assert z[0, 0] == 1  # -126 + 127
