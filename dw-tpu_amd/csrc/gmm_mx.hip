@@ -508,26 +508,36 @@ __global__ __launch_bounds__(C::THREADS) void gmm_mx_kernel(
 // bytes.  Stage t is published at barrier t (one step ahead of the
 // consumers' reads) and the stage of step t - 1 is refilled with step
 // t + NS - 1.
-template <int MB, int CW, int NP, int NS>
+// AF4: e2m1 lhs (MXFP4): 64 bytes per row and 128-deep step in four 16-byte
+// chunks, chunk c of row r at physical chunk c ^ ((r >> 2) & 3) (the e4m3
+// layout of the 64-deep kernel), 16 rows per 1 KiB load.
+template <int MB, int CW, int NP, int NS, bool AF4 = false>
 struct Mx128Cfg {
   static constexpr int CONS = CW, NPROD = NP, STAGES = NS;
+  static constexpr bool A_FP4 = AF4;
   static constexpr int GT = CW;
   static constexpr int THREADS = 64 * (CW + NP);
   static constexpr int NT = 64 * GT;
   static constexpr int ROWS = 32 * MB;
+  static constexpr int AB = AF4 ? 64 : 128;              // lhs bytes per row and step
+  static constexpr int RL = 1024 / AB;                   // rows per 1 KiB lhs load
   static constexpr int W = 0;                            // group i: 4 KiB at W + 4096 i
-  static constexpr int A = GT * 4096;                    // ROWS x 128 bytes
+  static constexpr int A = GT * 4096;                    // ROWS x AB bytes
   static constexpr int AS_LOADS = (ROWS + 63) / 64;
-  static constexpr int AS = A + ROWS * 128;              // AS_LOADS x 256 bytes (dword per row)
+  static constexpr int AS = A + ROWS * AB;               // AS_LOADS x 256 bytes (dword per row)
   static constexpr int S = AS + AS_LOADS * 256;          // group i: 256 bytes at S + 256 i
   static constexpr int STAGE = S + GT * 256;
-  static constexpr int A_LOADS = ROWS / 8 / NP;          // 1 KiB lhs loads (8 rows) per producer
+  static constexpr int A_GROUPS = ROWS / RL;             // 1 KiB lhs loads per step
+  static constexpr int A_LOADS = (A_GROUPS + NP - 1) / NP;  // most lhs loads of one producer (groups pw + NP i)
   static constexpr int G_LOADS = GT / NP;
   static constexpr int EP_STRIDE = 72;
-  static_assert(A_LOADS * NP * 8 == ROWS && G_LOADS * NP == GT, "load split");
+  static_assert(A_GROUPS * RL == ROWS && G_LOADS * NP == GT, "load split");
   static_assert(AS_LOADS <= NP && NS >= 2, "config");
   static_assert(CW * 32 * EP_STRIDE * 4 <= NS * STAGE, "epilogue staging fits the stages");
 };
+
+template <class C>
+__device__ __forceinline__ int mx128_swz(int r) { return C::A_FP4 ? ((r >> 2) & 3) : ((r >> 1) & 7); }
 
 template <class C, int NA, bool ASL>
 __device__ __forceinline__ void mx128_producer(const uint8_t *__restrict__ lhs, const uint8_t *__restrict__ lsc,
@@ -541,20 +551,28 @@ __device__ __forceinline__ void mx128_producer(const uint8_t *__restrict__ lhs, 
   static_assert(PENDING < 64, "vmcnt range");
   const int lane = threadIdx.x & 63;
 #pragma unroll
-  for (int i = NA; i < C::A_LOADS; ++i)
+  for (int i = NA; i < C::A_LOADS; ++i) {
+    const int ga = pw + NP * i;
+    if (ga < C::A_GROUPS) {
 #pragma unroll
-    for (int st = 0; st < NS; ++st)
-      *(u32x4_t *)(s_lds + st * C::STAGE + C::A + (pw + NP * i) * 1024 + lane * 16) = u32x4_t{0u, 0u, 0u, 0u};
+      for (int st = 0; st < NS; ++st)
+        *(u32x4_t *)(s_lds + st * C::STAGE + C::A + ga * 1024 + lane * 16) = u32x4_t{0u, 0u, 0u, 0u};
+    }
+  }
   const int KS = K / kMxBlock;
   auto src_row = [&](int r) -> int64_t {
     const int rs = r < rows ? r : rows - 1;
     return row_idx ? gather_index(row_idx[row0 + rs], lhs_rows) : row0 + rs;
   };
+  // lhs load i: rows RL (pw + NP i) .. + RL - 1; lane l fills physical chunk
+  // l % LPR of row + l / LPR with the logical chunk of the swizzle.
+  constexpr int LPR = C::AB / 16;
+  const int64_t KR = C::A_FP4 ? K / 2 : K;  // lhs bytes per row
   uint32_t aoff[NA > 0 ? NA : 1];
 #pragma unroll
   for (int i = 0; i < NA; ++i) {
-    const int r = 8 * (pw + NP * i) + (lane >> 3);
-    aoff[i] = (uint32_t)(src_row(r) * K) + (uint32_t)(((lane & 7) ^ ((r >> 1) & 7)) << 4);
+    const int r = C::RL * (pw + NP * i) + lane / LPR;
+    aoff[i] = (uint32_t)(src_row(r) * KR) + (uint32_t)(((lane % LPR) ^ mx128_swz<C>(r)) << 4);
   }
   const int aspart = pw - (NP - C::AS_LOADS);
   const uint32_t asoff = ASL ? (uint32_t)(src_row(64 * aspart + lane) * KS) : 0u;
@@ -568,7 +586,7 @@ __device__ __forceinline__ void mx128_producer(const uint8_t *__restrict__ lhs, 
   }
   auto issue = [&](int stage, int t) {
     uint8_t *const st = s_lds + stage * C::STAGE;
-    const uint8_t *const a = lhs + (int64_t)t * 128;
+    const uint8_t *const a = lhs + (int64_t)t * C::AB;
 #pragma unroll
     for (int i = 0; i < NA; ++i)
       __builtin_amdgcn_global_load_lds((const void *)(a + aoff[i]),
@@ -619,14 +637,21 @@ __device__ __forceinline__ void mx128_consumer(int T, uint8_t *s_lds, int cw, in
       for (int r = 0; r < 16; ++r) acc[mb][j][r] = 0.0f;
   const int woff = C::W + cw * 4096 + lane * 16;
   const int soff = C::S + cw * 256 + lane * 4;
-  const int sw = (c32 >> 1) & 7;  // rows mb * 32 + c32 share it
-  const int arow = C::A + c32 * 128;
+  const int sw = mx128_swz<C>(c32);  // rows mb * 32 + c32 share it
+  const int arow = C::A + c32 * C::AB;
   u32x4_t wa[2], wb[2];
   i32x8_t an;
+  // A fragment of substep f (k = 64 f .. + 63): e4m3 chunks 4 f + h and
+  // 4 f + 2 + h; e2m1 chunk 2 f + h (k = 64 f + 32 h .. + 31).
   auto read_a = [&](const uint8_t *st, int f, int mb) {
-    const u32x4_t lo = *(const u32x4_t *)(st + arow + mb * 32 * 128 + (((4 * f + h) ^ sw) << 4));
-    const u32x4_t hi = *(const u32x4_t *)(st + arow + mb * 32 * 128 + (((4 * f + 2 + h) ^ sw) << 4));
-    an = i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+    if constexpr (C::A_FP4) {
+      const u32x4_t lo = *(const u32x4_t *)(st + arow + mb * 32 * C::AB + (((2 * f + h) ^ sw) << 4));
+      an = i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], 0, 0, 0, 0};
+    } else {
+      const u32x4_t lo = *(const u32x4_t *)(st + arow + mb * 32 * C::AB + (((4 * f + h) ^ sw) << 4));
+      const u32x4_t hi = *(const u32x4_t *)(st + arow + mb * 32 * C::AB + (((4 * f + 2 + h) ^ sw) << 4));
+      an = i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+    }
   };
   // Steps in runs of NS, one per stage, so that every stage address is a
   // constant offset (cur = t % NS is known in each copy of the body).
@@ -663,8 +688,9 @@ __device__ __forceinline__ void mx128_consumer(int T, uint8_t *s_lds, int cw, in
           wb[0] = *(const u32x4_t *)(st + woff + 2048);
           wb[1] = *(const u32x4_t *)(st + woff + 3072);
         }
-        acc[mb][0] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b0, acc[mb][0], 0, 4, 0, sa_l, 0, sb);
-        acc[mb][1] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b1, acc[mb][1], 0, 4, 0, sa_l, 1, sb);
+        constexpr int AFMT = C::A_FP4 ? 4 : 0;  // A operand format: e2m1 or e4m3 (B: e2m1)
+        acc[mb][0] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b0, acc[mb][0], AFMT, 4, 0, sa_l, 0, sb);
+        acc[mb][1] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b1, acc[mb][1], AFMT, 4, 0, sa_l, 1, sb);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -705,13 +731,16 @@ __global__ __launch_bounds__(C::THREADS) void gmm_mx128_kernel(
     const int pw = wave - CW;
     const uint8_t *const wexp = wpk + e * G * T * 4096;
     const uint8_t *const sexp = spk + e * G * T * 256;
-    const int na = min(C::A_LOADS, (rows + 8 * NP - 1 - 8 * pw) / (8 * NP));
+    // Row groups pw + NP i (< A_GROUPS) with RL (pw + NP i) < rows are loaded.
+    int na = 0;
+    for (int ga = pw; ga < C::A_GROUPS; ga += NP) na += C::RL * ga < rows ? 1 : 0;
     const bool asl = pw >= NP - C::AS_LOADS;
     auto run = [&](auto na_c, auto asl_c) {
-      mx128_producer<C, decltype(na_c)::value, decltype(asl_c)::value != 0>(lhs, lsc, row_idx, lhs_rows, row0, rows,
-                                                                             K, T, wexp, sexp, g0, G, s_lds, pw);
+      mx128_producer<C, (decltype(na_c)::value < C::A_LOADS ? decltype(na_c)::value : C::A_LOADS),
+                     decltype(asl_c)::value != 0>(lhs, lsc, row_idx, lhs_rows, row0, rows, K, T, wexp, sexp, g0, G,
+                                                  s_lds, pw);
     };
-    static_assert(C::A_LOADS == 3, "three lhs row groups per producer");
+    static_assert(C::A_LOADS <= 3, "at most three lhs row groups per producer");
     if (asl) {
       if (na >= 3) run(IntC<3>{}, IntC<1>{});
       else if (na == 2) run(IntC<2>{}, IntC<1>{});
@@ -767,18 +796,19 @@ int launch_gmm_mx(const uint8_t *lhs, const uint8_t *lhs_scale, const int32_t *r
   using C64 = MxCfg<3, 8, 4, 5>;
   using C64H = MxCfg<3, 8, 4, 5, 2>;
   using C128 = Mx128Cfg<3, 8, 4, 3>;
-  // MXFP4 lhs: the 64-deep kernel at every K (its stages are 22 KB), with
-  // the same row-half stacking.
+  // MXFP4 lhs: the same kernels with e2m1 A operands.
   using F64 = MxCfg<3, 8, 4, 5, 1, true>;
   using F64H = MxCfg<3, 8, 4, 5, 2, true>;
-  const bool deep = !lhs_fp4 && K >= kMx128MinK;
+  using F128 = Mx128Cfg<3, 8, 4, 3, true>;
+  const bool deep = K >= kMx128MinK;
   const bool halves = !deep && M > 96 * E_local && M <= 192 * E_local;
 #define DWM_MX(CFG, TMB, ACT, DEEP)                                                                                \
   launch_mx<CFG, TMB, ACT, DEEP>(lhs, lhs_scale, row_idx, lhs_rows, M, K, weight, scale, group_sizes, num_groups, \
                                  group_offset, E_local, N, out, out_f32, ep, st)
   if (lhs_fp4) {
-    if (gated) return halves ? DWM_MX(F64H, 6, true, false) : DWM_MX(F64, 3, true, false);
-    return halves ? DWM_MX(F64H, 6, false, false) : DWM_MX(F64, 3, false, false);
+    if (gated)
+      return deep ? DWM_MX(F128, 3, true, true) : halves ? DWM_MX(F64H, 6, true, false) : DWM_MX(F64, 3, true, false);
+    return deep ? DWM_MX(F128, 3, false, true) : halves ? DWM_MX(F64H, 6, false, false) : DWM_MX(F64, 3, false, false);
   }
   if (gated)
     return deep ? DWM_MX(C128, 3, true, true) : halves ? DWM_MX(C64H, 6, true, false) : DWM_MX(C64, 3, true, false);

@@ -133,24 +133,32 @@ def test_moe_block_stagewise(dev, rng, f32_reduce):
 
 
 @pytest.mark.parametrize("f32_reduce", [False, True])
-def test_moe_block_mx_stagewise(dev, rng, f32_reduce):
-    """The block in the MX mode (lhs_quant_dtype=float8_e4m3fn): dispatch and
-    combine bit-exact; gmm1 + activation on the quantized hidden rows and
-    gmm2 on the quantized activation, each within the MX bound
-    (oracle.gmm.mx_error_bound propagated through the activation)."""
+@pytest.mark.parametrize("fmt", ["e4m3", "e2m1"])
+def test_moe_block_mx_stagewise(dev, rng, f32_reduce, fmt):
+    """The block in the MX modes (lhs_quant_dtype=float8_e4m3fn, or
+    float4_e2m1fn: MXFP4): dispatch and combine bit-exact; gmm1 + activation
+    on the quantized hidden rows and gmm2 on the quantized activation, each
+    within the MX bound (oracle.gmm.mx_error_bound propagated through the
+    activation)."""
     from dw_tpu_amd import fp4_weight_to_codes, moe_block
     from oracle import quant
+    qdt = torch.float8_e4m3fn if fmt == "e4m3" else "float4_e2m1fn"
+
+    def mxq(x):  # the oracle's quantize-dequantize of the chosen format
+        if fmt == "e4m3":
+            return quant.mx_dequantize(*quant.mx_quantize_e4m3(x))
+        return quant.mx_dequantize_e2m1(*quant.mx_quantize_e2m1(x))
     T, E, topk, H, I = 64, 8, 2, 256, 128
     ids, wts, hidden_bits, (r13, s13), (r2, s2) = _block_case(rng, T, E, topk, H, I, empty=(2,))
     w13 = fp4_weight_to_codes(torch.from_numpy(r13).to(dev), torch.from_numpy(s13).to(dev), gate_up=True)
     w2 = fp4_weight_to_codes(torch.from_numpy(r2).to(dev), torch.from_numpy(s2).to(dev))
     r = moe_block(bf16_tensor(hidden_bits, dev), torch.from_numpy(ids).to(dev), torch.from_numpy(wts).to(dev), w13,
-                  w2, E, f32_reduce=f32_reduce, return_intermediates=True, lhs_quant_dtype=torch.float8_e4m3fn)
+                  w2, E, f32_reduce=f32_reduce, return_intermediates=True, lhs_quant_dtype=qdt)
     torch.cuda.synchronize()
     perm, tok, rev, gs, _ = moe.dispatch(ids, E)
     assert np.array_equal(r.dispatch.group_sizes.cpu().numpy(), gs)
     # gmm1: the quantized hidden rows, gathered
-    a = quant.mx_dequantize(*quant.mx_quantize_e4m3(bf16_to_f32(hidden_bits)))[tok]
+    a = mxq(bf16_to_f32(hidden_bits))[tok]
     w13f = _dequant(r13, s13)
     acc64, _ = gmm.gmm(a, None, None, gs, out_dtype="float64", w=w13f)
     acc_err = H * 2.0 ** -24 * gmm.abs_product(a, w13f, gs) + gmm.MX_BLOCK_TERM * gmm.block_max_product(a, w13f, gs)
@@ -158,7 +166,7 @@ def test_moe_block_mx_stagewise(dev, rng, f32_reduce):
     err = np.abs(h - omb.apply_act(acc64, "silu_and_mul_with_clamp"))
     assert np.all(err <= omb.act_bound(acc64, acc_err, "silu_and_mul_with_clamp"))
     # gmm2: the kernel's activation, quantized
-    hq = quant.mx_dequantize(*quant.mx_quantize_e4m3(bf16_to_f32(bf16_bits(r.h))))
+    hq = mxq(bf16_to_f32(bf16_bits(r.h)))
     w2f = _dequant(r2, s2)
     y64, _ = gmm.gmm(hq, None, None, gs, out_dtype="float64", w=w2f)
     kind = "float32" if f32_reduce else "bfloat16"
