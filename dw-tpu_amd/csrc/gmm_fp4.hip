@@ -25,6 +25,7 @@
 // and it is the same for every row.
 #include <algorithm>
 #include <atomic>
+#include <cstdlib>
 
 #include "gmm_tiles.h"
 
@@ -548,7 +549,20 @@ static int launch_gmm_ws(const uint16_t *lhs, const int32_t *row_idx, int64_t lh
 
 // Groups of 2 .. kGmmBalancedTiles row tiles split their rows evenly, and
 // their row tiles of one column tile run side by side on one XCD (find_tile).
+// DWTPU_GMM_BALANCED_TILES (read at every launch) sets another bound: 0 or 1
+// balances no group, a bound past every group's tile count balances all of
+// them (each group's row tiles of one column tile then run together, so the
+// group's weight slice is read once per XCD).  Only the schedule changes:
+// every row's result is the same.
 constexpr int kGmmBalancedTiles = 4;
+
+static int balanced_tiles() {
+  const char *e = getenv("DWTPU_GMM_BALANCED_TILES");
+  if (!e || !*e) return kGmmBalancedTiles;
+  char *end = nullptr;
+  const long v = strtol(e, &end, 10);
+  return (*end == 0 && v >= 0 && v <= (1l << 30)) ? (int)v : kGmmBalancedTiles;
+}
 
 // The bf16 grouped matmul (arguments checked by the caller).
 int launch_gmm_bf16(const uint16_t *lhs, const int32_t *row_idx, int64_t lhs_rows, int64_t M, int64_t K,
@@ -566,7 +580,7 @@ int launch_gmm_bf16(const uint16_t *lhs, const int32_t *row_idx, int64_t lhs_row
   const bool narrow = ((M + 95) / 96) * ((N + 511) / 512) < ncu;
 #define DWM_GMM_WS(ACT, NARROW)                                                                                   \
   launch_gmm_ws<3, 8, 2, 4, 4, ACT, NARROW>(lhs, row_idx, lhs_rows, M, K, weight, scale, group_sizes, num_groups, \
-                                             group_offset, E_local, N, out, out_f32, ep, ncu, kGmmBalancedTiles, st)
+                                             group_offset, E_local, N, out, out_f32, ep, ncu, balanced_tiles(), st)
   if (gated) return narrow ? DWM_GMM_WS(true, true) : DWM_GMM_WS(true, false);
   return narrow ? DWM_GMM_WS(false, true) : DWM_GMM_WS(false, false);
 #undef DWM_GMM_WS

@@ -264,6 +264,26 @@ def test_gmm_full_size_exact_scaling(dev, name):
     assert torch.isfinite(y1).all()
 
 
+@pytest.mark.parametrize("name", ["decode_gate_up", "decode_down", "prefill"])
+def test_gmm_balanced_tile_bound_changes_only_the_schedule(dev, monkeypatch, name):
+    """DWTPU_GMM_BALANCED_TILES moves rows between the row tiles of a group
+    (0: no group balanced, 10**6: every group) and the order tiles run in;
+    every row's bits stay those of the default schedule."""
+    from dw_tpu_amd import fp4_weight_to_codes, gmm_v2
+    from dw_tpu_amd.workloads import make_gmm_workload
+    wl = make_gmm_workload(name)
+    pw = fp4_weight_to_codes(torch.from_numpy(wl.rhs_e2m1).to(dev), torch.from_numpy(wl.scale_codes).to(dev))
+    lhs = bf16_tensor(wl.lhs_bits, dev)
+    gs = torch.from_numpy(wl.group_sizes).to(dev)
+    monkeypatch.delenv("DWTPU_GMM_BALANCED_TILES", raising=False)
+    y = gmm_v2(lhs, pw, gs, preferred_element_type=torch.float32)
+    for bound in ("0", "2", "1000000", "not a number"):
+        monkeypatch.setenv("DWTPU_GMM_BALANCED_TILES", bound)
+        yb = gmm_v2(lhs, pw, gs, preferred_element_type=torch.float32)
+        torch.cuda.synchronize()
+        assert torch.equal(yb.view(torch.int32), y.view(torch.int32)), bound
+
+
 def test_gmm_full_size_row_permutation_and_group_independence(dev, rng):
     """decode_gate_up at full size: permuting rows inside each expert group
     permutes the output rows bit for bit (each row's result depends on its
