@@ -124,16 +124,24 @@ struct IntC {
   static constexpr int value = V;
 };
 
-// Inclusive prefix sum across a 64-lane wavefront.
+// Inclusive prefix sum across a 64-lane wavefront, all 64 lanes active.
+// Register-to-register DPP moves, no LDS round trip: row_shr 1, 2, 4, 8 scan
+// each 16-lane row (a lane whose source lies before its row reads 0), then
+// row_bcast:15 adds lane 15's total to row 1 and lane 47's to row 3, and
+// row_bcast:31 adds lane 31's total to rows 2 and 3 (the row masks 0xA and
+// 0xC leave the other rows at +0).
 __device__ __forceinline__ int wave_inclusive_scan(int v) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    int t = __shfl_up(v, d, 64);
-    if (lane >= d) v += t;
-  }
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);  // row_bcast:15
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);  // row_bcast:31
   return v;
 }
+
+// Lane 63's value, as a wave-uniform scalar (the total of an inclusive scan).
+__device__ __forceinline__ int wave_last(int v) { return __builtin_amdgcn_readlane(v, 63); }
 
 __device__ __forceinline__ int wave_sum(int v) {
 #pragma unroll

@@ -68,14 +68,14 @@ __device__ __forceinline__ void tile_classes(const int32_t *group_sizes, int num
       const int rem_cls = (rem + CG - 1) / CG;  // 0 when there is no partial tile
       const int ri = wave_inclusive_scan(sz);
       if (g < num_groups) s_rowstart[g] = row_carry + ri - sz;
-      row_carry += __shfl(ri, 63, 64);
+      row_carry += wave_last(ri);
 #pragma unroll
       for (int a = 0; a < NC; ++a) {
         const int cnt = sp.bal ? (sp.top == NC - a ? sp.n : 0)
                                : (a == 0 ? n_full : 0) + (rem_cls == NC - a ? 1 : 0);
         const int ci = wave_inclusive_scan(cnt);
         if (g < num_groups) s_cls[a * kClsStride + g] = carry[a] + ci - cnt;
-        carry[a] += __shfl(ci, 63, 64);
+        carry[a] += wave_last(ci);
       }
     }
     if (lane == 0) {

@@ -90,7 +90,7 @@ __global__ __launch_bounds__(1024) void dispatch_scan_kernel(int32_t *counts, in
       const int v = ee < C ? s_tot[ee] : 0;
       const int inc = wave_inclusive_scan(v);
       if (ee < C) s_off[ee] = carry + inc - v;
-      carry += __shfl(inc, 63, 64);
+      carry += wave_last(inc);
     }
   }
   __syncthreads();
@@ -201,7 +201,7 @@ __global__ __launch_bounds__(kFusedThreads) void dispatch_fused_kernel(const int
         if (group_offsets) group_offsets[e] = carry + inc - v;  // entry E = number of valid ids
         s_run[e] = carry + inc - v;
       }
-      carry += __shfl(inc, 63, 64);
+      carry += wave_last(inc);
     }
   }
   int nbits = 0;
