@@ -46,12 +46,19 @@ typedef __attribute__((ext_vector_type(16))) float f32x16_t;
 typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;
 typedef __attribute__((ext_vector_type(2))) uint32_t u32x2_t;
 
-// float -> bf16 bits, round to nearest even; NaN stays a quiet NaN.
+// float -> bf16 bits, round to nearest even (f32 denormals kept); a NaN keeps
+// its sign and top payload bits and is made quiet: bits (u >> 16) | 0x40.
+// gfx950's v_cvt_pk_bf16_f32 (what the __bf16 conversion compiles to) gives
+// exactly these bits for every one of the 2^32 inputs, in either half of its
+// packed result, so no software rounding is needed.
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-  uint32_t u = __builtin_bit_cast(uint32_t, f);
-  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);
-  u += 0x7FFFu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
+}
+
+// Two floats -> packed bf16 bits (lo in bits 0..15), one v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2_bits(float lo, float hi) {
+  const bf16x2_t p = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, p);
 }
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) {

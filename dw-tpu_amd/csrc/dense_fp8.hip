@@ -76,7 +76,7 @@ __global__ void dense_fp8_prepack_kernel(const uint8_t *w, int64_t K, int64_t N,
 __device__ __forceinline__ uint32_t scale_bf16x2(uint32_t v, float s) {
   const float lo = bf16_bits_to_f32(v & 0xFFFFu) * s;
   const float hi = __builtin_bit_cast(float, v & 0xFFFF0000u) * s;
-  return (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
+  return f32x2_to_bf16x2_bits(lo, hi);
 }
 
 // A8: activations are e4m3 codes with scales sx [M, K/128]; else bf16.
@@ -798,8 +798,8 @@ __global__ void dense_fp8_reduce4_kernel(const float *__restrict__ partial, int 
       s[3] = s[3] + p[3];
     }
     u32x2_t o;
-    o[0] = (uint32_t)f32_to_bf16_bits(s[0]) | ((uint32_t)f32_to_bf16_bits(s[1]) << 16);
-    o[1] = (uint32_t)f32_to_bf16_bits(s[2]) | ((uint32_t)f32_to_bf16_bits(s[3]) << 16);
+    o[0] = f32x2_to_bf16x2_bits(s[0], s[1]);
+    o[1] = f32x2_to_bf16x2_bits(s[2], s[3]);
     ((u32x2_t *)out)[i] = o;
   }
 }

@@ -241,7 +241,7 @@ __device__ __forceinline__ void store8(void *__restrict__ out, int64_t o, const 
     u32x4_t p;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      p[i] = (uint32_t)f32_to_bf16_bits(v[2 * i]) | ((uint32_t)f32_to_bf16_bits(v[2 * i + 1]) << 16);
+      p[i] = f32x2_to_bf16x2_bits(v[2 * i], v[2 * i + 1]);
     __builtin_nontemporal_store(p, (u32x4_t *)((uint16_t *)out + o));
   }
 }
@@ -263,8 +263,10 @@ __device__ __forceinline__ void store_tile(const f32x16_t (&acc)[AM][2], float *
   constexpr int CO = ACT ? 32 : 64;  // output columns of this wave
   const int64_t n_out = ACT ? N / 2 : N;
   const int64_t ocol0 = ACT ? col0 / 2 : col0;
-  // The bias of this lane's two accumulator columns (source column order).
-  float b0 = 0.0f, b1 = 0.0f;
+  // The bias of this lane's two accumulator columns (source column order);
+  // -0.0f without a bias: x + -0.0f is x for every accumulator value (f32
+  // denormals are kept), so no per-value select is needed.
+  float b0 = -0.0f, b1 = -0.0f;
   if (bias) {
     const int64_t s0 = ACT ? col0 / 2 + c32 : col0 + c32;
     const int64_t s1 = ACT ? N / 2 + col0 / 2 + c32 : col0 + 32 + c32;
@@ -276,8 +278,8 @@ __device__ __forceinline__ void store_tile(const f32x16_t (&acc)[AM][2], float *
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int lr = 8 * (r >> 2) + 4 * h + (r & 3);
-      const float v0 = bias ? acc[mb][0][r] + b0 : acc[mb][0][r];
-      const float v1 = bias ? acc[mb][1][r] + b1 : acc[mb][1][r];
+      const float v0 = acc[mb][0][r] + b0;
+      const float v1 = acc[mb][1][r] + b1;
       if constexpr (ACT) {
         ep[lr * ES + c32] = act_pair(act, v0, v1);
       } else {
@@ -319,7 +321,7 @@ __device__ __forceinline__ void store_halves(const f32x4_t (&acc)[NH][4], float 
   constexpr int CO = ACT ? 32 : 64;
   const int64_t n_out = ACT ? N / 2 : N;
   const int64_t ocol0 = ACT ? col0 / 2 : col0;
-  float b[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  float b[4] = {-0.0f, -0.0f, -0.0f, -0.0f};  // no bias: x + -0.0f is x (see store_tile)
   if (bias) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -335,7 +337,7 @@ __device__ __forceinline__ void store_halves(const f32x4_t (&acc)[NH][4], float 
       const int lr = 4 * q + r;
       float v[4];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) v[u] = bias ? acc[hb][u][r] + b[u] : acc[hb][u][r];
+      for (int u = 0; u < 4; ++u) v[u] = acc[hb][u][r] + b[u];
       if constexpr (ACT) {
         ep[lr * ES + c16] = act_pair(act, v[0], v[2]);
         ep[lr * ES + 16 + c16] = act_pair(act, v[1], v[3]);

@@ -434,7 +434,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const void *x, int64_t x_r
         u32x4_t q;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          q[i] = (uint32_t)f32_to_bf16_bits(acc[2 * i]) | ((uint32_t)f32_to_bf16_bits(acc[2 * i + 1]) << 16);
+          q[i] = f32x2_to_bf16x2_bits(acc[2 * i], acc[2 * i + 1]);
         *(u32x4_t *)((uint16_t *)out + t * H + c) = q;
       }
     } else {
@@ -494,7 +494,7 @@ __global__ __launch_bounds__(256) void combine_bf16_kernel(const uint16_t *__res
       u32x4_t q;
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        q[i] = (uint32_t)f32_to_bf16_bits(acc[2 * i]) | ((uint32_t)f32_to_bf16_bits(acc[2 * i + 1]) << 16);
+        q[i] = f32x2_to_bf16x2_bits(acc[2 * i], acc[2 * i + 1]);
       *(u32x4_t *)((uint16_t *)out + t * H + c) = q;
     }
   }
