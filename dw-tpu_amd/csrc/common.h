@@ -147,6 +147,24 @@ __device__ __forceinline__ int wave_inclusive_scan(int v) {
   return v;
 }
 
+// N independent inclusive scans, step by step side by side, so that each DPP
+// step's latency is covered by the other scans' steps.
+template <int N>
+__device__ __forceinline__ void wave_inclusive_scan_n(int (&v)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += __builtin_amdgcn_update_dpp(0, v[i], 0x111, 0xF, 0xF, false);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += __builtin_amdgcn_update_dpp(0, v[i], 0x112, 0xF, 0xF, false);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += __builtin_amdgcn_update_dpp(0, v[i], 0x114, 0xF, 0xF, false);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += __builtin_amdgcn_update_dpp(0, v[i], 0x118, 0xF, 0xF, false);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += __builtin_amdgcn_update_dpp(0, v[i], 0x142, 0xA, 0xF, false);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += __builtin_amdgcn_update_dpp(0, v[i], 0x143, 0xC, 0xF, false);
+}
+
 // Lane 63's value, as a wave-uniform scalar (the total of an inclusive scan).
 __device__ __forceinline__ int wave_last(int v) { return __builtin_amdgcn_readlane(v, 63); }
 

@@ -417,7 +417,7 @@ __global__ __launch_bounds__(C::THREADS) void gmm_fp4_ws_kernel(
   static_assert(C::STAGES * C::STAGE >= (kMaxGroups + NC * kClsStride) * 4, "tile classes alias the stages");
   static_assert(C::GT % (2 * C::NPROD) == 0, "a narrow tile's groups split evenly over the producers");
   __shared__ __attribute__((aligned(1024))) uint8_t s_lds[C::STAGES * C::STAGE];
-  __shared__ int s_info[4];
+  __shared__ int s_info[kTileInfo];
   int *s_rowstart = (int *)s_lds;
   int *s_cls = s_rowstart + kMaxGroups;
 

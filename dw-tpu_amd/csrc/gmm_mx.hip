@@ -456,7 +456,7 @@ __global__ __launch_bounds__(C::THREADS) void gmm_mx_kernel(
   constexpr int CW = C::CONS, NP = C::NPROD, TMB = C::TMB, CMB = C::CMB;
   static_assert(C::STAGES * C::STAGE >= (kMaxGroups + TMB * kClsStride) * 4, "tile classes alias the stages");
   __shared__ __attribute__((aligned(1024))) uint8_t s_lds[C::STAGES * C::STAGE];
-  __shared__ int s_info[4];
+  __shared__ int s_info[kTileInfo];
   int *s_rowstart = (int *)s_lds;
   int *s_cls = s_rowstart + kMaxGroups;
 
@@ -713,7 +713,7 @@ __global__ __launch_bounds__(C::THREADS) void gmm_mx128_kernel(
   constexpr int CW = C::CONS, NP = C::NPROD;
   static_assert(C::STAGES * C::STAGE >= (kMaxGroups + MB * kClsStride) * 4, "tile classes alias the stages");
   __shared__ __attribute__((aligned(1024))) uint8_t s_lds[C::STAGES * C::STAGE];
-  __shared__ int s_info[4];
+  __shared__ int s_info[kTileInfo];
   int *s_rowstart = (int *)s_lds;
   int *s_cls = s_rowstart + kMaxGroups;
   const int tid = threadIdx.x, wave = tid >> 6;

@@ -91,37 +91,23 @@ struct TileRef {
   int g, rows, nt, narrow;
   int64_t row0;
 };
+constexpr int kTileInfo = 5;  // s_info: g (-1: no tile), row0, rows, nt, narrow
 
-// Every thread of the block calls this (it holds two block barriers).  Work
-// list: the (row tile, column tile) pairs of class 0 (NC blocks), then class
-// 1, ... (longest first, so the dispatcher's in-order refill of free CUs
-// balances them).  Each class is cut into 8 contiguous runs, one per XCD
-// (blocks equal mod 8 run on one XCD), so a row tile's column tiles share
-// that XCD's L2.
-//
-// Narrow split (n_tiles_n > 0): when the wide tiles leave some of the ncu CUs
-// idle, the costliest classes are cut into column tiles of half the width
-// (n_tiles_n per row tile), whole classes at a time and only while the tile
-// count stays within ncu, so the longest tiles of a one-round launch get the
-// idle CUs.  Returns false when the block has no tile.
-template <int MB, int CG, int THREADS>
-__device__ __forceinline__ bool find_tile(const int32_t *__restrict__ group_sizes, int num_groups, int go,
-                                          int64_t e_local, int64_t M, int n_tiles, int n_tiles_n, int ncu, int bal,
-                                          int *s_rowstart, int *s_cls, int *s_info, TileRef &ref) {
-  constexpr int MT = 32 * MB, NC = MT / CG;
-  const int tid = threadIdx.x;
-  tile_classes<MB, CG>(group_sizes, num_groups, go, e_local, bal, s_rowstart, s_cls);
-  if (tid == 0) s_info[0] = -1;
-  __syncthreads();
-  int nsplit = 0;
+// The block's work-list entry from the class totals tot(a) (see find_tile):
+// the narrow split, then the class `cls` (-1: no tile) of block (xcd, j),
+// its entry within the class and the class's column tiles per row tile.
+template <int NC, class Tot>
+__device__ __forceinline__ void class_entry(Tot tot, int n_tiles, int n_tiles_n, int ncu, int &nsplit, int &cls,
+                                            int &per_row, int64_t &entry) {
+  nsplit = 0;
   if (n_tiles_n > 0) {
     int64_t spare = (int64_t)ncu;
 #pragma unroll
-    for (int a = 0; a < NC; ++a) spare -= (int64_t)s_cls[a * kClsStride + num_groups] * n_tiles;
+    for (int a = 0; a < NC; ++a) spare -= (int64_t)tot(a) * n_tiles;
     bool open = true;
 #pragma unroll
     for (int a = 0; a < NC; ++a) {
-      const int64_t extra = (int64_t)s_cls[a * kClsStride + num_groups] * (n_tiles_n - n_tiles);
+      const int64_t extra = (int64_t)tot(a) * (n_tiles_n - n_tiles);
       if (open && extra <= spare) {
         spare -= extra;
         nsplit = a + 1;
@@ -132,12 +118,13 @@ __device__ __forceinline__ bool find_tile(const int32_t *__restrict__ group_size
   }
   const int xcd = blockIdx.x & 7;
   int64_t j = blockIdx.x >> 3;
-  int cls = -1, per_row = n_tiles;
-  int64_t entry = 0;
+  cls = -1;
+  per_row = n_tiles;
+  entry = 0;
 #pragma unroll
   for (int a = 0; a < NC; ++a) {
     const int nt_a = a < nsplit ? n_tiles_n : n_tiles;
-    const int64_t n_a = (int64_t)s_cls[a * kClsStride + num_groups] * nt_a;
+    const int64_t n_a = (int64_t)tot(a) * nt_a;
     const int64_t per = (n_a + 7) / 8;
     const int64_t lo = xcd * per, hi = min(lo + per, n_a);
     const int64_t len = hi > lo ? hi - lo : 0;
@@ -151,40 +138,133 @@ __device__ __forceinline__ bool find_tile(const int32_t *__restrict__ group_size
       }
     }
   }
-  const int trow = cls >= 0 ? (int)(entry / per_row) : -1;
+}
+
+// Rows and column tile of entry `entry` (row tile trow of class cls) in
+// group g of sz rows starting at row rs, whose class-cls row tiles start at
+// cs_g in the class's list.  s_info[1 .. 3] = row0, rows, nt.
+template <int MT, int CG>
+__device__ __forceinline__ void tile_rows(int sz, int rs, int cs_g, int cls, int trow, int64_t entry, int per_row,
+                                          int bal, int *s_info) {
+  const RowSplit<MT, CG> sp(sz, bal);
+  if (sp.bal) {
+    // (column tile, row tile) with the row tile innermost; tile tt starts
+    // after tt * base + min(tt, extra) blocks.
+    const int64_t local = entry - (int64_t)cs_g * per_row;
+    const int tt = (int)(local % sp.n);
+    const int base = sp.nb / sp.n, extra = sp.nb % sp.n;
+    const int b0 = tt * base + min(tt, extra);
+    s_info[1] = rs + CG * b0;
+    s_info[2] = min(CG * (base + (tt < extra ? 1 : 0)), sz - CG * b0);
+    s_info[3] = (int)(local / sp.n);
+  } else {
+    // Class 0 holds the full tiles (then a partial one of NC blocks); the
+    // other classes hold one partial tile per group.
+    const int tt = cls == 0 ? trow - cs_g : sz / MT;
+    s_info[1] = rs + tt * MT;
+    s_info[2] = min(MT, sz - tt * MT);
+    s_info[3] = (int)(entry % per_row);
+  }
+}
+
+// Wave 0 lists the tiles of at most 64 groups (group g in lane g) without
+// LDS: the row starts and the per-class tile counts are seven independent
+// prefix sums run side by side in registers, the block's group is the one
+// lane whose class range holds its row tile (a ballot), and that lane's
+// values are read with readlane.  Same list and same tile as the LDS path.
+template <int MB, int CG>
+__device__ __forceinline__ void pick_tile_lanes(const int32_t *__restrict__ group_sizes, int num_groups, int go,
+                                                int64_t e_local, int n_tiles, int n_tiles_n, int ncu, int bal,
+                                                int *s_info) {
+  constexpr int MT = 32 * MB, NC = MT / CG;
+  const int g = threadIdx.x & 63;
+  int sz = g < num_groups ? group_sizes[g] : 0;
+  sz = sz > 0 ? sz : 0;
+  const bool local = g >= go && (int64_t)g < (int64_t)go + e_local;
+  const RowSplit<MT, CG> sp(local ? sz : 0, bal);
+  const int n_full = local && !sp.bal ? sz / MT : 0;
+  const int rem = local && !sp.bal ? sz % MT : 0;
+  const int rem_cls = (rem + CG - 1) / CG;  // 0 when there is no partial tile
+  int cnt[NC], inc[NC + 1];
+#pragma unroll
+  for (int a = 0; a < NC; ++a) {
+    cnt[a] = sp.bal ? (sp.top == NC - a ? sp.n : 0) : (a == 0 ? n_full : 0) + (rem_cls == NC - a ? 1 : 0);
+    inc[a] = cnt[a];
+  }
+  inc[NC] = sz;
+  wave_inclusive_scan_n<NC + 1>(inc);
+  int tot[NC];
+#pragma unroll
+  for (int a = 0; a < NC; ++a) tot[a] = wave_last(inc[a]);
+  int nsplit, cls, per_row;
+  int64_t entry;
+  class_entry<NC>([&](int a) { return tot[a]; }, n_tiles, n_tiles_n, ncu, nsplit, cls, per_row, entry);
+  int gsel = -1;
+  int trow = 0, ci = 0, cc = 0;
   if (cls >= 0) {
-    const int *const cs = s_cls + cls * kClsStride;
-    for (int g = tid; g < num_groups; g += THREADS) {
-      if (cs[g] <= trow && trow < cs[g + 1]) {
-        const int sz = group_sizes[g];
-        const RowSplit<MT, CG> sp(sz, bal);
-        s_info[0] = g;
-        if (sp.bal) {
-          // (column tile, row tile) with the row tile innermost; tile tt
-          // starts after tt * base + min(tt, extra) blocks.
-          const int64_t local = entry - (int64_t)cs[g] * per_row;
-          const int tt = (int)(local % sp.n);
-          const int base = sp.nb / sp.n, extra = sp.nb % sp.n;
-          const int b0 = tt * base + min(tt, extra);
-          s_info[1] = s_rowstart[g] + CG * b0;
-          s_info[2] = min(CG * (base + (tt < extra ? 1 : 0)), sz - CG * b0);
-          s_info[3] = (int)(local / sp.n);
-        } else {
-          // Class 0 holds the full tiles (then a partial one of NC blocks);
-          // the other classes hold one partial tile per group.
-          const int tt = cls == 0 ? trow - cs[g] : sz / MT;
-          s_info[1] = s_rowstart[g] + tt * MT;
-          s_info[2] = min(MT, sz - tt * MT);
-          s_info[3] = (int)(entry % per_row);
+    trow = (int)(entry / per_row);
+#pragma unroll
+    for (int a = 0; a < NC; ++a)
+      if (a == cls) ci = inc[a], cc = cnt[a];
+    const uint64_t hit = __ballot(g < num_groups && ci - cc <= trow && trow < ci);
+    if (hit) gsel = __ffsll((unsigned long long)hit) - 1;
+  }
+  const int rs = __builtin_amdgcn_readlane(inc[NC] - sz, gsel < 0 ? 0 : gsel);
+  const int szg = __builtin_amdgcn_readlane(sz, gsel < 0 ? 0 : gsel);
+  const int csg = __builtin_amdgcn_readlane(ci - cc, gsel < 0 ? 0 : gsel);
+  if (g == 0) {
+    s_info[0] = gsel;
+    s_info[4] = cls >= 0 && cls < nsplit;
+    if (gsel >= 0) tile_rows<MT, CG>(szg, rs, csg, cls, trow, entry, per_row, bal, s_info);
+  }
+}
+
+// Every thread of the block calls this (it holds one block barrier, two
+// when there are more than 64 groups).  Work list: the (row tile, column
+// tile) pairs of class 0 (NC blocks), then class 1, ... (longest first, so
+// the dispatcher's in-order refill of free CUs balances them).  Each class is
+// cut into 8 contiguous runs, one per XCD (blocks equal mod 8 run on one
+// XCD), so a row tile's column tiles share that XCD's L2.
+//
+// Narrow split (n_tiles_n > 0): when the wide tiles leave some of the ncu CUs
+// idle, the costliest classes are cut into column tiles of half the width
+// (n_tiles_n per row tile), whole classes at a time and only while the tile
+// count stays within ncu, so the longest tiles of a one-round launch get the
+// idle CUs.  Returns false when the block has no tile.
+template <int MB, int CG, int THREADS>
+__device__ __forceinline__ bool find_tile(const int32_t *__restrict__ group_sizes, int num_groups, int go,
+                                          int64_t e_local, int64_t M, int n_tiles, int n_tiles_n, int ncu, int bal,
+                                          int *s_rowstart, int *s_cls, int *s_info, TileRef &ref) {
+  constexpr int MT = 32 * MB, NC = MT / CG;
+  const int tid = threadIdx.x;
+  if (num_groups <= 64) {
+    if ((tid >> 6) == 0)
+      pick_tile_lanes<MB, CG>(group_sizes, num_groups, go, e_local, n_tiles, n_tiles_n, ncu, bal, s_info);
+  } else {
+    tile_classes<MB, CG>(group_sizes, num_groups, go, e_local, bal, s_rowstart, s_cls);
+    if (tid == 0) s_info[0] = -1;
+    __syncthreads();
+    int nsplit, cls, per_row;
+    int64_t entry;
+    class_entry<NC>([&](int a) { return s_cls[a * kClsStride + num_groups]; }, n_tiles, n_tiles_n, ncu, nsplit, cls,
+                    per_row, entry);
+    if (tid == 0) s_info[4] = cls >= 0 && cls < nsplit;
+    if (cls >= 0) {
+      const int trow = (int)(entry / per_row);
+      const int *const cs = s_cls + cls * kClsStride;
+      for (int g = tid; g < num_groups; g += THREADS) {
+        if (cs[g] <= trow && trow < cs[g + 1]) {
+          s_info[0] = g;
+          tile_rows<MT, CG>(group_sizes[g], s_rowstart[g], cs[g], cls, trow, entry, per_row, bal, s_info);
         }
       }
     }
   }
   __syncthreads();  // also retires the class reads before the stages overwrite them
   ref.g = s_info[0];
-  if (cls < 0 || ref.g < 0) return false;
+  if (ref.g < 0) return false;
   ref.nt = s_info[3];
-  ref.narrow = cls < nsplit;
+  ref.narrow = s_info[4];
   ref.row0 = s_info[1];
   // group_sizes lives on the device and is not checked by the host: sizes
   // whose sum leaves int32 would give row starts outside [0, M).  Such tiles
