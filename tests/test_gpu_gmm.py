@@ -284,6 +284,29 @@ def test_gmm_balanced_tile_bound_changes_only_the_schedule(dev, monkeypatch, nam
         assert torch.equal(yb.view(torch.int32), y.view(torch.int32)), bound
 
 
+@pytest.mark.parametrize("mx", [False, True])
+@pytest.mark.parametrize("name", ["decode_gate_up", "decode_down", "prefill"])
+def test_gmm_tile_list_paths_agree(dev, name, mx):
+    """Up to 64 groups wave 0 builds the tile list in registers; above 64 it
+    goes through LDS (find_tile).  Empty groups appended after the local ones
+    own no rows and no tile, so the list -- and every output bit -- stays the
+    same while the launch switches path (bf16 and MX kernels)."""
+    from dw_tpu_amd import fp4_weight_to_codes, gmm_v2
+    from dw_tpu_amd.workloads import make_gmm_workload
+    wl = make_gmm_workload(name)
+    pw = fp4_weight_to_codes(torch.from_numpy(wl.rhs_e2m1).to(dev), torch.from_numpy(wl.scale_codes).to(dev))
+    lhs = bf16_tensor(wl.lhs_bits, dev)
+    gs = torch.from_numpy(wl.group_sizes).to(dev)
+    assert len(gs) <= 64
+    gs_long = torch.cat([gs, torch.zeros(72 - len(gs), dtype=gs.dtype, device=dev)])
+    q = torch.float8_e4m3fn if mx else None
+    y = gmm_v2(lhs, pw, gs, preferred_element_type=torch.float32, lhs_quant_dtype=q)
+    yl = gmm_v2(lhs, pw, gs_long, preferred_element_type=torch.float32, lhs_quant_dtype=q)
+    torch.cuda.synchronize()
+    assert torch.isfinite(y).all()
+    assert torch.equal(yl.view(torch.int32), y.view(torch.int32))
+
+
 def test_gmm_full_size_row_permutation_and_group_independence(dev, rng):
     """decode_gate_up at full size: permuting rows inside each expert group
     permutes the output rows bit for bit (each row's result depends on its
