@@ -248,6 +248,46 @@ __device__ __forceinline__ void ws_consumer(int T, uint8_t *s_lds, int cw, int64
 #pragma unroll
     for (int i = 0; i < nb; ++i) an[i] = *(const u32x4_t *)(st + arow + (b0 + i) * 2048 + ach);
   };
+  // One MFMA group (row group rg of MFMA step v) on stage cs; ns is the next
+  // step's stage (read by the last group only).  par0 / par1: the scale
+  // parity of this step and of the next.
+  auto run_group = [&](const uint8_t *cs, const uint8_t *ns, auto vc, auto rgc, int par0, int par1) {
+    constexpr int v = decltype(vc)::value, rg = decltype(rgc)::value;
+    constexpr int nb = (DRG == 2 && rg == 0) ? G0 : 3;
+    constexpr int b0 = (DRG == 2 && rg == 1) ? G0 : 0;
+    u32x4_t a[3];
+#pragma unroll
+    for (int i = 0; i < nb; ++i) a[i] = an[i];
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (rg + 1 < DRG) read_g(cs, v, rg + 1);
+    else if constexpr (v == 0) read_g(cs, 1, 0);
+    else read_g(ns, 0, 0);
+    if constexpr (rg + 1 < DRG) {
+#pragma unroll
+      for (int i = 0; i < nb; ++i)
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          acc[b0 + i][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              __builtin_bit_cast(bf16x8_t, a[i]), __builtin_bit_cast(bf16x8_t, bop[u]), acc[b0 + i][u], 0, 0, 0);
+    } else {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+#pragma unroll
+        for (int i = 0; i < nb; ++i)
+          acc[b0 + i][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              __builtin_bit_cast(bf16x8_t, a[i]), __builtin_bit_cast(bf16x8_t, bop[u]), acc[b0 + i][u], 0, 0, 0);
+        decode(u, v == 0 ? 1 : 0, v == 0 ? par0 : par1);
+        __builtin_amdgcn_sched_barrier(0);  // keep each decode after the MFMAs that read the old bop[u]
+      }
+      if constexpr (v == 0) read_w(ns);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // With two row groups, the first group of step t + 1 runs before barrier
+  // t + 1: that step was published at barrier t, and its lhs fragments and
+  // B operands are already in registers, so the wave that finishes step t
+  // first keeps the SIMD's MFMA unit busy instead of waiting.  Every
+  // accumulator still takes its MFMAs in step order.
   static_assert(NS % 2 == 0, "t & 1 == cur & 1");
   for (int t0 = 0; t0 < T; t0 += NS) {
 #pragma unroll
@@ -268,40 +308,13 @@ __device__ __forceinline__ void ws_consumer(int T, uint8_t *s_lds, int cw, int64
 #pragma unroll
       for (int u = 0; u < 4; ++u) decode(u, 0, 0);
     }
-#pragma unroll
-    for (int v = 0; v < 2; ++v) {
-#pragma unroll
-      for (int rg = 0; rg < DRG; ++rg) {
-        const int nb = (DRG == 2 && rg == 0) ? G0 : 3;
-        const int b0 = (DRG == 2 && rg == 1) ? G0 : 0;
-        u32x4_t a[3];
-#pragma unroll
-        for (int i = 0; i < nb; ++i) a[i] = an[i];
-        __builtin_amdgcn_sched_barrier(0);
-        if (rg + 1 < DRG) read_g(st, v, rg + 1);
-        else if (v == 0) read_g(st, 1, 0);
-        else read_g(sx, 0, 0);
-        if (rg + 1 < DRG) {
-#pragma unroll
-          for (int i = 0; i < nb; ++i)
-#pragma unroll
-            for (int u = 0; u < 4; ++u)
-              acc[b0 + i][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                  __builtin_bit_cast(bf16x8_t, a[i]), __builtin_bit_cast(bf16x8_t, bop[u]), acc[b0 + i][u], 0, 0, 0);
-        } else {
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {
-#pragma unroll
-            for (int i = 0; i < nb; ++i)
-              acc[b0 + i][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                  __builtin_bit_cast(bf16x8_t, a[i]), __builtin_bit_cast(bf16x8_t, bop[u]), acc[b0 + i][u], 0, 0, 0);
-            decode(u, v == 0 ? 1 : 0, v == 0 ? (cur & 1) : ((cur + 1) & 1));
-            __builtin_amdgcn_sched_barrier(0);  // keep each decode after the MFMAs that read the old bop[u]
-          }
-          if (v == 0) read_w(sx);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-      }
+    const int p0 = cur & 1, p1 = (cur + 1) & 1;
+    if (DRG == 1 || t == 0) run_group(st, sx, IntC<0>{}, IntC<0>{}, p0, p1);
+    if constexpr (DRG == 2) run_group(st, sx, IntC<0>{}, IntC<1>{}, p0, p1);
+    run_group(st, sx, IntC<1>{}, IntC<0>{}, p0, p1);
+    if constexpr (DRG == 2) {
+      run_group(st, sx, IntC<1>{}, IntC<1>{}, p0, p1);
+      if (t + 1 < T) run_group(sx, sx, IntC<0>{}, IntC<0>{}, p1, p0);
     }
   }
   }
