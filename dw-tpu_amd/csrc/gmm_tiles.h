@@ -168,10 +168,11 @@ __device__ __forceinline__ void tile_rows(int sz, int rs, int cs_g, int cls, int
 }
 
 // Wave 0 lists the tiles of at most 64 groups (group g in lane g) without
-// LDS: the row starts and the per-class tile counts are seven independent
-// prefix sums run side by side in registers, the block's group is the one
-// lane whose class range holds its row tile (a ballot), and that lane's
-// values are read with readlane.  Same list and same tile as the LDS path.
+// LDS: the row starts and the per-class tile counts are independent prefix
+// sums (one of sizes, one per class) run side by side in registers, the
+// block's group is the one lane whose class range holds its row tile (a
+// ballot), and that lane's values are read with readlane.  Same list and
+// same tile as the LDS path.
 template <int MB, int CG>
 __device__ __forceinline__ void pick_tile_lanes(const int32_t *__restrict__ group_sizes, int num_groups, int go,
                                                 int64_t e_local, int n_tiles, int n_tiles_n, int ncu, int bal,
