@@ -549,6 +549,109 @@ def prep_dense(dev, steps, warmup, ms_list=(1, 16, 128, 1024, 4096)):
     return run
 
 
+TIMELINE_SLOTS = 24  # words per block record of the timeline build (kTlSlots in csrc/gmm_fp4.hip)
+
+
+def probe_timeline(dev, names=("decode_gate_up", "decode_down", "prefill")):
+    """Profiling aid (``--probe timeline``): the bf16 gmm's per-block
+    timeline from the library's timeline build (libdwtpu_moe_timeline.so:
+    the same kernels with s_memrealtime / s_memtime stores compiled in), one
+    launch per workload after at least 0.2 s of warmup launches.  Per block: entry, the
+    tile's rows, consumer wave 0's first barrier / K-loop end / stores issued,
+    every wave's exit (100 MHz realtime, one clock for all XCDs) and wave 0's
+    shader-clock counter.  Reports, per row-block count (narrow tiles apart),
+    the blocks' spans from entry to the last wave's exit; the mean phases of
+    consumer wave 0; tiles per CU and the quantiles of the tile blocks'
+    start times (the rounds of a multi-round launch); the shader clock."""
+    import numpy as np
+    import torch
+    from dw_tpu_amd import _lib, fp4_weight_to_codes
+    from dw_tpu_amd.workloads import make_gmm_workload
+    lib = ctypes.CDLL(os.path.join(os.path.dirname(_lib.LIB_PATH), "libdwtpu_moe_timeline.so"))
+    for n, a in _lib.SIGNATURES.items():
+        f = getattr(lib, n)
+        f.argtypes = a
+        f.restype = _lib._RESTYPES.get(n, ctypes.c_int)
+    lib.dwm_timeline_set.argtypes = [ctypes.c_void_p, ctypes.c_int64]
+    st = _lib.stream_handle(dev)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    out_all = {}
+    for name in names:
+        wl = make_gmm_workload(name)
+        pw = fp4_weight_to_codes(torch.from_numpy(wl.rhs_e2m1).to(dev), torch.from_numpy(wl.scale_codes).to(dev))
+        lhs = torch.from_numpy(wl.lhs_bits.view(np.int16)).view(torch.bfloat16).to(dev)
+        gs = torch.from_numpy(wl.group_sizes).to(dev)
+        out = torch.empty((wl.M, wl.N), dtype=torch.bfloat16, device=dev)
+        blocks = 16384
+        buf = torch.zeros(blocks * TIMELINE_SLOTS, dtype=torch.int64, device=dev)
+
+        def launch():
+            rc = lib.dwm_gmm_fp4(P(lhs), wl.M, wl.K, P(pw.weight), P(pw.scale), P(gs), wl.E, None, wl.E, wl.N,
+                                 P(out), _lib.BF16, 0, 0, st)
+            if rc:
+                raise RuntimeError(lib.dwm_last_error().decode())
+
+        if lib.dwm_timeline_set(None, 0):
+            raise RuntimeError(lib.dwm_last_error().decode())
+        # At least 0.2 s of back-to-back launches first: after the host-side
+        # input generation the power manager needs tens of ms of load to
+        # bring the clock back up.
+        t_end = time.time() + 0.2
+        n = 0
+        while n < 30 or time.time() < t_end:
+            for _ in range(10):
+                launch()
+            n += 10
+            torch.cuda.synchronize()
+        if lib.dwm_timeline_set(P(buf), blocks):
+            raise RuntimeError(lib.dwm_last_error().decode())
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        launch()
+        e1.record()
+        torch.cuda.synchronize()
+        lib.dwm_timeline_set(None, 0)
+        d = buf.view(blocks, TIMELINE_SLOTS).cpu().numpy().astype(np.int64)
+        d = d[d[:, 0] != 0]
+        rows = d[:, 3] & 0xFFFF
+        narrow = (d[:, 3] >> 16) & 1
+        exits = np.where(d[:, 8:20] != 0, d[:, 8:20], 0).max(axis=1)
+        t0 = d[:, 0].min()
+        tiles = d[rows > 0]
+        tr, tn, tx = rows[rows > 0], narrow[rows > 0], exits[rows > 0]
+        span = (tx - tiles[:, 0]) / 100.0
+        classes = {}
+        for nh in sorted(set(((tr + 15) // 16).tolist())):
+            for nw in (0, 1):
+                m = ((tr + 15) // 16 == nh) & (tn == nw)
+                if m.any():
+                    classes[f"{nh} blocks{' narrow' if nw else ''}"] = {
+                        "tiles": int(m.sum()), "span_us_mean": round(float(span[m].mean()), 1),
+                        "span_us_min": round(float(span[m].min()), 1), "span_us_max": round(float(span[m].max()), 1)}
+        ph = lambda a, b: round(float(((tiles[:, b] - tiles[:, a]) / 100.0).mean()), 2)  # noqa: E731
+        cu = (tiles[:, 1] >> 32) * 256 + ((tiles[:, 1] >> 8) & 0xFF)  # XCC_ID, then CU / SH / SE of HW_ID
+        per_cu = np.unique(np.unique(cu, return_counts=True)[1], return_counts=True)
+        starts = np.sort(tiles[:, 0] - t0) / 100.0
+        w0 = (tiles[:, 8] > tiles[:, 0]) & (tiles[:, 20] > tiles[:, 7])
+        clock = float(np.median((tiles[w0, 20] - tiles[w0, 7]) / (tiles[w0, 8] - tiles[w0, 0]) / 10.0))
+        out_all[name] = {
+            "event_us": round(e0.elapsed_time(e1) * 1e3, 1),
+            "blocks": int(len(d)), "tile_blocks": int(len(tiles)),
+            "first_entry_to_last_exit_us": round(float((exits.max() - t0) / 100.0), 1),
+            "shader_clock_GHz": round(clock, 3),
+            "by_row_blocks": classes,
+            "phases_us_mean": {"entry_to_tile": ph(0, 2), "tile_to_first_barrier": ph(2, 4), "k_loop": ph(4, 5),
+                               "epilogue_stores_issued": ph(5, 6),
+                               "stores_to_last_exit": round(float(((tx - tiles[:, 6]) / 100.0).mean()), 2)},
+            "tiles_per_cu": {int(k): int(v) for k, v in zip(*per_cu)},
+            "tile_start_us_quantiles": [round(float(np.quantile(starts, q)), 1) for q in (0, .125, .25, .375, .5,
+                                                                                           .625, .75, .875, 1)],
+        }
+        log(f"timeline {name}: {out_all[name]}")
+        del pw, lhs, gs, out, buf
+    return out_all
+
+
 def probe_equal_experts(dev, kind):
     """Profiling aid (``--probe``): the grouped matmul on synthetic equal
     experts (K = 7168, N = 4096, random prepacked weights, two copies
@@ -754,9 +857,10 @@ def main():
     ap.add_argument("--extra", choices=["all", "none"], default="all")
     ap.add_argument("--cpu-budget", type=float, default=15.0,
                     help="seconds of CPU-baseline work (0 skips it)")
-    ap.add_argument("--probe", choices=("rows", "cus"), default=None,
+    ap.add_argument("--probe", choices=("rows", "cus", "timeline"), default=None,
                     help="profiling aid: the grouped matmul on synthetic equal experts (rows per expert, or all "
-                         "CUs busy); prints {\"probe\": kind, \"us\": {...}}; not the benchmark line")
+                         "CUs busy), or the per-block timeline of the bf16 gmm on the three workloads (the "
+                         "library's timeline build); prints {\"probe\": kind, ...}; not the benchmark line")
     ap.add_argument("--calib-copy", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy (byte-counter calibration)")
     ap.add_argument("--only", choices=ONLY_CHOICES, default=None,
@@ -773,6 +877,9 @@ def main():
     import numpy as np
     import torch
     dev = torch.device("cuda:0")
+    if args.probe == "timeline":
+        print(json.dumps({"probe": "timeline", "workloads": probe_timeline(dev)}), flush=True)
+        return
     if args.probe:
         print(json.dumps({"probe": args.probe, "us": probe_equal_experts(dev, args.probe)}), flush=True)
         return

@@ -31,6 +31,27 @@
 
 namespace dwm {
 
+// Per-block timeline, compiled only into the timeline build of the library
+// (-DDWTPU_TIMELINE, libdwtpu_moe_timeline.so; the product library has no
+// trace of it).  Lane 0 of a wave stores a counter into slot `slot` of its
+// block's record of kTlSlots words: s_memrealtime (100 MHz, the same clock
+// on every XCD) unless noted.  Slots: 0 block entry; 1 HW_ID | XCC_ID << 32;
+// 2 tile found; 3 rows | narrow << 16 (0: no tile); 4, 5, 6 consumer wave
+// 0's first barrier passed, K loop done, stores issued; 7 and 20 wave 0's
+// s_memtime (shader clock) at entry and exit; 8 + w wave w's exit.
+constexpr int kTlSlots = 24;
+#ifdef DWTPU_TIMELINE
+static __device__ uint64_t *g_timeline;
+static __device__ int64_t g_timeline_blocks;
+#define DWM_TL(slot, v)                                                                     \
+  do {                                                                                      \
+    if ((threadIdx.x & 63) == 0 && g_timeline && (int64_t)blockIdx.x < g_timeline_blocks) \
+      g_timeline[(int64_t)blockIdx.x * kTlSlots + (slot)] = (uint64_t)(v);                  \
+  } while (0)
+#else
+#define DWM_TL(slot, v) ((void)0)
+#endif
+
 // lhs tile rows hold 8 16-byte chunks; chunk c of row r sits at physical
 // chunk c ^ ((r >> 1) & 7), so that the 16 lanes of one LDS cycle (16
 // consecutive rows, one logical chunk) hit 16 distinct 16-byte bank groups.
@@ -303,6 +324,7 @@ __device__ __forceinline__ void ws_consumer(int T, uint8_t *s_lds, int cw, int64
     // Step t + 1 was published at this barrier (stale contents in the last step, never used).
     const uint8_t *const sx = s_lds + nxt * C::STAGE;
     if (t == 0) {
+      if (cw == 0) DWM_TL(4, __builtin_amdgcn_s_memrealtime());
       read_w(st);
       read_g(st, 0, 0);
 #pragma unroll
@@ -338,6 +360,7 @@ __device__ __forceinline__ void ws_consumer(int T, uint8_t *s_lds, int cw, int64
     // stale stage contents that are never used.
     const uint8_t *const sx = s_lds + nxt * C::STAGE;
     if (t == 0) {
+      if (cw == 0) DWM_TL(4, __builtin_amdgcn_s_memrealtime());
       read_w(st);
       read_a(st, 0, 0);
     }
@@ -385,12 +408,14 @@ __device__ __forceinline__ void ws_consumer(int T, uint8_t *s_lds, int cw, int64
   // One more barrier: every wave is done with the stages and every load has
   // landed, so each consumer stages its results in a private LDS region and
   // writes whole 8-column runs of a row.
+  if (cw == 0) DWM_TL(5, __builtin_amdgcn_s_memrealtime());
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
   store_halves<NH, ACT, C::EP_STRIDE>(acc, (float *)(s_lds + cw * 32 * C::EP_STRIDE * 4), row0, rows, col0, N, out,
                                       out_f32, bias, ep.bias_bf16, ep.act);
+  if (cw == 0) DWM_TL(6, __builtin_amdgcn_s_memrealtime());
 }
 
 // A consumer wave with no columns in a narrow tile: it only keeps the
@@ -435,14 +460,34 @@ __global__ __launch_bounds__(C::THREADS) void gmm_fp4_ws_kernel(
   int *s_cls = s_rowstart + kMaxGroups;
 
   const int tid = threadIdx.x, wave = tid >> 6;
+  if (wave == 0) {
+    DWM_TL(0, __builtin_amdgcn_s_memrealtime());
+    DWM_TL(7, __builtin_amdgcn_s_memtime());
+    DWM_TL(1, (uint32_t)__builtin_amdgcn_s_getreg(4 | (31 << 11)) |
+                  ((uint64_t)(uint32_t)__builtin_amdgcn_s_getreg(20 | (31 << 11)) << 32));
+  }
+  // Every wave's exit (timeline build only).
+  auto tl_exit = [&]() {
+#ifdef DWTPU_TIMELINE
+    __builtin_amdgcn_s_waitcnt(0);
+    DWM_TL(8 + wave, __builtin_amdgcn_s_memrealtime());
+    if (wave == 0) DWM_TL(20, __builtin_amdgcn_s_memtime());
+#endif
+  };
   const int go = group_offset ? group_offset[0] : 0;
   const int G = (N + 63) >> 6;
   const int n_tiles = (G + C::GT - 1) / C::GT;
   const int n_tiles_n = NARROW ? (G + C::GT / 2 - 1) / (C::GT / 2) : 0;
   TileRef ref;
   if (!find_tile<MB, 16, C::THREADS>(group_sizes, num_groups, go, e_local, M, n_tiles, n_tiles_n, ncu, bal,
-                                     s_rowstart, s_cls, s_info, ref))
+                                     s_rowstart, s_cls, s_info, ref)) {
+    tl_exit();
     return;
+  }
+  if (wave == 0) {
+    DWM_TL(2, __builtin_amdgcn_s_memrealtime());
+    DWM_TL(3, (uint32_t)ref.rows | ((uint32_t)ref.narrow << 16));
+  }
   const int g = ref.g, nt = ref.nt, rows = ref.rows;
   const bool narrow = NARROW && ref.narrow;
   const int64_t row0 = ref.row0;
@@ -459,12 +504,14 @@ __global__ __launch_bounds__(C::THREADS) void gmm_fp4_ws_kernel(
       ws_produce<C, C::G_LOADS / 2>(na, lhs, row_idx, lhs_rows, row0, rows, K, T, KB, wexp, sexp, g0, G, s_lds, pw);
     else
       ws_produce<C, C::G_LOADS>(na, lhs, row_idx, lhs_rows, row0, rows, K, T, KB, wexp, sexp, g0, G, s_lds, pw);
+    tl_exit();
     return;
   }
   // Every consumer runs exactly T + 1 barriers (the producers' count),
   // whatever its row-block count.
   if (narrow && wave >= C::GT / 2) {
     ws_idle_consumer(T);
+    tl_exit();
     return;
   }
   const int nh = (rows + 15) >> 4;  // 16-row blocks holding rows
@@ -478,6 +525,7 @@ __global__ __launch_bounds__(C::THREADS) void gmm_fp4_ws_kernel(
     case 5: ws_consumer<C, 5, ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32, bias, ep); break;
     default: ws_consumer<C, 6, ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32, bias, ep); break;
   }
+  tl_exit();
 }
 
 // zero_initialize: zero rows outside [start(go), start(go + E_local)).
@@ -652,6 +700,19 @@ static int gmm_run(const dwm_gmm_lhs &L, int64_t M, int64_t K, const uint8_t *we
 }  // namespace dwm
 
 using namespace dwm;
+
+#ifdef DWTPU_TIMELINE
+// Timeline build only: record the bf16 gmm kernel's blocks 0 .. blocks - 1
+// into buf (blocks x kTlSlots words, zeroed by the caller), or stop (NULL).
+extern "C" int dwm_timeline_set(uint64_t *buf, int64_t blocks) {
+  clear_error();
+  DWM_CHECK_ARG(blocks >= 0 && (buf || blocks == 0), "timeline_set: bad buffer");
+  if (hipMemcpyToSymbol(HIP_SYMBOL(dwm::g_timeline), &buf, sizeof(buf)) != hipSuccess ||
+      hipMemcpyToSymbol(HIP_SYMBOL(dwm::g_timeline_blocks), &blocks, sizeof(blocks)) != hipSuccess)
+    return launch_status("timeline_set");
+  return DWM_OK;
+}
+#endif
 
 extern "C" int dwm_gmm_fp4_ex(const dwm_gmm_lhs *lhs, int64_t M, int64_t K, const uint8_t *weight,
                               const uint8_t *scale, const void *rhs_bias, int bias_dtype, const int32_t *group_sizes,

@@ -307,6 +307,44 @@ def test_gmm_tile_list_paths_agree(dev, name, mx):
     assert torch.equal(yl.view(torch.int32), y.view(torch.int32))
 
 
+def test_gmm_timeline_build_same_bits(dev):
+    """The timeline build (libdwtpu_moe_timeline.so, what bench.py --probe
+    timeline loads) runs the same kernels with per-block timestamps compiled
+    in: the same output bits as the library, and every tile block's record is
+    in order (entry <= tile found <= consumer 0's first barrier <= its K loop
+    end <= its stores issued <= the block's last wave exit)."""
+    import ctypes
+    import os
+    from dw_tpu_amd import _lib, fp4_weight_to_codes, gmm_v2
+    from dw_tpu_amd.workloads import make_gmm_workload
+    tl = ctypes.CDLL(os.path.join(os.path.dirname(_lib.LIB_PATH), "libdwtpu_moe_timeline.so"))
+    tl.dwm_gmm_fp4.argtypes = _lib.SIGNATURES["dwm_gmm_fp4"]
+    tl.dwm_timeline_set.argtypes = [ctypes.c_void_p, ctypes.c_int64]
+    wl = make_gmm_workload("decode_down")
+    pw = fp4_weight_to_codes(torch.from_numpy(wl.rhs_e2m1).to(dev), torch.from_numpy(wl.scale_codes).to(dev))
+    lhs = bf16_tensor(wl.lhs_bits, dev)
+    gs = torch.from_numpy(wl.group_sizes).to(dev)
+    y = gmm_v2(lhs, pw, gs)
+    out = torch.empty_like(y)
+    blocks, slots = 4096, 24
+    buf = torch.zeros(blocks * slots, dtype=torch.int64, device=dev)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    assert tl.dwm_timeline_set(P(buf), blocks) == 0
+    rc = tl.dwm_gmm_fp4(P(lhs), wl.M, wl.K, P(pw.weight), P(pw.scale), P(gs), wl.E, None, wl.E, wl.N, P(out),
+                        _lib.BF16, 0, 0, _lib.stream_handle(dev))
+    torch.cuda.synchronize()
+    assert tl.dwm_timeline_set(None, 0) == 0
+    assert rc == 0
+    assert torch.equal(out.view(torch.int16), y.view(torch.int16))
+    d = buf.view(blocks, slots).cpu().numpy().astype(np.int64)
+    t = d[(d[:, 0] != 0) & ((d[:, 3] & 0xFFFF) > 0)]
+    assert len(t) == 896  # decode_down's tiles: 64 row tiles x 14 column tiles
+    last = t[:, 8:20].max(axis=1)
+    for a, b in ((0, 2), (2, 4), (4, 5), (5, 6)):
+        assert np.all(t[:, a] <= t[:, b]), (a, b)
+    assert np.all(t[:, 6] <= last)
+
+
 def test_gmm_full_size_row_permutation_and_group_independence(dev, rng):
     """decode_gate_up at full size: permuting rows inside each expert group
     permutes the output rows bit for bit (each row's result depends on its
