@@ -307,6 +307,38 @@ def test_gmm_tile_list_paths_agree(dev, name, mx):
     assert torch.equal(yl.view(torch.int32), y.view(torch.int32))
 
 
+@pytest.mark.parametrize("mx", [False, True])
+def test_gmm_tile_list_paths_agree_with_window(dev, rng, mx):
+    """As above with a group_offset window inside 48 groups (groups before
+    the window shift the row starts; groups after it own no tiles), ragged
+    and empty local groups, balanced and partial row tiles: the register
+    path (48 groups) and the LDS path (the same groups plus 20 empty ones)
+    give the same bits."""
+    from dw_tpu_amd import fp4_weight_to_codes, gmm_v2
+    K, N, go, e_local = 256, 1024, 10, 20
+    sizes = rng.integers(0, 200, 48).astype(np.int32)
+    sizes[rng.random(48) < 0.25] = 0
+    sizes[go + 3] = 7
+    sizes[go + 5] = 290  # a balanced group of 4 row tiles
+    M = int(sizes.sum())
+    lhs_bits = bf16_bits_np(rng.standard_normal((M, K)).astype(np.float32))
+    rhs = rng.integers(0, 256, (e_local, K, N // 2), dtype=np.uint8)
+    sc = rng.integers(123, 130, (e_local, K // 32, 1, N), dtype=np.uint8)
+    pw = fp4_weight_to_codes(torch.from_numpy(rhs).to(dev), torch.from_numpy(sc).to(dev))
+    lhs = bf16_tensor(lhs_bits, dev)
+    q = torch.float8_e4m3fn if mx else None
+    gs = torch.from_numpy(sizes).to(dev)
+    gs_long = torch.cat([gs, torch.zeros(20, dtype=gs.dtype, device=dev)])
+    y = gmm_v2(lhs, pw, gs, group_offset=go, preferred_element_type=torch.float32, lhs_quant_dtype=q)
+    yl = gmm_v2(lhs, pw, gs_long, group_offset=go, preferred_element_type=torch.float32, lhs_quant_dtype=q)
+    torch.cuda.synchronize()
+    assert torch.isfinite(y).all()
+    assert torch.equal(yl.view(torch.int32), y.view(torch.int32))
+    start = int(sizes[:go].sum())
+    stop = start + int(sizes[go:go + e_local].sum())
+    assert (y[:start] == 0).all() and (y[stop:] == 0).all() and (y[start:stop] != 0).any()
+
+
 def test_gmm_timeline_build_same_bits(dev):
     """The timeline build (libdwtpu_moe_timeline.so, what bench.py --probe
     timeline loads) runs the same kernels with per-block timestamps compiled
