@@ -158,6 +158,7 @@ _M, _K, _N = 160, 2048, 512  # 2 x 4 MFMA tiles: the default plan splits K 16 wa
     (None, (2, 128, 128, 16, 3)),                            # the library's plan
     (("native", 256, 2048, 128, 2), (2, 256, 128, 1, 2)),    # one 256-row tile per column tile, no split
     (("native", 128, 512, 128, 4), (2, 128, 128, 4, 4)),     # 4 K runs, 4-stage ring
+    (("native", 128, 512, 128, 3), (2, 128, 128, 4, 3)),     # 4 K runs, 3-stage ring
     (("megablox", 64, 1024, 128, 2), (3, 64, 128, 2, 2)),    # the general tiled kernel, 2 K runs
     (("megablox", 16, 2048, 64, 2), (3, 16, 64, 1, 2)),
 ])
@@ -181,6 +182,31 @@ def test_w8a16_tile_choice_is_launched(dev, tile, plan):
     xf = bf16_to_f32(wl.x_bits)
     y64 = odf.matmul_w8a16(xf, wl.wq, wl.s_w8a16, out_dtype="float64")
     print(tile, _check(out, y64, odf.abs_product_w8a16(xf, wl.wq, wl.s_w8a16), _K))
+
+
+@pytest.mark.parametrize("tk", [1024, 512, 384, 128])  # 2, 4, 6 (runs of 3, 3, 3, 3, 3, 1) and 16 K runs
+def test_w8a16_ring_depth_keeps_bits(dev, tk):
+    """With the same K runs, the ring depth only reschedules the same
+    products: 2, 3 and 4 stages give the same bits, through the split-K sum
+    in run order (this grid is small: the sum issues the loads of 2, 4 or 8
+    runs at a time, the last chunk of 6 and 16 runs partly past the end)."""
+    from dw_tpu_amd.dense_fp8 import last_plan, matmul
+    from dw_tpu_amd.workloads import make_dense_workload
+    wl = make_dense_workload(_M, _K, _N, seed=84)
+    x = bf16_tensor(wl.x_bits, dev)
+    w = torch.from_numpy(wl.wq).to(dev).view(torch.float8_e4m3fn)
+    s = torch.from_numpy(wl.s_w8a16).to(dev)
+    runs = -(-(_K // 128) // (tk // 128))
+    outs = []
+    for stages in (2, 3, 4):
+        outs.append(matmul(x, w, s, mode="native", tm=128, tk=tk, tn=128, stages=stages))
+        torch.cuda.synchronize()
+        assert last_plan().astuple() == (2, 128, 128, runs, stages)
+    for o in outs[1:]:
+        assert torch.equal(o.view(torch.int16), outs[0].view(torch.int16))
+    xf = bf16_to_f32(wl.x_bits)
+    _check(outs[0], odf.matmul_w8a16(xf, wl.wq, wl.s_w8a16, out_dtype="float64"),
+           odf.abs_product_w8a16(xf, wl.wq, wl.s_w8a16), _K)
 
 
 def test_override_file_steers_try_dense_fp8(dev, tmp_path, monkeypatch):
