@@ -550,6 +550,101 @@ def prep_dense(dev, steps, warmup, ms_list=(1, 16, 128, 1024, 4096)):
 
 
 TIMELINE_SLOTS = 24  # words per block record of the timeline build (kTlSlots in csrc/gmm_fp4.hip)
+DENSE_STEP_SLOTS = 10  # words per wave record of the dense step accounting (kDsSlots in csrc/dense_fp8.hip)
+
+
+def probe_dense_steps(dev, ms_list=(128, 1024)):
+    """Profiling aid (``--probe dense_steps``): where a K step of the dense
+    FP8 MFMA tile kernel goes, from the library's timeline build (the same
+    kernels with per-wave s_memtime sums compiled in): one launch of the
+    library's default plan per (M, variant) after at least 0.2 s of warmup
+    launches (K = 7168, N = 4096, the dense workload).  Each wave sums its
+    shader cycles waiting for data, at barriers and working between barriers;
+    reported per step, separately for the first and the second wave of each
+    SIMD (waves w and w + 4 of an 8-wave block), with the prologue (entry to
+    the first wait), the epilogue (loop end to its stores complete) and the
+    shader clock (s_memtime against s_memrealtime)."""
+    import numpy as np
+    import torch
+    from dw_tpu_amd import _lib
+    from dw_tpu_amd.dense_fp8 import prepack_fp8
+    from dw_tpu_amd.workloads import make_dense_workload
+    lib = ctypes.CDLL(os.path.join(os.path.dirname(_lib.LIB_PATH), "libdwtpu_moe_timeline.so"))
+    for n, a in _lib.SIGNATURES.items():
+        f = getattr(lib, n)
+        f.argtypes = a
+        f.restype = _lib._RESTYPES.get(n, ctypes.c_int)
+    lib.dwm_dense_steps_set.argtypes = [ctypes.c_void_p, ctypes.c_int64]
+    st = _lib.stream_handle(dev)
+    P = _lib.ptr
+    res = {}
+    for m in ms_list:
+        wl = make_dense_workload(m)
+        k, n = wl.K, wl.N
+        pw = prepack_fp8(torch.from_numpy(wl.wq).to(dev))
+        x = _to_dev_bf16(wl.x_bits, dev)
+        xq, sx, sw = (torch.from_numpy(v).to(dev) for v in (wl.xq, wl.sx, wl.sw))
+        s16 = torch.from_numpy(wl.s_w8a16.reshape(k // 128, n)).to(dev)
+        out = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+        wsb = ctypes.c_int64()
+        _lib.call("dwm_dense_fp8_workspace_size", m, k, n, ctypes.byref(wsb))
+        ws = torch.empty(max(1, wsb.value), dtype=torch.uint8, device=dev)
+        for tag in ("w8a16", "w8a8"):
+            def launch():
+                if tag == "w8a16":
+                    rc = lib.dwm_dense_fp8_w8a16(P(x), m, k, n, P(pw.weight), P(s16), P(out), P(ws), wsb.value, st)
+                else:
+                    rc = lib.dwm_dense_fp8_w8a8(P(xq), P(sx), m, k, n, P(pw.weight), P(sw), P(out), P(ws),
+                                                wsb.value, st)
+                if rc:
+                    raise RuntimeError(lib.dwm_last_error().decode())
+
+            if lib.dwm_dense_steps_set(None, 0):
+                raise RuntimeError(lib.dwm_last_error().decode())
+            t_end = time.time() + 0.2
+            done = 0
+            while done < 100 or time.time() < t_end:
+                for _ in range(20):
+                    launch()
+                done += 20
+                torch.cuda.synchronize()
+            plan = _lib.DensePlan()
+            if lib.dwm_dense_fp8_last_plan(ctypes.byref(plan)):
+                raise RuntimeError(lib.dwm_last_error().decode())
+            waves = 16 * 4096
+            buf = torch.zeros(waves * DENSE_STEP_SLOTS, dtype=torch.int64, device=dev)
+            if lib.dwm_dense_steps_set(P(buf), waves):
+                raise RuntimeError(lib.dwm_last_error().decode())
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            launch()
+            e1.record()
+            torch.cuda.synchronize()
+            lib.dwm_dense_steps_set(None, 0)
+            d = buf.view(waves, DENSE_STEP_SLOTS).cpu().numpy().astype(np.int64)
+            wave = np.arange(waves) % 16
+            live = d[:, 8] != 0
+            d, wave = d[live], wave[live]
+            nw = int(wave.max()) + 1
+            steps = d[:, 5].astype(np.float64)
+            clock = float(d[:, 9].sum() / ((d[:, 8] - d[:, 7]).sum() / 100.0) / 1e3)
+            pos = {}
+            for name, sel in (("first wave of a SIMD", wave < 4), ("second wave of a SIMD", wave >= 4)):
+                if not sel.any():
+                    continue
+                pos[name] = {"wait_per_step": round(float((d[sel, 1] / steps[sel]).mean()), 1),
+                             "barrier_per_step": round(float((d[sel, 2] / steps[sel]).mean()), 1),
+                             "work_per_step": round(float((d[sel, 3] / steps[sel]).mean()), 1),
+                             "prologue": round(float(d[sel, 0].mean()), 1),
+                             "epilogue": round(float(d[sel, 4].mean()), 1)}
+            res[f"dense_{tag}_M{m}"] = {
+                "plan": [plan.kernel, plan.tile_m, plan.tile_n, plan.ksplit, plan.stages],
+                "event_us": round(e0.elapsed_time(e1) * 1e3, 2), "waves": int(len(d)), "waves_per_block": nw,
+                "steps_per_wave": float(np.median(steps)), "shader_clock_GHz": round(clock, 3),
+                "launch_span_us": round(float((d[:, 8].max() - d[:, 7].min()) / 100.0), 2),
+                "cycles": pos}
+            log(f"dense steps M={m} {tag}: {res[f'dense_{tag}_M{m}']}")
+    return res
 
 
 def probe_timeline(dev, names=("decode_gate_up", "decode_down", "prefill")):
@@ -857,9 +952,10 @@ def main():
     ap.add_argument("--extra", choices=["all", "none"], default="all")
     ap.add_argument("--cpu-budget", type=float, default=15.0,
                     help="seconds of CPU-baseline work (0 skips it)")
-    ap.add_argument("--probe", choices=("rows", "cus", "timeline"), default=None,
+    ap.add_argument("--probe", choices=("rows", "cus", "timeline", "dense_steps"), default=None,
                     help="profiling aid: the grouped matmul on synthetic equal experts (rows per expert, or all "
-                         "CUs busy), or the per-block timeline of the bf16 gmm on the three workloads (the "
+                         "CUs busy), the per-block timeline of the bf16 gmm on the three workloads, or the dense "
+                         "FP8 kernel's per-wave step accounting at M = 128 and 1024 (the last two from the "
                          "library's timeline build); prints {\"probe\": kind, ...}; not the benchmark line")
     ap.add_argument("--calib-copy", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy (byte-counter calibration)")
@@ -879,6 +975,9 @@ def main():
     dev = torch.device("cuda:0")
     if args.probe == "timeline":
         print(json.dumps({"probe": "timeline", "workloads": probe_timeline(dev)}), flush=True)
+        return
+    if args.probe == "dense_steps":
+        print(json.dumps({"probe": "dense_steps", "cases": probe_dense_steps(dev)}), flush=True)
         return
     if args.probe:
         print(json.dumps({"probe": args.probe, "us": probe_equal_experts(dev, args.probe)}), flush=True)

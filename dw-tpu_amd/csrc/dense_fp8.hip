@@ -434,12 +434,32 @@ struct DenseMfmaCfg {
 
 typedef __attribute__((ext_vector_type(8))) int i32x8_t;
 
+// Per-wave step accounting of dense_fp8_mfma_kernel, compiled into the
+// library's timeline build only (-DDWTPU_TIMELINE, libdwtpu_moe_timeline.so;
+// the product library has no trace of it).  Every wave sums its shader
+// cycles (s_memtime) by phase and lane 0 stores kDsSlots words for wave w of
+// block b (linear block index) at (16 b + w) * kDsSlots: 0 prologue (entry to
+// the first wait), 1 waits for data, 2 barriers, 3 work between barriers,
+// 4 epilogue (loop end to its stores complete), 5 steps, 6 HW_ID | XCC_ID << 32,
+// 7 and 8 s_memrealtime (100 MHz) at entry and exit, 9 s_memtime from entry
+// to exit.
+constexpr int kDsSlots = 10;
+#ifdef DWTPU_TIMELINE
+static __device__ uint64_t *g_dense_steps;
+static __device__ int64_t g_dense_steps_waves;
+#define DWM_DS(...) __VA_ARGS__
+#else
+#define DWM_DS(...)
+#endif
+
 template <class C, bool A8, int NS, bool PF = false>
 __global__ __launch_bounds__(C::THREADS) void dense_fp8_mfma_kernel(
     const void *__restrict__ xin, const float *__restrict__ sx, int64_t M, int K, int N,
     const uint8_t *__restrict__ wpk, const float *__restrict__ sw, int sw_ld, int ksplit, uint16_t *__restrict__ out,
     float *__restrict__ partial) {
   __shared__ __attribute__((aligned(1024))) uint8_t s_lds[NS * C::STAGE + C::SX_BYTES];
+  DWM_DS(const uint64_t ds_rt0 = __builtin_amdgcn_s_memrealtime(); const uint64_t ds_t0 = __builtin_amdgcn_s_memtime();
+         uint64_t ds_prev = ds_t0, ds_pro = 0, ds_wait = 0, ds_bar = 0, ds_work = 0; int ds_n = 0;)
   // The wave index is made wave-uniform, so that every load address below
   // is a scalar base plus a per-lane 32-bit offset (no per-step vector
   // address arithmetic) and the LDS destinations are scalar.
@@ -657,10 +677,15 @@ __global__ __launch_bounds__(C::THREADS) void dense_fp8_mfma_kernel(
 #pragma unroll
     for (int hs = 0; hs < TS; ++hs) {
       const int cur = A8 ? cur_rt : (rep * TS + hs) % NS;
+      DWM_DS(const uint64_t ds_ta = __builtin_amdgcn_s_memtime();)
       __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(PENDING));
+      DWM_DS(const uint64_t ds_tb = __builtin_amdgcn_s_memtime();)
       asm volatile("" ::: "memory");
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
+      DWM_DS(const uint64_t ds_tc = __builtin_amdgcn_s_memtime();
+             if (ds_n == 0) ds_pro = ds_ta - ds_prev; else ds_work += ds_ta - ds_prev;
+             ds_wait += ds_tb - ds_ta; ds_bar += ds_tc - ds_tb; ds_prev = ds_tc; ++ds_n;)
       // Every wave is done with step t + hs - 1: refill its stage.
       if constexpr (A8) {
         if (t % C::SX_KB == 0 && t + C::SX_KB < T) issue_sx(t / C::SX_KB + 1);
@@ -753,6 +778,7 @@ __global__ __launch_bounds__(C::THREADS) void dense_fp8_mfma_kernel(
     }
   }
   }
+  DWM_DS(const uint64_t ds_te = __builtin_amdgcn_s_memtime(); ds_work += ds_te - ds_prev;)
   __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
   // Epilogue: the 32x32 layout (register r of lane (c32, h) is row
   // 8 (r / 4) + 4 h + r % 4, column c32).
@@ -772,6 +798,28 @@ __global__ __launch_bounds__(C::THREADS) void dense_fp8_mfma_kernel(
       }
     }
   }
+#ifdef DWTPU_TIMELINE
+  __builtin_amdgcn_s_waitcnt(0);
+  {
+    const uint64_t ds_end = __builtin_amdgcn_s_memtime(), ds_rt1 = __builtin_amdgcn_s_memrealtime();
+    const int64_t blk = blockIdx.x + (int64_t)gridDim.x * (blockIdx.y + (int64_t)gridDim.y * blockIdx.z);
+    const int64_t slot = blk * 16 + wave;
+    if (lane == 0 && g_dense_steps && slot < g_dense_steps_waves) {
+      uint64_t *const p = g_dense_steps + slot * kDsSlots;
+      p[0] = ds_pro;
+      p[1] = ds_wait;
+      p[2] = ds_bar;
+      p[3] = ds_work;
+      p[4] = ds_end - ds_te;
+      p[5] = (uint64_t)ds_n;
+      p[6] = (uint32_t)__builtin_amdgcn_s_getreg(4 | (31 << 11)) |
+             ((uint64_t)(uint32_t)__builtin_amdgcn_s_getreg(20 | (31 << 11)) << 32);
+      p[7] = ds_rt0;
+      p[8] = ds_rt1;
+      p[9] = ds_end - ds_t0;
+    }
+  }
+#endif
 }
 
 // out = bf16(sum_{ks} partial[ks]) in split order.  Each thread issues the
@@ -1162,3 +1210,17 @@ extern "C" int dwm_dense_fp8_w8a16_pre(const uint16_t *x, int64_t M, int64_t K, 
   if (!partial) return DWM_OK;
   return launch_reduce(partial, ks, M * N, out, st);
 }
+
+#ifdef DWTPU_TIMELINE
+// Timeline build only: record the MFMA tile kernel's per-wave step accounting
+// for waves 0 .. waves - 1 (16 per block) into buf (waves x kDsSlots words,
+// zeroed by the caller), or stop (NULL).
+extern "C" int dwm_dense_steps_set(uint64_t *buf, int64_t waves) {
+  clear_error();
+  DWM_CHECK_ARG(waves >= 0 && (buf || waves == 0), "dense_steps_set: bad buffer");
+  if (hipMemcpyToSymbol(HIP_SYMBOL(dwm::g_dense_steps), &buf, sizeof(buf)) != hipSuccess ||
+      hipMemcpyToSymbol(HIP_SYMBOL(dwm::g_dense_steps_waves), &waves, sizeof(waves)) != hipSuccess)
+    return launch_status("dense_steps_set");
+  return DWM_OK;
+}
+#endif

@@ -339,3 +339,61 @@ def test_pre_mode_power_of_two_scales_equal_native_on_its_plan(dev):
         t = plan_to_tile(last_plan(), K)
         nat = bf16_bits(matmul(x, w, s, mode=t.mode, tm=t.tm, tk=t.tk, tn=t.tn, stages=t.stages))
         assert np.array_equal(pre, nat), (M, K, N, t)
+
+
+@pytest.mark.parametrize("w8a8", [False, True])
+def test_dense_timeline_build_same_bits(dev, w8a8):
+    """The timeline build (libdwtpu_moe_timeline.so, what bench.py --probe
+    dense_steps loads) runs the dense MFMA kernel with per-wave cycle sums
+    compiled in: the same output bits as the library (8 K runs, split-K
+    reduce included), one record per wave of every block, each wave's step
+    count that of its K run (W8A16 two 64-deep steps per 128-deep K block,
+    W8A8 one), and its phases within its own entry-to-exit cycles."""
+    import ctypes
+    import os
+    from dw_tpu_amd import _lib
+    from dw_tpu_amd.dense_fp8 import last_plan, matmul, matmul_w8a8, prepack_fp8
+    from dw_tpu_amd.dense_fp8_tiles import DenseTile
+    from dw_tpu_amd.workloads import make_dense_workload
+    tl = ctypes.CDLL(os.path.join(os.path.dirname(_lib.LIB_PATH), "libdwtpu_moe_timeline.so"))
+    for n in ("dwm_dense_fp8_w8a16_plan", "dwm_dense_fp8_w8a8_plan"):
+        getattr(tl, n).argtypes = _lib.SIGNATURES[n]
+    tl.dwm_dense_steps_set.argtypes = [ctypes.c_void_p, ctypes.c_int64]
+    M, K, N = 128, 2048, 1024  # 8 column tiles x 8 K runs of 2 K blocks: 64 blocks
+    wl = make_dense_workload(M, K, N, seed=85)
+    pw = prepack_fp8(torch.from_numpy(wl.wq).to(dev))
+    x = bf16_tensor(wl.x_bits, dev)
+    xq, sx, sw = (torch.from_numpy(v).to(dev) for v in (wl.xq, wl.sx, wl.sw))
+    s16 = torch.from_numpy(wl.s_w8a16.reshape(K // 128, N)).to(dev)
+    plan = _lib.DensePlan(2, 128, 128, 8, 4 if w8a8 else 3)
+    if w8a8:
+        y = matmul_w8a8(xq, sx, pw, sw, tile=DenseTile("native", 128, 256, 128, 4))
+    else:
+        y = matmul(x, pw, torch.from_numpy(wl.s_w8a16).to(dev), mode="native", tm=128, tk=256, tn=128, stages=3)
+    torch.cuda.synchronize()
+    assert last_plan().astuple() == plan.astuple()
+    out = torch.empty_like(y)
+    ws = torch.empty(8 * M * N * 4, dtype=torch.uint8, device=dev)
+    waves, slots = 16 * 64, 10
+    buf = torch.zeros(waves * slots, dtype=torch.int64, device=dev)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    assert tl.dwm_dense_steps_set(P(buf), waves) == 0
+    if w8a8:
+        rc = tl.dwm_dense_fp8_w8a8_plan(P(xq), P(sx), M, K, N, P(pw.weight), P(sw), P(out), ctypes.byref(plan),
+                                        P(ws), ws.numel(), _lib.stream_handle(dev))
+    else:
+        rc = tl.dwm_dense_fp8_w8a16_plan(P(x), M, K, N, P(pw.weight), P(s16), P(out), ctypes.byref(plan), P(ws),
+                                         ws.numel(), _lib.stream_handle(dev))
+    torch.cuda.synchronize()
+    assert tl.dwm_dense_steps_set(None, 0) == 0
+    assert rc == 0
+    assert torch.equal(out.view(torch.int16), y.view(torch.int16))
+    d = buf.view(waves, slots).cpu().numpy().astype(np.int64)
+    per_block = 4 if w8a8 else 8
+    live = d[:, 8] != 0
+    assert live.sum() == 64 * per_block
+    assert np.all((np.arange(waves) % 16)[live] < per_block)
+    d = d[live]
+    assert np.all(d[:, 5] == (2 if w8a8 else 4))
+    assert np.all(d[:, 0] + d[:, 1] + d[:, 2] + d[:, 3] + d[:, 4] <= d[:, 9])
+    assert np.all(d[:, 7] < d[:, 8])
