@@ -551,6 +551,97 @@ def prep_dense(dev, steps, warmup, ms_list=(1, 16, 128, 1024, 4096)):
 
 TIMELINE_SLOTS = 24  # words per block record of the timeline build (kTlSlots in csrc/gmm_fp4.hip)
 DENSE_STEP_SLOTS = 10  # words per wave record of the dense step accounting (kDsSlots in csrc/dense_fp8.hip)
+GMM_STEP_SLOTS = 10  # words per wave record of the gmm step accounting (kGsSlots in csrc/gmm_fp4.hip)
+
+
+def probe_gmm_steps(dev, names=("decode_gate_up", "decode_down", "prefill")):
+    """Profiling aid (``--probe gmm_steps``): where a 64-deep K step of the
+    bf16 gmm goes, from the library's timeline build (the same kernels with
+    per-wave s_memtime sums compiled in), one launch per workload after at
+    least 0.2 s of warmup launches.  Every wave of a tile block sums its shader
+    cycles waiting before each barrier (producers: vmcnt for their loads;
+    consumers: their LDS reads), at the barrier, and working between barriers.
+    Reported per K step (the sums over the T + 1 barriers, the epilogue's
+    included, over the T steps) and per tile shape (16-row blocks, narrow tiles apart)
+    for the older and the younger consumer of each SIMD (waves 0-3 and 4-7)
+    and the producers (waves 8-11), with the role's prologue (start to the
+    first wait) and end (last barrier to stores issued), and the shader clock
+    (s_memtime against s_memrealtime)."""
+    import numpy as np
+    import torch
+    from dw_tpu_amd import _lib, fp4_weight_to_codes
+    from dw_tpu_amd.workloads import make_gmm_workload
+    lib = ctypes.CDLL(os.path.join(os.path.dirname(_lib.LIB_PATH), "libdwtpu_moe_timeline.so"))
+    for n, a in _lib.SIGNATURES.items():
+        f = getattr(lib, n)
+        f.argtypes = a
+        f.restype = _lib._RESTYPES.get(n, ctypes.c_int)
+    lib.dwm_gmm_steps_set.argtypes = [ctypes.c_void_p, ctypes.c_int64]
+    st = _lib.stream_handle(dev)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    out_all = {}
+    for name in names:
+        wl = make_gmm_workload(name)
+        pw = fp4_weight_to_codes(torch.from_numpy(wl.rhs_e2m1).to(dev), torch.from_numpy(wl.scale_codes).to(dev))
+        lhs = torch.from_numpy(wl.lhs_bits.view(np.int16)).view(torch.bfloat16).to(dev)
+        gs = torch.from_numpy(wl.group_sizes).to(dev)
+        out = torch.empty((wl.M, wl.N), dtype=torch.bfloat16, device=dev)
+        waves = 16 * 16384
+        buf = torch.zeros(waves * GMM_STEP_SLOTS, dtype=torch.int64, device=dev)
+
+        def launch():
+            rc = lib.dwm_gmm_fp4(P(lhs), wl.M, wl.K, P(pw.weight), P(pw.scale), P(gs), wl.E, None, wl.E, wl.N,
+                                 P(out), _lib.BF16, 0, 0, st)
+            if rc:
+                raise RuntimeError(lib.dwm_last_error().decode())
+
+        if lib.dwm_gmm_steps_set(None, 0):
+            raise RuntimeError(lib.dwm_last_error().decode())
+        t_end = time.time() + 0.2
+        n = 0
+        while n < 30 or time.time() < t_end:
+            for _ in range(10):
+                launch()
+            n += 10
+            torch.cuda.synchronize()
+        if lib.dwm_gmm_steps_set(P(buf), waves):
+            raise RuntimeError(lib.dwm_last_error().decode())
+        launch()
+        torch.cuda.synchronize()
+        lib.dwm_gmm_steps_set(None, 0)
+        d = buf.view(waves, GMM_STEP_SLOTS).cpu().numpy().astype(np.int64)
+        wave = np.arange(waves) % 16
+        live = d[:, 8] != 0
+        d, wave = d[live], wave[live]
+        role, rows, narrow = d[:, 6] & 0xFF, (d[:, 6] >> 8) & 0xFFFF, (d[:, 6] >> 24) & 1
+        # T + 1 barriers (the K steps' and the epilogue's) around T steps of work.
+        steps = np.maximum(d[:, 5] - 1, 1).astype(np.float64)
+        clock = float(d[:, 9].sum() / ((d[:, 8] - d[:, 7]).sum() / 100.0) / 1e3)
+        shapes = {}
+        for nh in sorted(set(((rows + 15) // 16).tolist())):
+            for nw in (0, 1):
+                tile = ((rows + 15) // 16 == nh) & (narrow == nw)
+                if not tile.any():
+                    continue
+                roles = {}
+                for rname, sel in (("older consumer", (role == 2) & (wave < 4)),
+                                   ("younger consumer", (role == 2) & (wave >= 4)),
+                                   ("producer", role == 1)):
+                    m = tile & sel
+                    if not m.any():
+                        continue
+                    roles[rname] = {"waves": int(m.sum()),
+                                    "wait_per_step": round(float((d[m, 1] / steps[m]).mean()), 1),
+                                    "barrier_per_step": round(float((d[m, 2] / steps[m]).mean()), 1),
+                                    "work_per_step": round(float((d[m, 3] / steps[m]).mean()), 1),
+                                    "prologue": round(float(d[m, 0].mean()), 1),
+                                    "end": round(float(d[m, 4].mean()), 1)}
+                shapes[f"{nh} blocks{' narrow' if nw else ''}"] = {
+                    "tiles": int((tile & (role == 1) & (wave == 8)).sum()),
+                    "barriers": int(np.median(d[tile, 5])), "roles": roles}
+        out_all[name] = {"shader_clock_GHz": round(clock, 3), "shapes": shapes}
+        log(f"gmm steps {name}: {out_all[name]}")
+    return out_all
 
 
 def probe_dense_steps(dev, ms_list=(128, 1024)):
@@ -952,11 +1043,12 @@ def main():
     ap.add_argument("--extra", choices=["all", "none"], default="all")
     ap.add_argument("--cpu-budget", type=float, default=15.0,
                     help="seconds of CPU-baseline work (0 skips it)")
-    ap.add_argument("--probe", choices=("rows", "cus", "timeline", "dense_steps"), default=None,
+    ap.add_argument("--probe", choices=("rows", "cus", "timeline", "gmm_steps", "dense_steps"), default=None,
                     help="profiling aid: the grouped matmul on synthetic equal experts (rows per expert, or all "
-                         "CUs busy), the per-block timeline of the bf16 gmm on the three workloads, or the dense "
-                         "FP8 kernel's per-wave step accounting at M = 128 and 1024 (the last two from the "
-                         "library's timeline build); prints {\"probe\": kind, ...}; not the benchmark line")
+                         "CUs busy), the per-block timeline or the per-wave step accounting of the bf16 gmm on "
+                         "the three workloads, or the dense FP8 kernel's per-wave step accounting at M = 128 and "
+                         "1024 (the last three from the library's timeline build); prints {\"probe\": kind, "
+                         "...}; not the benchmark line")
     ap.add_argument("--calib-copy", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy (byte-counter calibration)")
     ap.add_argument("--only", choices=ONLY_CHOICES, default=None,
@@ -975,6 +1067,9 @@ def main():
     dev = torch.device("cuda:0")
     if args.probe == "timeline":
         print(json.dumps({"probe": "timeline", "workloads": probe_timeline(dev)}), flush=True)
+        return
+    if args.probe == "gmm_steps":
+        print(json.dumps({"probe": "gmm_steps", "workloads": probe_gmm_steps(dev)}), flush=True)
         return
     if args.probe == "dense_steps":
         print(json.dumps({"probe": "dense_steps", "cases": probe_dense_steps(dev)}), flush=True)

@@ -443,7 +443,7 @@ typedef __attribute__((ext_vector_type(8))) int i32x8_t;
 // 4 epilogue (loop end to its stores complete), 5 steps, 6 HW_ID | XCC_ID << 32,
 // 7 and 8 s_memrealtime (100 MHz) at entry and exit, 9 s_memtime from entry
 // to exit.
-constexpr int kDsSlots = 10;
+[[maybe_unused]] constexpr int kDsSlots = 10;
 #ifdef DWTPU_TIMELINE
 static __device__ uint64_t *g_dense_steps;
 static __device__ int64_t g_dense_steps_waves;

@@ -39,7 +39,7 @@ namespace dwm {
 // 2 tile found; 3 rows | narrow << 16 (0: no tile); 4, 5, 6 consumer wave
 // 0's first barrier passed, K loop done, stores issued; 7 and 20 wave 0's
 // s_memtime (shader clock) at entry and exit; 8 + w wave w's exit.
-constexpr int kTlSlots = 24;
+[[maybe_unused]] constexpr int kTlSlots = 24;
 #ifdef DWTPU_TIMELINE
 static __device__ uint64_t *g_timeline;
 static __device__ int64_t g_timeline_blocks;
@@ -50,6 +50,63 @@ static __device__ int64_t g_timeline_blocks;
   } while (0)
 #else
 #define DWM_TL(slot, v) ((void)0)
+#endif
+
+// Per-wave step accounting, also in the timeline build only: every wave of a
+// tile block sums its shader cycles (s_memtime) by phase into kGsSlots words
+// at (blockIdx.x * 16 + wave) * kGsSlots of a second buffer: 0 from its
+// role's start to its first wait, 1 waits before barriers (producers: vmcnt
+// for their loads; consumers: their LDS reads), 2 barriers, 3 work between
+// barriers, 4 from the last barrier to the role's end (consumers: epilogue
+// stores issued), 5 barriers passed, 6 role (1 producer, 2 consumer, 3 idle
+// consumer of a narrow tile) | rows << 8 | narrow << 24, 7 and 8
+// s_memrealtime at the role's start and end, 9 s_memtime from start to end.
+[[maybe_unused]] constexpr int kGsSlots = 10;
+#ifdef DWTPU_TIMELINE
+static __device__ uint64_t *g_gmm_steps;
+static __device__ int64_t g_gmm_steps_waves;
+struct GsAcct {
+  uint64_t rt0, t0, prev, pro, wait, bar, work;
+  int n;
+  __device__ void start() {
+    rt0 = __builtin_amdgcn_s_memrealtime();
+    t0 = prev = __builtin_amdgcn_s_memtime();
+    pro = wait = bar = work = 0;
+    n = 0;
+  }
+  // ta before a wait, tb after it, tc after the barrier that follows.
+  __device__ void step(uint64_t ta, uint64_t tb, uint64_t tc) {
+    if (n == 0) pro = ta - prev;
+    else work += ta - prev;
+    wait += tb - ta;
+    bar += tc - tb;
+    prev = tc;
+    ++n;
+  }
+  __device__ void finish() {
+    const uint64_t end = __builtin_amdgcn_s_memtime(), rt1 = __builtin_amdgcn_s_memrealtime();
+    const int64_t slot = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 6);
+    if ((threadIdx.x & 63) == 0 && g_gmm_steps && slot < g_gmm_steps_waves) {
+      uint64_t *const p = g_gmm_steps + slot * kGsSlots;
+      p[0] = pro;
+      p[1] = wait;
+      p[2] = bar;
+      p[3] = work;
+      p[4] = end - prev;
+      p[5] = (uint64_t)n;
+      p[7] = rt0;
+      p[8] = rt1;
+      p[9] = end - t0;
+    }
+  }
+};
+__device__ __forceinline__ void gs_role(uint64_t info) {
+  const int64_t slot = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 6);
+  if ((threadIdx.x & 63) == 0 && g_gmm_steps && slot < g_gmm_steps_waves) g_gmm_steps[slot * kGsSlots + 6] = info;
+}
+#define DWM_GS(...) __VA_ARGS__
+#else
+#define DWM_GS(...)
 #endif
 
 // lhs tile rows hold 8 16-byte chunks; chunk c of row r sits at physical
@@ -120,6 +177,7 @@ __device__ __forceinline__ void ws_producer(const uint16_t *__restrict__ lhs, co
   constexpr int PENDING = LOADS * (NS - 1 - C::AHEAD);
   static_assert(PENDING < 64, "vmcnt range");
   const int lane = threadIdx.x & 63;
+  DWM_GS(GsAcct gs; gs.start();)
   // Row groups pw + NP i, i >= NA, lie past the tile's rows: zero them.
 #pragma unroll
   for (int i = NA; i < C::A_LOADS; ++i)
@@ -172,19 +230,25 @@ __device__ __forceinline__ void ws_producer(const uint16_t *__restrict__ lhs, co
   for (int t = 0; t < T; ++t) {
     // Steps t .. t + AHEAD - 1 have landed once at most the loads of the
     // later steps are pending.
+    DWM_GS(const uint64_t gs_a = __builtin_amdgcn_s_memtime();)
     __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(PENDING));
+    DWM_GS(const uint64_t gs_b = __builtin_amdgcn_s_memtime();)
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
+    DWM_GS(gs.step(gs_a, gs_b, __builtin_amdgcn_s_memtime());)
     // The consumers are done with step t - 1: refill its stage with step
     // t + NS - 1 (clamped to the last step, so every step issues the same loads).
     issue(refill, min(t + NS - 1, T - 1));
     refill = refill == NS - 1 ? 0 : refill + 1;
   }
   // Every load has landed before the stages are reused for the epilogue.
+  DWM_GS(const uint64_t gs_a = __builtin_amdgcn_s_memtime();)
   __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
+  DWM_GS(const uint64_t gs_b = __builtin_amdgcn_s_memtime();)
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_barrier();
+  DWM_GS(gs.step(gs_a, gs_b, __builtin_amdgcn_s_memtime()); gs.finish();)
 }
 
 // A consumer wave runs its 64 columns for NH 16-row blocks of the tile with
@@ -209,6 +273,7 @@ __device__ __forceinline__ void ws_consumer(int T, uint8_t *s_lds, int cw, int64
   constexpr int H0 = NH > 3 ? 3 : NH;     // blocks of row group 0 (row group 1: NH - H0)
   static_assert(C::JWAVE == 2 && NH >= 1 && NH <= 6, "64 columns and 16 .. 96 rows per consumer");
   const int lane = threadIdx.x & 63, q = lane >> 4;
+  DWM_GS(GsAcct gs; gs.start();)
   f32x4_t acc[NH][4];
 #pragma unroll
   for (int hb = 0; hb < NH; ++hb)
@@ -316,9 +381,12 @@ __device__ __forceinline__ void ws_consumer(int T, uint8_t *s_lds, int cw, int64
     const int t = t0 + cur;
     if (t >= T) break;
     asm volatile("" ::: "memory");
+    DWM_GS(const uint64_t gs_a = __builtin_amdgcn_s_memtime();)
     __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
+    DWM_GS(const uint64_t gs_b = __builtin_amdgcn_s_memtime();)
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
+    DWM_GS(gs.step(gs_a, gs_b, __builtin_amdgcn_s_memtime());)
     const uint8_t *const st = s_lds + cur * C::STAGE;
     const int nxt = cur == NS - 1 ? 0 : cur + 1;
     // Step t + 1 was published at this barrier (stale contents in the last step, never used).
@@ -350,9 +418,12 @@ __device__ __forceinline__ void ws_consumer(int T, uint8_t *s_lds, int cw, int64
     const int t = t0 + cur;
     if (t >= T) break;
     asm volatile("" ::: "memory");
+    DWM_GS(const uint64_t gs_a = __builtin_amdgcn_s_memtime();)
     __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
+    DWM_GS(const uint64_t gs_b = __builtin_amdgcn_s_memtime();)
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
+    DWM_GS(gs.step(gs_a, gs_b, __builtin_amdgcn_s_memtime());)
     const uint8_t *const st = s_lds + cur * C::STAGE;
     const int nxt = cur == NS - 1 ? 0 : cur + 1;
     // Step t + 1 was published at this barrier and its stage is not refilled
@@ -410,22 +481,30 @@ __device__ __forceinline__ void ws_consumer(int T, uint8_t *s_lds, int cw, int64
   // writes whole 8-column runs of a row.
   if (cw == 0) DWM_TL(5, __builtin_amdgcn_s_memrealtime());
   asm volatile("" ::: "memory");
+  DWM_GS(const uint64_t gs_a = __builtin_amdgcn_s_memtime();)
   __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
+  DWM_GS(const uint64_t gs_b = __builtin_amdgcn_s_memtime();)
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
+  DWM_GS(gs.step(gs_a, gs_b, __builtin_amdgcn_s_memtime());)
   store_halves<NH, ACT, C::EP_STRIDE>(acc, (float *)(s_lds + cw * 32 * C::EP_STRIDE * 4), row0, rows, col0, N, out,
                                       out_f32, bias, ep.bias_bf16, ep.act);
   if (cw == 0) DWM_TL(6, __builtin_amdgcn_s_memrealtime());
+  DWM_GS(gs.finish();)
 }
 
 // A consumer wave with no columns in a narrow tile: it only keeps the
 // barrier count (T + 1) of the others.
 __device__ __forceinline__ void ws_idle_consumer(int T) {
+  DWM_GS(GsAcct gs; gs.start();)
   for (int t = 0; t <= T; ++t) {
     asm volatile("" ::: "memory");
+    DWM_GS(const uint64_t gs_a = __builtin_amdgcn_s_memtime();)
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
+    DWM_GS(gs.step(gs_a, gs_a, __builtin_amdgcn_s_memtime());)
   }
+  DWM_GS(gs.finish();)
 }
 
 // Producer dispatch on the number of lhs row groups that hold rows.
@@ -504,6 +583,7 @@ __global__ __launch_bounds__(C::THREADS) void gmm_fp4_ws_kernel(
       ws_produce<C, C::G_LOADS / 2>(na, lhs, row_idx, lhs_rows, row0, rows, K, T, KB, wexp, sexp, g0, G, s_lds, pw);
     else
       ws_produce<C, C::G_LOADS>(na, lhs, row_idx, lhs_rows, row0, rows, K, T, KB, wexp, sexp, g0, G, s_lds, pw);
+    DWM_GS(gs_role(1u | (uint64_t)rows << 8 | (uint64_t)narrow << 24);)
     tl_exit();
     return;
   }
@@ -511,6 +591,7 @@ __global__ __launch_bounds__(C::THREADS) void gmm_fp4_ws_kernel(
   // whatever its row-block count.
   if (narrow && wave >= C::GT / 2) {
     ws_idle_consumer(T);
+    DWM_GS(gs_role(3u | (uint64_t)rows << 8 | (uint64_t)narrow << 24);)
     tl_exit();
     return;
   }
@@ -525,6 +606,7 @@ __global__ __launch_bounds__(C::THREADS) void gmm_fp4_ws_kernel(
     case 5: ws_consumer<C, 5, ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32, bias, ep); break;
     default: ws_consumer<C, 6, ACT>(T, s_lds, wave, row0, rows, col0, N, out, out_f32, bias, ep); break;
   }
+  DWM_GS(gs_role(2u | (uint64_t)rows << 8 | (uint64_t)narrow << 24);)
   tl_exit();
 }
 
@@ -702,6 +784,18 @@ static int gmm_run(const dwm_gmm_lhs &L, int64_t M, int64_t K, const uint8_t *we
 using namespace dwm;
 
 #ifdef DWTPU_TIMELINE
+// Timeline build only: record the bf16 gmm kernel's per-wave step accounting
+// for waves 0 .. waves - 1 (16 per block) into buf (waves x kGsSlots words,
+// zeroed by the caller), or stop (NULL).
+extern "C" int dwm_gmm_steps_set(uint64_t *buf, int64_t waves) {
+  clear_error();
+  DWM_CHECK_ARG(waves >= 0 && (buf || waves == 0), "gmm_steps_set: bad buffer");
+  if (hipMemcpyToSymbol(HIP_SYMBOL(dwm::g_gmm_steps), &buf, sizeof(buf)) != hipSuccess ||
+      hipMemcpyToSymbol(HIP_SYMBOL(dwm::g_gmm_steps_waves), &waves, sizeof(waves)) != hipSuccess)
+    return launch_status("gmm_steps_set");
+  return DWM_OK;
+}
+
 // Timeline build only: record the bf16 gmm kernel's blocks 0 .. blocks - 1
 // into buf (blocks x kTlSlots words, zeroed by the caller), or stop (NULL).
 extern "C" int dwm_timeline_set(uint64_t *buf, int64_t blocks) {

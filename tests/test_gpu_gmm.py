@@ -377,6 +377,51 @@ def test_gmm_timeline_build_same_bits(dev):
     assert np.all(t[:, 6] <= last)
 
 
+def test_gmm_step_accounting_build_same_bits(dev):
+    """The timeline build's per-wave step accounting (what bench.py --probe
+    gmm_steps reads) leaves the output bits unchanged; every wave of every
+    tile block leaves one record; every role passes the T + 1 barriers of the
+    block (T = K / 64 steps and the epilogue's); a wide tile holds 8
+    consumers and 4 producers, a narrow one 4 consumers, 4 idle consumers and
+    4 producers; and each wave's phases add up to its cycles."""
+    import ctypes
+    import os
+    from dw_tpu_amd import _lib, fp4_weight_to_codes, gmm_v2
+    from dw_tpu_amd.workloads import make_gmm_workload
+    tl = ctypes.CDLL(os.path.join(os.path.dirname(_lib.LIB_PATH), "libdwtpu_moe_timeline.so"))
+    tl.dwm_gmm_fp4.argtypes = _lib.SIGNATURES["dwm_gmm_fp4"]
+    tl.dwm_gmm_steps_set.argtypes = [ctypes.c_void_p, ctypes.c_int64]
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    for name, tiles in (("decode_down", 896), ("decode_gate_up", 256)):
+        wl = make_gmm_workload(name)
+        pw = fp4_weight_to_codes(torch.from_numpy(wl.rhs_e2m1).to(dev), torch.from_numpy(wl.scale_codes).to(dev))
+        lhs = bf16_tensor(wl.lhs_bits, dev)
+        gs = torch.from_numpy(wl.group_sizes).to(dev)
+        y = gmm_v2(lhs, pw, gs)
+        out = torch.empty_like(y)
+        waves, slots = 16 * 4096, 10
+        buf = torch.zeros(waves * slots, dtype=torch.int64, device=dev)
+        assert tl.dwm_gmm_steps_set(P(buf), waves) == 0
+        rc = tl.dwm_gmm_fp4(P(lhs), wl.M, wl.K, P(pw.weight), P(pw.scale), P(gs), wl.E, None, wl.E, wl.N, P(out),
+                            _lib.BF16, 0, 0, _lib.stream_handle(dev))
+        torch.cuda.synchronize()
+        assert tl.dwm_gmm_steps_set(None, 0) == 0
+        assert rc == 0
+        assert torch.equal(out.view(torch.int16), y.view(torch.int16)), name
+        d = buf.view(waves, slots).cpu().numpy().astype(np.int64)
+        live = d[:, 8] != 0
+        assert live.sum() == 12 * tiles, name
+        blk = np.arange(waves)[live] // 16
+        d = d[live]
+        assert np.all(d[:, 5] == wl.K // 64 + 1), name
+        role, narrow = d[:, 6] & 0xFF, (d[:, 6] >> 24) & 1
+        for b in np.unique(blk):
+            r = np.sort(role[blk == b])
+            want = [1] * 4 + ([2] * 4 + [3] * 4 if narrow[blk == b][0] else [2] * 8)
+            assert sorted(r.tolist()) == sorted(want), (name, b, r)
+        assert np.all(d[:, 0] + d[:, 1] + d[:, 2] + d[:, 3] + d[:, 4] == d[:, 9]), name
+
+
 def test_gmm_full_size_row_permutation_and_group_independence(dev, rng):
     """decode_gate_up at full size: permuting rows inside each expert group
     permutes the output rows bit for bit (each row's result depends on its
